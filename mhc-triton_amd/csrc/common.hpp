@@ -1,0 +1,198 @@
+// Shared device helpers for the gfx950 mHC kernels.
+//
+// Bulk tensors (H, branch_input, H_residual, branch_output and their
+// gradients) are stored as fp32, bf16 or fp16 and always computed in fp32.
+// Every streaming kernel moves 16 bytes per lane per access
+// (global_load_dwordx4 / global_store_dwordx4): 4 fp32 or 8 bf16/fp16
+// elements.  Small per-batch weights (H_pre, H_post, H_res: 24 floats) are
+// fp32 and are read through the scalar cache because the batch index is
+// uniform across a workgroup (blockIdx.y).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "../../include/mhc_abi.h"
+
+namespace mhc {
+
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x2 __attribute__((ext_vector_type(2)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x8 __attribute__((ext_vector_type(8)));
+
+constexpr int kThreads = 256;  // 4 waves of 64 lanes
+
+// Elements per 16-byte access.
+template <typename T> struct Vec { static constexpr int N = 16 / sizeof(T); };
+
+// ---------------------------------------------------------------------------
+// Scalar conversions.  bf16 <- f32 and f16 <- f32 round to nearest even, the
+// same rounding torch uses for .to(bfloat16) / .to(float16); gfx950 has
+// v_cvt_pk_bf16_f32 for the former.
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ float to_f32(float v) { return v; }
+__device__ __forceinline__ float to_f32(__bf16 v) { return (float)v; }
+__device__ __forceinline__ float to_f32(_Float16 v) { return (float)v; }
+
+template <typename T> __device__ __forceinline__ T from_f32(float v);
+template <> __device__ __forceinline__ float from_f32<float>(float v) { return v; }
+template <> __device__ __forceinline__ __bf16 from_f32<__bf16>(float v) { return (__bf16)v; }
+template <> __device__ __forceinline__ _Float16 from_f32<_Float16>(float v) { return (_Float16)v; }
+
+// ---------------------------------------------------------------------------
+// 16-byte vector load / store with conversion to / from fp32.
+// ---------------------------------------------------------------------------
+template <typename T> struct Io;
+
+template <> struct Io<float> {
+  __device__ __forceinline__ static void load(const float* p, float* f) {
+    f32x4 v = *reinterpret_cast<const f32x4*>(p);
+    f[0] = v.x; f[1] = v.y; f[2] = v.z; f[3] = v.w;
+  }
+  template <bool NT>
+  __device__ __forceinline__ static void store(float* p, const float* f) {
+    f32x4 v = {f[0], f[1], f[2], f[3]};
+    if constexpr (NT) __builtin_nontemporal_store(v, reinterpret_cast<f32x4*>(p));
+    else *reinterpret_cast<f32x4*>(p) = v;
+  }
+};
+
+template <> struct Io<__bf16> {
+  __device__ __forceinline__ static void load(const __bf16* p, float* f) {
+    u32x4 r = *reinterpret_cast<const u32x4*>(p);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      f[2 * i] = __uint_as_float(r[i] << 16);
+      f[2 * i + 1] = __uint_as_float(r[i] & 0xffff0000u);
+    }
+  }
+  template <bool NT>
+  __device__ __forceinline__ static void store(__bf16* p, const float* f) {
+    u32x4 r;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      f32x2 pair = {f[2 * i], f[2 * i + 1]};
+      r[i] = __builtin_bit_cast(uint32_t, __builtin_convertvector(pair, bf16x2));
+    }
+    if constexpr (NT) __builtin_nontemporal_store(r, reinterpret_cast<u32x4*>(p));
+    else *reinterpret_cast<u32x4*>(p) = r;
+  }
+};
+
+template <> struct Io<_Float16> {
+  __device__ __forceinline__ static void load(const _Float16* p, float* f) {
+    const f16x8 v = *reinterpret_cast<const f16x8*>(p);
+    const f32x8 w = __builtin_convertvector(v, f32x8);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) f[i] = w[i];
+  }
+  template <bool NT>
+  __device__ __forceinline__ static void store(_Float16* p, const float* f) {
+    f32x8 w;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) w[i] = f[i];
+    const f16x8 v = __builtin_convertvector(w, f16x8);
+    if constexpr (NT) __builtin_nontemporal_store(v, reinterpret_cast<f16x8*>(p));
+    else *reinterpret_cast<f16x8*>(p) = v;
+  }
+};
+
+// Load W consecutive elements when W is a multiple of the 16-byte vector
+// width of T (several 16-byte loads), or W == 1.
+template <typename T, int W>
+__device__ __forceinline__ void ld(const T* p, float* f) {
+  constexpr int N = Vec<T>::N;
+  if constexpr (W >= N) {
+#pragma unroll
+    for (int q = 0; q < W / N; ++q) Io<T>::load(p + q * N, f + q * N);
+  } else {
+#pragma unroll
+    for (int i = 0; i < W; ++i) f[i] = to_f32(p[i]);
+  }
+}
+
+template <typename T, int W, bool NT = false>
+__device__ __forceinline__ void st(T* p, const float* f) {
+  constexpr int N = Vec<T>::N;
+  if constexpr (W >= N) {
+#pragma unroll
+    for (int q = 0; q < W / N; ++q) Io<T>::template store<NT>(p + q * N, f + q * N);
+  } else {
+#pragma unroll
+    for (int i = 0; i < W; ++i) p[i] = from_f32<T>(f[i]);
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Reductions.  Lane order and tree shape are fixed, so every reduction in this
+// library is deterministic run to run (no floating-point atomics).
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
+  return v;
+}
+
+// Sums NV per-thread values across a 256-thread workgroup.  The result is
+// valid in thread 0 only (out[0..NV-1]).  `lds` must hold 4 * NV floats.
+template <int NV>
+__device__ __forceinline__ void block_sum(float (&v)[NV], float* lds) {
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+#pragma unroll
+  for (int i = 0; i < NV; ++i) v[i] = wave_sum(v[i]);
+  if (lane == 0) {
+#pragma unroll
+    for (int i = 0; i < NV; ++i) lds[wave * NV + i] = v[i];
+  }
+  __syncthreads();
+  if (threadIdx.x == 0) {
+#pragma unroll
+    for (int i = 0; i < NV; ++i) v[i] = (lds[i] + lds[NV + i]) + (lds[2 * NV + i] + lds[3 * NV + i]);
+  }
+}
+
+// Zero-fills n floats.  A kernel rather than hipMemsetAsync so that callers may
+// capture the work in a HIP graph.
+template <int = 0>
+__global__ __launch_bounds__(256) void fill_zero_kernel(float* __restrict__ p, int64_t n) {
+  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (i < n) p[i] = 0.f;
+}
+
+// ---------------------------------------------------------------------------
+// Host-side helpers shared by the entry points.
+// ---------------------------------------------------------------------------
+void set_error(const char* fmt, ...);
+int hip_status(hipError_t e, const char* where);
+int num_cus();
+
+inline int fill_zero(float* p, int64_t n, hipStream_t st) {
+  if (n <= 0) return MHC_OK;
+  fill_zero_kernel<><<<dim3((unsigned)((n + 255) / 256)), 256, 0, st>>>(p, n);
+  return hip_status(hipGetLastError(), "fill_zero launch");
+}
+
+inline bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+// Batches go on grid.y; HIP caps grid.y, so larger batches are split into
+// several launches by the entry points.
+constexpr int64_t kMaxGridY = 65535;
+
+}  // namespace mhc
+
+// Dispatch on the bulk dtype: defines `using T = ...` inside the body.
+#define MHC_DISPATCH_DTYPE(dtype, ...)                                   \
+  [&]() -> int {                                                         \
+    switch (dtype) {                                                     \
+      case MHC_DTYPE_F32: { using T = float; return __VA_ARGS__(); }     \
+      case MHC_DTYPE_BF16: { using T = __bf16; return __VA_ARGS__(); }   \
+      case MHC_DTYPE_F16: { using T = _Float16; return __VA_ARGS__(); }  \
+      default: ::mhc::set_error("unsupported dtype code %d", (int)(dtype)); \
+               return MHC_ERR_DTYPE;                                     \
+    }                                                                    \
+  }()

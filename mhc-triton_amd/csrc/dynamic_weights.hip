@@ -1,0 +1,196 @@
+// Entry points: fused_dynamic_weights forward / backward and the sequence
+// mean-pool (reference src/mhc/_kernels.py:690-752, src/mhc/ops.py:72-228,
+// src/mhc/module.py:161).
+#include "dynw_kernels.hpp"
+#include "stream_kernels.hpp"
+
+namespace mhc {
+
+int check_workspace(const char* who, const void* ws, size_t have, size_t need);
+
+constexpr int kRT = 4;  // rows per workgroup in dynw_partial_kernel
+
+struct DynPlan {
+  int64_t KC;  // K chunk per workgroup (multiple of 256)
+  int nK;      // number of chunks
+};
+
+// Aim for at most ~4096 workgroups: small R splits K finely (R = 4, K = 16384
+// -> 64 chunks of 256), large R gives each workgroup a longer K run.
+static DynPlan dyn_plan(int64_t R, int64_t K) {
+  const int64_t rtiles = (R + kRT - 1) / kRT;
+  const int64_t k256 = (K + kThreads - 1) / kThreads;
+  int64_t kpt = (rtiles * k256 + 4095) / 4096;
+  if (kpt < 1) kpt = 1;
+  if (kpt > 64) kpt = 64;
+  DynPlan p;
+  p.KC = kThreads * kpt;
+  p.nK = (int)((K + p.KC - 1) / p.KC);
+  if (p.nK < 1) p.nK = 1;
+  return p;
+}
+
+static size_t align256(size_t v) { return (v + 255) & ~(size_t)255; }
+
+}  // namespace mhc
+
+using namespace mhc;
+
+extern "C" size_t mhc_dynamic_weights_workspace_bytes(int64_t R, int64_t K) {
+  if (R <= 0) return 0;
+  const DynPlan p = dyn_plan(R, K);
+  return align256((size_t)R * p.nK * kPart * sizeof(float));
+}
+
+extern "C" int mhc_dynamic_weights_forward(const void* x, int dtype_x, const float* phi, const float* bias,
+                                           const float* alpha_pre, const float* alpha_post,
+                                           const float* alpha_res, float* H_pre, float* H_post, float* H_res,
+                                           float* aux, int64_t R, int64_t K, int iters, float eps,
+                                           void* workspace, size_t workspace_bytes, mhc_stream_t stream) {
+  if (R < 0 || K < 0 || iters < 0) {
+    set_error("dynamic_weights_forward: bad size (R=%lld K=%lld iters=%d)", (long long)R, (long long)K, iters);
+    return MHC_ERR_ARG;
+  }
+  if (R == 0) return MHC_OK;
+  if (!x || !phi || !bias || !alpha_pre || !alpha_post || !alpha_res || !H_pre || !H_post || !H_res) {
+    set_error("dynamic_weights_forward: null pointer");
+    return MHC_ERR_ARG;
+  }
+  if (int rc = check_workspace("dynamic_weights_forward", workspace, workspace_bytes,
+                               mhc_dynamic_weights_workspace_bytes(R, K)))
+    return rc;
+  hipStream_t st = (hipStream_t)stream;
+  const DynPlan p = dyn_plan(R, K);
+  float* part = (float*)workspace;
+  const bool phi_vec = aligned16(phi);
+  int rc = MHC_DISPATCH_DTYPE(dtype_x, [&] {
+    dynw_partial_kernel<T, kRT><<<dim3((unsigned)((R + kRT - 1) / kRT), p.nK), kThreads, 0, st>>>(
+        (const T*)x, phi, part, R, K, p.nK, p.KC, phi_vec);
+    return hip_status(hipGetLastError(), "dynamic_weights_forward partial launch");
+  });
+  if (rc) return rc;
+  DynParams P{bias, bias + 4, bias + 8, alpha_pre, alpha_post, alpha_res};
+  dynw_finalize_kernel<><<<dim3((unsigned)((R + 3) / 4)), kThreads, 0, st>>>(
+      part, p.nK, R, K, P, OutRow{H_pre, 4}, OutRow{H_post, 4}, OutRow{H_res, 16}, aux, iters, eps);
+  return hip_status(hipGetLastError(), "dynamic_weights_forward finalize launch");
+}
+
+extern "C" size_t mhc_dynamic_weights_backward_workspace_bytes(int64_t R, int64_t K) {
+  (void)K;
+  if (R <= 0) return 0;
+  return align256((size_t)R * kRow * sizeof(float));
+}
+
+extern "C" int mhc_dynamic_weights_backward(const void* x, int dtype_x, const float* phi, const float* bias,
+                                            const float* alpha_pre, const float* alpha_post,
+                                            const float* alpha_res, const float* aux, const float* H_pre,
+                                            const float* grad_H_pre, const float* grad_H_post,
+                                            const float* grad_H_res, float* grad_x, float* grad_phi,
+                                            float* grad_bias, float* grad_alpha, int64_t R, int64_t K, int iters,
+                                            float eps, void* workspace, size_t workspace_bytes,
+                                            mhc_stream_t stream) {
+  if (R < 0 || K < 0 || iters < 0) {
+    set_error("dynamic_weights_backward: bad size (R=%lld K=%lld iters=%d)", (long long)R, (long long)K, iters);
+    return MHC_ERR_ARG;
+  }
+  if (!phi || !bias || !alpha_pre || !alpha_post || !alpha_res) {
+    set_error("dynamic_weights_backward: null parameter pointer");
+    return MHC_ERR_ARG;
+  }
+  hipStream_t st = (hipStream_t)stream;
+  if (R == 0) {
+    // No rows: every gradient is an empty sum.
+    if (grad_phi && K > 0)
+      if (int rc = fill_zero(grad_phi, K * kOut, st)) return rc;
+    if (grad_bias)
+      if (int rc = fill_zero(grad_bias, kOut, st)) return rc;
+    if (grad_alpha)
+      if (int rc = fill_zero(grad_alpha, 3, st)) return rc;
+    return MHC_OK;
+  }
+  if (!x || !aux || !H_pre) {
+    set_error("dynamic_weights_backward: null pointer");
+    return MHC_ERR_ARG;
+  }
+  if (int rc = check_workspace("dynamic_weights_backward", workspace, workspace_bytes,
+                               mhc_dynamic_weights_backward_workspace_bytes(R, K)))
+    return rc;
+  float* rowbuf = (float*)workspace;
+  DynParams P{bias, bias + 4, bias + 8, alpha_pre, alpha_post, alpha_res};
+  dynw_bwd_rows_kernel<><<<dim3((unsigned)((R + kThreads - 1) / kThreads)), kThreads, 0, st>>>(
+      aux, P, InRow{H_pre, 4}, InRow{grad_H_pre, 4}, InRow{grad_H_post, 4}, InRow{grad_H_res, 16}, rowbuf, R, K,
+      iters, eps);
+  if (int rc = hip_status(hipGetLastError(), "dynamic_weights_backward rows launch")) return rc;
+  if (K > 0 && (grad_x || grad_phi)) {
+    const bool phi_vec = aligned16(phi);
+    int rc = MHC_DISPATCH_DTYPE(dtype_x, [&] {
+      dynw_bwd_wide_kernel<T><<<dim3((unsigned)((K + kThreads - 1) / kThreads)), kThreads, 0, st>>>(
+          (const T*)x, phi, rowbuf, grad_x, grad_phi, R, K, phi_vec);
+      return hip_status(hipGetLastError(), "dynamic_weights_backward wide launch");
+    });
+    if (rc) return rc;
+  }
+  dynw_bwd_sum_kernel<><<<1, kThreads, 0, st>>>(rowbuf, R, grad_bias, grad_alpha);
+  return hip_status(hipGetLastError(), "dynamic_weights_backward sum launch");
+}
+
+// ---------------------------------------------------------------------------
+// Mean-pool
+// ---------------------------------------------------------------------------
+namespace mhc {
+
+constexpr int kPoolUN = 8;
+
+template <typename T, int W, int LPR, bool PROJ>
+int launch_meanpool(const T* H, float* x, const float* phi, float* part, int64_t B, int64_t S, int64_t K,
+                    hipStream_t st) {
+  constexpr int CW = LPR * W;
+  const unsigned nchunk = (unsigned)((K + CW - 1) / CW);
+  const float inv_S = S > 0 ? 1.f / (float)S : __builtin_nanf("");
+  const bool phi_vec = phi ? aligned16(phi) : false;
+  return for_batch_chunks(B, [&](int64_t b0, int64_t nb) {
+    meanpool_kernel<T, W, LPR, kPoolUN, PROJ><<<dim3(nchunk, nb), kThreads, 0, st>>>(H, x, phi, part, S, K, inv_S,
+                                                                                     b0, phi_vec);
+    return hip_status(hipGetLastError(), "mean_pool launch");
+  });
+}
+
+// Lanes per row: 8 lanes x 16 bytes = 128-byte row segments per workgroup
+// column chunk, which gives B*4D/(8W) workgroups (1024 at B=4, D=4096 bf16).
+constexpr int kPoolLPR = 8;
+
+int meanpool_columns(int dtype, int64_t D) {
+  const int W = dtype == MHC_DTYPE_F32 ? 4 : 8;
+  (void)D;
+  return kPoolLPR * W;
+}
+
+int mean_pool_any(const void* H, int dtype, float* x, const float* phi, float* part, int64_t B, int64_t S,
+                  int64_t D, hipStream_t st) {
+  const int64_t K = 4 * D;
+  return MHC_DISPATCH_DTYPE(dtype, [&] {
+    constexpr int WV = Vec<T>::N;
+    const bool vec = (K % WV == 0) && aligned16(H);
+    if (phi) {
+      if (vec) return launch_meanpool<T, WV, kPoolLPR, true>((const T*)H, x, phi, part, B, S, K, st);
+      return launch_meanpool<T, 1, kPoolLPR * WV, true>((const T*)H, x, phi, part, B, S, K, st);
+    }
+    if (vec) return launch_meanpool<T, WV, kPoolLPR, false>((const T*)H, x, nullptr, nullptr, B, S, K, st);
+    return launch_meanpool<T, 1, kPoolLPR * WV, false>((const T*)H, x, nullptr, nullptr, B, S, K, st);
+  });
+}
+
+}  // namespace mhc
+
+extern "C" int mhc_mean_pool(const void* H, int dtype, float* x, int64_t B, int64_t S, int64_t D, void* workspace,
+                             size_t workspace_bytes, mhc_stream_t stream) {
+  (void)workspace;
+  (void)workspace_bytes;
+  if (int rc = check_bsd("mean_pool", B, S, D)) return rc;
+  if (B * D == 0) return MHC_OK;
+  if (!H || !x) {
+    set_error("mean_pool: null pointer");
+    return MHC_ERR_ARG;
+  }
+  return mean_pool_any(H, dtype, x, nullptr, nullptr, B, S, D, (hipStream_t)stream);
+}

@@ -1,0 +1,414 @@
+// HyperConnection layer path (reference src/mhc/module.py:141-220 composed with
+// ops.py / _kernels.py / _backward.py).
+//
+// Forward, dynamic:   meanpool<PROJ> (reads H)  -> finalize (weights w[B,24])
+//                     -> branch_input pass (reads H, writes bi)
+// Closure forward:    H_new = H_res @ H + H_post * bo (reads H, bo; writes H_new)
+// Closure backward:   d_bo, dH_post (reads dH_new, bo; writes d_bo)
+// Backward, dynamic:  pass B reductions dH_pre, dH_res (reads d_bi, dH_new, H)
+//                     -> weights backward (rows, wide: grad_x, grad_phi; sums)
+//                     -> pass C: dH = H_pre d_bi + H_res^T dH_new + grad_x / S
+//                        (reads d_bi, dH_new; writes dH)
+// Per token that is 18 D e bytes forward and 24 D e backward (e = element
+// size), against 22 + ~39 for the reference's op-by-op composition.
+// Static layers skip the mean-pool and fold pass B into pass C.
+#include "dynw_kernels.hpp"
+#include "stream_kernels.hpp"
+
+namespace mhc {
+
+int check_workspace(const char* who, const void* ws, size_t have, size_t need);
+int add_residual_backward_any(const void* dhn, int dtype_h, const void* bo, int dtype_bo, WRow post, void* dbo,
+                              float* dpost, int64_t B, int64_t S, int64_t D, float* part, hipStream_t st);
+int mean_pool_any(const void* H, int dtype, float* x, const float* phi, float* part, int64_t B, int64_t S,
+                  int64_t D, hipStream_t st);
+int meanpool_columns(int dtype, int64_t D);
+
+constexpr int kLU = 2;
+
+static size_t al(size_t v) { return (v + 255) & ~(size_t)255; }
+
+// Workspace layout shared by all layer entry points (each uses a prefix of it).
+struct LayerWs {
+  size_t pool_part;  // [B][nchunk][25]
+  size_t red_part;   // [B][nblk][20]
+  size_t dpre;       // [B][4]
+  size_t dres;       // [B][16]
+  size_t rowbuf;     // [B][52]
+  size_t gx;         // [B][4D]
+  size_t total;
+};
+
+static LayerWs layer_ws(int64_t B, int64_t S, int64_t D, int dtype) {
+  (void)S;
+  LayerWs w;
+  const int64_t cw = meanpool_columns(dtype, D);
+  const int64_t nchunk = (4 * D + cw - 1) / cw;
+  size_t o = 0;
+  w.pool_part = o; o += al((size_t)B * nchunk * kPart * sizeof(float));
+  w.red_part = o;  o += al(partial_bytes(B, 20));
+  w.dpre = o;      o += al((size_t)B * 4 * sizeof(float));
+  w.dres = o;      o += al((size_t)B * 16 * sizeof(float));
+  w.rowbuf = o;    o += al((size_t)B * kRow * sizeof(float));
+  w.gx = o;        o += al((size_t)B * 4 * D * sizeof(float));
+  w.total = o;
+  return w;
+}
+
+template <typename T, int W>
+static int launch_bi(const T* H, const float* w, T* bi, int64_t B, int64_t S, int64_t D, hipStream_t st) {
+  return for_batch_chunks(B, [&](int64_t b0, int64_t nb) {
+    const Geom g = make_geom<W, kLU>(S, D, b0);
+    if (g.ntiles == 0) return (int)MHC_OK;
+    mix_fwd_kernel<T, T, W, kLU, true, false, false><<<dim3(g.ntiles, nb), kThreads, 0, st>>>(
+        H, (const T*)nullptr, WRow{w, kOut}, WRow{nullptr, 0}, WRow{nullptr, 0}, bi, nullptr, g);
+    return hip_status(hipGetLastError(), "layer branch_input launch");
+  });
+}
+
+static int branch_input_any(const void* H, int dtype, const float* w, void* bi, int64_t B, int64_t S, int64_t D,
+                            hipStream_t st) {
+  if (S * D == 0) return MHC_OK;
+  return MHC_DISPATCH_DTYPE(dtype, [&] {
+    constexpr int WV = Vec<T>::N;
+    if (vec_ok(D, WV, {H, bi})) return launch_bi<T, WV>((const T*)H, w, (T*)bi, B, S, D, st);
+    return launch_bi<T, 1>((const T*)H, w, (T*)bi, B, S, D, st);
+  });
+}
+
+// Static weights (module.py:146-155), replicated for every batch row:
+// H_post = sigmoid(b_post), H_pre = sigmoid(b_pre)/(sum + 1e-8),
+// H_res = Sinkhorn(H_res_base, iters, eps = 1e-8).
+__global__ __launch_bounds__(kThreads) void static_weights_kernel(const float* __restrict__ bpre,
+                                                                  const float* __restrict__ bpost,
+                                                                  const float* __restrict__ bres,
+                                                                  float* __restrict__ w, int64_t B, int iters) {
+  const int64_t b = (int64_t)blockIdx.x * kThreads + threadIdx.x;
+  if (b >= B) return;
+  float* o = w + b * kOut;
+  float sg[4];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) sg[j] = sigmoidf(bpre[j]);
+  const float den = sg[0] + sg[1] + sg[2] + sg[3] + 1e-8f;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) o[j] = sg[j] / den;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) o[4 + j] = sigmoidf(bpost[j]);
+  float m[16];
+#pragma unroll
+  for (int j = 0; j < 16; ++j) m[j] = bres[j];
+  sk_forward(m, iters, 1e-8f);
+#pragma unroll
+  for (int j = 0; j < 16; ++j) o[8 + j] = m[j];
+}
+
+// Backward of static_weights_kernel through the batch expand:
+// every cotangent is first summed over b (fixed order), then pushed through
+// sigmoid / normalise / Sinkhorn once (the Sinkhorn VJP is linear in the cotangent).
+__global__ __launch_bounds__(kThreads) void static_weights_bwd_kernel(
+    const float* __restrict__ bpre, const float* __restrict__ bpost, const float* __restrict__ bres,
+    const float* __restrict__ w, const float* __restrict__ dpre, const float* __restrict__ dpost,
+    const float* __restrict__ dres, float* __restrict__ gbias, int64_t B, int iters) {
+  __shared__ float lds[4 * kOut];
+  float acc[kOut];
+#pragma unroll
+  for (int j = 0; j < kOut; ++j) acc[j] = 0.f;
+  for (int64_t b = threadIdx.x; b < B; b += kThreads) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) acc[j] += dpre[b * 4 + j];
+    if (dpost) {
+#pragma unroll
+      for (int j = 0; j < 4; ++j) acc[4 + j] += dpost[b * 4 + j];
+    }
+#pragma unroll
+    for (int j = 0; j < 16; ++j) acc[8 + j] += dres[b * 16 + j];
+  }
+  block_sum<kOut>(acc, lds);
+  if (threadIdx.x != 0) return;
+  // H_pre
+  float sg[4];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) sg[j] = sigmoidf(bpre[j]);
+  const float den = sg[0] + sg[1] + sg[2] + sg[3] + 1e-8f;
+  const float dot = acc[0] * w[0] + acc[1] * w[1] + acc[2] * w[2] + acc[3] * w[3];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) gbias[j] = (acc[j] - dot) / den * sg[j] * (1.f - sg[j]);
+  // H_post
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const float s = sigmoidf(bpost[j]);
+    gbias[4 + j] = acc[4 + j] * s * (1.f - s);
+  }
+  // H_res
+  float m[16], d[16];
+#pragma unroll
+  for (int j = 0; j < 16; ++j) {
+    m[j] = bres[j];
+    d[j] = acc[8 + j];
+  }
+  sk_backward(m, d, iters, 1e-8f);
+#pragma unroll
+  for (int j = 0; j < 16; ++j) gbias[8 + j] = d[j];
+}
+
+// Pass B (REDUCE only), pass C (WRITE_DH + HAS_GX) and the static pass BC
+// (REDUCE + WRITE_DH) share mix_bwd_kernel.
+template <typename T, int W, bool HAS_DHN, bool REDUCE, bool WRITE_DH, bool HAS_GX>
+static int launch_mix_bwd(const T* dbi, const T* dhn, const T* H, const float* gx, const float* w, T* dH,
+                          float* part, int64_t B, int64_t S, int64_t D, uint32_t* nblk_out, hipStream_t st) {
+  const Geom g0 = make_geom<W, kLU>(S, D, 0);
+  const uint32_t nblk = REDUCE ? reduce_blocks(g0.ntiles, B) : g0.ntiles;
+  if (nblk_out) *nblk_out = nblk;
+  if (nblk == 0) return MHC_OK;
+  const float inv_S = S > 0 ? 1.f / (float)S : 0.f;
+  return for_batch_chunks(B, [&](int64_t b0, int64_t nb) {
+    const Geom g = make_geom<W, kLU>(S, D, b0);
+    mix_bwd_kernel<T, W, kLU, HAS_DHN, REDUCE, WRITE_DH, HAS_GX><<<dim3(nblk, nb), kThreads, 0, st>>>(
+        dbi, dhn, H, gx, inv_S, WRow{w, kOut}, WRow{w + 8, kOut}, dH, part, g);
+    return hip_status(hipGetLastError(), "layer mix backward launch");
+  });
+}
+
+template <typename T, bool REDUCE, bool WRITE_DH, bool HAS_GX>
+static int mix_bwd_dispatch(const void* dbi, const void* dhn, const void* H, const float* gx, const float* w,
+                            void* dH, float* part, int64_t B, int64_t S, int64_t D, uint32_t* nblk,
+                            hipStream_t st) {
+  constexpr int WV = Vec<T>::N;
+  const bool vec = vec_ok(D, WV, {dbi, dhn, H, dH}) && (!HAS_GX || aligned16(gx));
+  if (dhn) {
+    if (vec)
+      return launch_mix_bwd<T, WV, true, REDUCE, WRITE_DH, HAS_GX>((const T*)dbi, (const T*)dhn, (const T*)H, gx, w,
+                                                                   (T*)dH, part, B, S, D, nblk, st);
+    return launch_mix_bwd<T, 1, true, REDUCE, WRITE_DH, HAS_GX>((const T*)dbi, (const T*)dhn, (const T*)H, gx, w,
+                                                                (T*)dH, part, B, S, D, nblk, st);
+  }
+  if (vec)
+    return launch_mix_bwd<T, WV, false, REDUCE, WRITE_DH, HAS_GX>((const T*)dbi, nullptr, (const T*)H, gx, w, (T*)dH,
+                                                                  part, B, S, D, nblk, st);
+  return launch_mix_bwd<T, 1, false, REDUCE, WRITE_DH, HAS_GX>((const T*)dbi, nullptr, (const T*)H, gx, w, (T*)dH,
+                                                               part, B, S, D, nblk, st);
+}
+
+}  // namespace mhc
+
+using namespace mhc;
+
+extern "C" size_t mhc_layer_workspace_bytes(int64_t B, int64_t S, int64_t D, int dtype) {
+  if (B <= 0) return 0;
+  return layer_ws(B, S, D, dtype).total;
+}
+
+#define LAYER_WS_CHECK(who)                                                                 \
+  const LayerWs L = layer_ws(B, S, D, dtype);                                               \
+  if (int rc_ = check_workspace(who, workspace, workspace_bytes, L.total)) return rc_;      \
+  char* wsb = (char*)workspace;
+
+extern "C" int mhc_layer_dynamic_forward(const void* H, int dtype, const float* phi, const float* H_pre_base,
+                                         const float* H_post_base, const float* H_res_base,
+                                         const float* alpha_pre, const float* alpha_post, const float* alpha_res,
+                                         void* branch_input, float* x, float* w, float* aux, int64_t B, int64_t S,
+                                         int64_t D, int iters, float eps, void* workspace, size_t workspace_bytes,
+                                         mhc_stream_t stream) {
+  if (int rc = check_bsd("layer_dynamic_forward", B, S, D)) return rc;
+  if (iters < 0) { set_error("layer_dynamic_forward: negative iters"); return MHC_ERR_ARG; }
+  if (B == 0) return MHC_OK;
+  if (!H || !phi || !H_pre_base || !H_post_base || !H_res_base || !alpha_pre || !alpha_post || !alpha_res ||
+      !branch_input || !x || !w || !aux) {
+    set_error("layer_dynamic_forward: null pointer");
+    return MHC_ERR_ARG;
+  }
+  LAYER_WS_CHECK("layer_dynamic_forward");
+  hipStream_t st = (hipStream_t)stream;
+  float* part = (float*)(wsb + L.pool_part);
+  if (int rc = mean_pool_any(H, dtype, x, phi, part, B, S, D, st)) return rc;
+  const int64_t cw = meanpool_columns(dtype, D);
+  const int nK = (int)((4 * D + cw - 1) / cw);
+  DynParams P{H_pre_base, H_post_base, H_res_base, alpha_pre, alpha_post, alpha_res};
+  dynw_finalize_kernel<><<<dim3((unsigned)((B + 3) / 4)), kThreads, 0, st>>>(
+      part, nK, B, 4 * D, P, OutRow{w, kOut}, OutRow{w + 4, kOut}, OutRow{w + 8, kOut}, aux, iters, eps);
+  if (int rc = hip_status(hipGetLastError(), "layer finalize launch")) return rc;
+  return branch_input_any(H, dtype, w, branch_input, B, S, D, st);
+}
+
+extern "C" int mhc_layer_static_forward(const void* H, int dtype, const float* H_pre_base, const float* H_post_base,
+                                        const float* H_res_base, void* branch_input, float* w, int64_t B,
+                                        int64_t S, int64_t D, int iters, mhc_stream_t stream) {
+  if (int rc = check_bsd("layer_static_forward", B, S, D)) return rc;
+  if (iters < 0) { set_error("layer_static_forward: negative iters"); return MHC_ERR_ARG; }
+  if (B == 0) return MHC_OK;
+  if (!H || !H_pre_base || !H_post_base || !H_res_base || !branch_input || !w) {
+    set_error("layer_static_forward: null pointer");
+    return MHC_ERR_ARG;
+  }
+  hipStream_t st = (hipStream_t)stream;
+  static_weights_kernel<<<dim3((unsigned)((B + kThreads - 1) / kThreads)), kThreads, 0, st>>>(
+      H_pre_base, H_post_base, H_res_base, w, B, iters);
+  if (int rc = hip_status(hipGetLastError(), "static weights launch")) return rc;
+  return branch_input_any(H, dtype, w, branch_input, B, S, D, st);
+}
+
+extern "C" int mhc_layer_add_forward(const void* H, int dtype_h, const void* branch_output, int dtype_bo,
+                                     const float* w, void* H_new, int64_t B, int64_t S, int64_t D,
+                                     mhc_stream_t stream) {
+  if (int rc = check_bsd("layer_add_forward", B, S, D)) return rc;
+  if (B * S * D == 0) return MHC_OK;
+  if (!H || !branch_output || !w || !H_new) {
+    set_error("layer_add_forward: null pointer");
+    return MHC_ERR_ARG;
+  }
+  hipStream_t st = (hipStream_t)stream;
+  return MHC_DISPATCH_DTYPE2(dtype_h, dtype_bo, [&] {
+    constexpr int WV = Vec<TH>::N > Vec<TB>::N ? Vec<TH>::N : Vec<TB>::N;
+    auto go = [&](auto wtag) {
+      constexpr int W = decltype(wtag)::value;
+      return for_batch_chunks(B, [&](int64_t b0, int64_t nb) {
+        const Geom g = make_geom<W, kLU>(S, D, b0);
+        mix_fwd_kernel<TH, TB, W, kLU, false, true, true><<<dim3(g.ntiles, nb), kThreads, 0, st>>>(
+            (const TH*)H, (const TB*)branch_output, WRow{nullptr, 0}, WRow{w + 8, kOut}, WRow{w + 4, kOut},
+            nullptr, (TH*)H_new, g);
+        return hip_status(hipGetLastError(), "layer add forward launch");
+      });
+    };
+    if (vec_ok(D, WV, {H, branch_output, H_new})) return go(std::integral_constant<int, WV>{});
+    return go(std::integral_constant<int, 1>{});
+  });
+}
+
+extern "C" int mhc_layer_add_backward(const void* dH_new, int dtype_h, const void* branch_output, int dtype_bo,
+                                      const float* w, void* d_branch_output, float* dH_post, int64_t B, int64_t S,
+                                      int64_t D, void* workspace, size_t workspace_bytes, mhc_stream_t stream) {
+  const int dtype = dtype_h;
+  if (int rc = check_bsd("layer_add_backward", B, S, D)) return rc;
+  if (B == 0) return MHC_OK;
+  if (!dH_new || !branch_output || !w || !d_branch_output || !dH_post) {
+    set_error("layer_add_backward: null pointer");
+    return MHC_ERR_ARG;
+  }
+  LAYER_WS_CHECK("layer_add_backward");
+  return add_residual_backward_any(dH_new, dtype_h, branch_output, dtype_bo, WRow{w + 4, kOut}, d_branch_output,
+                                   dH_post, B, S, D, (float*)(wsb + L.red_part), (hipStream_t)stream);
+}
+
+extern "C" int mhc_layer_dynamic_backward(const void* H, int dtype, const void* d_branch_input, const void* dH_new,
+                                          const float* dH_post, const float* phi, const float* H_pre_base,
+                                          const float* H_post_base, const float* H_res_base,
+                                          const float* alpha_pre, const float* alpha_post,
+                                          const float* alpha_res, const float* x, const float* w,
+                                          const float* aux, void* dH, float* grad_phi, float* grad_bias,
+                                          float* grad_alpha, int64_t B, int64_t S, int64_t D, int iters, float eps,
+                                          void* workspace, size_t workspace_bytes, mhc_stream_t stream) {
+  if (int rc = check_bsd("layer_dynamic_backward", B, S, D)) return rc;
+  if (iters < 0) { set_error("layer_dynamic_backward: negative iters"); return MHC_ERR_ARG; }
+  if (B == 0) return MHC_OK;
+  if (!H || !d_branch_input || !phi || !H_pre_base || !H_post_base || !H_res_base || !alpha_pre || !alpha_post ||
+      !alpha_res || !x || !w || !aux) {
+    set_error("layer_dynamic_backward: null pointer");
+    return MHC_ERR_ARG;
+  }
+  LAYER_WS_CHECK("layer_dynamic_backward");
+  hipStream_t st = (hipStream_t)stream;
+  float* part = (float*)(wsb + L.red_part);
+  float* dpre = (float*)(wsb + L.dpre);
+  float* dres = (float*)(wsb + L.dres);
+  float* rowbuf = (float*)(wsb + L.rowbuf);
+  float* gx = (float*)(wsb + L.gx);
+  // Pass B: dH_pre, dH_res.
+  uint32_t nblk = 0;
+  int rc = MHC_DISPATCH_DTYPE(dtype, [&] {
+    return mix_bwd_dispatch<T, true, false, false>(d_branch_input, dH_new, H, nullptr, w, nullptr, part, B, S, D,
+                                                   &nblk, st);
+  });
+  if (rc) return rc;
+  reduce_split_kernel<20, 4><<<dim3((unsigned)B), kThreads, 0, st>>>(part, dpre, dres, (int)nblk);
+  if ((rc = hip_status(hipGetLastError(), "layer pass B reduce launch"))) return rc;
+  // Weights backward.
+  DynParams P{H_pre_base, H_post_base, H_res_base, alpha_pre, alpha_post, alpha_res};
+  const int64_t K = 4 * D;
+  dynw_bwd_rows_kernel<><<<dim3((unsigned)((B + kThreads - 1) / kThreads)), kThreads, 0, st>>>(
+      aux, P, InRow{w, kOut}, InRow{dpre, 4}, InRow{dH_post, 4}, InRow{dres, 16}, rowbuf, B, K, iters, eps);
+  if ((rc = hip_status(hipGetLastError(), "layer weights backward rows launch"))) return rc;
+  if (K > 0) {
+    dynw_bwd_wide_kernel<float><<<dim3((unsigned)((K + kThreads - 1) / kThreads)), kThreads, 0, st>>>(
+        x, phi, rowbuf, dH ? gx : nullptr, grad_phi, B, K, aligned16(phi));
+    if ((rc = hip_status(hipGetLastError(), "layer weights backward wide launch"))) return rc;
+  }
+  dynw_bwd_sum_kernel<><<<1, kThreads, 0, st>>>(rowbuf, B, grad_bias, grad_alpha);
+  if ((rc = hip_status(hipGetLastError(), "layer weights backward sum launch"))) return rc;
+  if (!dH || S * D == 0) return MHC_OK;
+  // Pass C: dH.
+  return MHC_DISPATCH_DTYPE(dtype, [&] {
+    return mix_bwd_dispatch<T, false, true, true>(d_branch_input, dH_new, nullptr, gx, w, dH, nullptr, B, S, D,
+                                                  nullptr, st);
+  });
+}
+
+extern "C" int mhc_layer_static_backward(const void* H, int dtype, const void* d_branch_input, const void* dH_new,
+                                         const float* dH_post, const float* H_pre_base, const float* H_post_base,
+                                         const float* H_res_base, const float* w, void* dH, float* grad_bias,
+                                         int64_t B, int64_t S, int64_t D, int iters, void* workspace,
+                                         size_t workspace_bytes, mhc_stream_t stream) {
+  if (int rc = check_bsd("layer_static_backward", B, S, D)) return rc;
+  if (iters < 0) { set_error("layer_static_backward: negative iters"); return MHC_ERR_ARG; }
+  if (B == 0) return MHC_OK;
+  if (!H || !d_branch_input || !H_pre_base || !H_post_base || !H_res_base || !w || !grad_bias) {
+    set_error("layer_static_backward: null pointer");
+    return MHC_ERR_ARG;
+  }
+  LAYER_WS_CHECK("layer_static_backward");
+  hipStream_t st = (hipStream_t)stream;
+  float* part = (float*)(wsb + L.red_part);
+  float* dpre = (float*)(wsb + L.dpre);
+  float* dres = (float*)(wsb + L.dres);
+  // Pass BC: reductions and dH in one sweep.
+  uint32_t nblk = 0;
+  int rc = MHC_DISPATCH_DTYPE(dtype, [&] {
+    if (dH)
+      return mix_bwd_dispatch<T, true, true, false>(d_branch_input, dH_new, H, nullptr, w, dH, part, B, S, D, &nblk,
+                                                    st);
+    return mix_bwd_dispatch<T, true, false, false>(d_branch_input, dH_new, H, nullptr, w, nullptr, part, B, S, D,
+                                                   &nblk, st);
+  });
+  if (rc) return rc;
+  reduce_split_kernel<20, 4><<<dim3((unsigned)B), kThreads, 0, st>>>(part, dpre, dres, (int)nblk);
+  if ((rc = hip_status(hipGetLastError(), "layer static reduce launch"))) return rc;
+  static_weights_bwd_kernel<<<1, kThreads, 0, st>>>(H_pre_base, H_post_base, H_res_base, w, dpre, dH_post, dres,
+                                                    grad_bias, B, iters);
+  return hip_status(hipGetLastError(), "static weights backward launch");
+}
+
+extern "C" int mhc_layer_branch_input(const void* H, int dtype, const float* w, void* branch_input, int64_t B,
+                                      int64_t S, int64_t D, mhc_stream_t stream) {
+  if (int rc = check_bsd("layer_branch_input", B, S, D)) return rc;
+  if (B * S * D == 0) return MHC_OK;
+  if (!H || !w || !branch_input) {
+    set_error("layer_branch_input: null pointer");
+    return MHC_ERR_ARG;
+  }
+  return branch_input_any(H, dtype, w, branch_input, B, S, D, (hipStream_t)stream);
+}
+
+extern "C" int mhc_layer_mix_backward(const void* H, int dtype, const void* d_branch_input, const void* dH_new,
+                                      const float* w, void* dH, float* dH_pre, float* dH_res, int64_t B,
+                                      int64_t S, int64_t D, void* workspace, size_t workspace_bytes,
+                                      mhc_stream_t stream) {
+  if (int rc = check_bsd("layer_mix_backward", B, S, D)) return rc;
+  if (B == 0) return MHC_OK;
+  if (!H || !d_branch_input || !w || !dH_pre || !dH_res) {
+    set_error("layer_mix_backward: null pointer");
+    return MHC_ERR_ARG;
+  }
+  LAYER_WS_CHECK("layer_mix_backward");
+  hipStream_t st = (hipStream_t)stream;
+  float* part = (float*)(wsb + L.red_part);
+  uint32_t nblk = 0;
+  int rc = MHC_DISPATCH_DTYPE(dtype, [&] {
+    if (dH)
+      return mix_bwd_dispatch<T, true, true, false>(d_branch_input, dH_new, H, nullptr, w, dH, part, B, S, D, &nblk,
+                                                    st);
+    return mix_bwd_dispatch<T, true, false, false>(d_branch_input, dH_new, H, nullptr, w, nullptr, part, B, S, D,
+                                                   &nblk, st);
+  });
+  if (rc) return rc;
+  reduce_split_kernel<20, 4><<<dim3((unsigned)B), kThreads, 0, st>>>(part, dH_pre, dH_res, (int)nblk);
+  return hip_status(hipGetLastError(), "layer mix backward reduce launch");
+}

@@ -1,0 +1,419 @@
+// HBM-streaming kernels over the (B, S, 4, D) stream tensor.
+//
+// Work decomposition (all kernels here): grid.y = batch (so the 4-24 mixing
+// weights of a batch are wave-uniform scalar loads), grid.x = workgroups per
+// batch.  The per-batch index space is S * D/W "items"; an item is W
+// consecutive elements of one token row (W = 16 bytes worth, 4 fp32 or 8
+// bf16/fp16; W = 1 on the unaligned / ragged-D path) across all 4 streams.
+// Consecutive lanes take consecutive items, so each wave access is one
+// contiguous 1 KiB span per stream row.  A workgroup processes tiles of
+// 256 * U items; with U = 2 a lane keeps 8 (forward) to 18 (backward)
+// 16-byte loads in flight.  Kernels that reduce over (s, d) stride over tiles
+// and write one partial vector per workgroup; reduce_partials_kernel then sums
+// them in a fixed order (deterministic).
+#pragma once
+
+#include "common.hpp"
+
+namespace mhc {
+
+// Per-batch fp32 weight rows: element n of batch b is p[b * stride + n].
+struct WRow {
+  const float* p;
+  int64_t stride;
+};
+
+struct Geom {
+  int64_t S, D;   // sequence, per-stream dim
+  uint32_t nch;   // D / W
+  uint32_t items; // S * nch
+  uint32_t ntiles;
+  int64_t b0;     // first batch of this launch
+};
+
+template <int W, int U>
+__host__ inline Geom make_geom(int64_t S, int64_t D, int64_t b0) {
+  Geom g;
+  g.S = S;
+  g.D = D;
+  g.nch = (uint32_t)(D / W);
+  g.items = (uint32_t)(S * (D / W));
+  g.ntiles = (g.items + kThreads * U - 1) / (kThreads * U);
+  g.b0 = b0;
+  return g;
+}
+
+__device__ __forceinline__ void load_w4(WRow w, int64_t b, float (&v)[4]) {
+#pragma unroll
+  for (int n = 0; n < 4; ++n) v[n] = w.p[b * w.stride + n];
+}
+
+__device__ __forceinline__ void load_w16(WRow w, int64_t b, float (&v)[16]) {
+#pragma unroll
+  for (int n = 0; n < 16; ++n) v[n] = w.p[b * w.stride + n];
+}
+
+// ---------------------------------------------------------------------------
+// Forward mixing from H.
+//   BI:   bi[s,:]        = sum_n pre[n] H[s,n,:]
+//   RES:  out[s,n,:]     = sum_m res[n,m] H[s,m,:]            (+ ADD_BO)
+//   ADD_BO: out[s,n,:]  += post[n] bo[s,:]
+// Used for fused_stream_mix (BI + RES), the layer's branch_input pass (BI)
+// and the layer closure (RES + ADD_BO, H_residual never stored).
+// ---------------------------------------------------------------------------
+template <typename T, typename TB, int W, int U, bool BI, bool RES, bool ADD_BO>
+__global__ __launch_bounds__(kThreads) void mix_fwd_kernel(const T* __restrict__ H, const TB* __restrict__ bo,
+                                                           WRow pre, WRow res, WRow post, T* __restrict__ bi,
+                                                           T* __restrict__ out, Geom g) {
+  const int64_t b = g.b0 + blockIdx.y;
+  float wp[4], wr[16], wq[4];
+  if constexpr (BI) load_w4(pre, b, wp);
+  if constexpr (RES) load_w16(res, b, wr);
+  if constexpr (ADD_BO) load_w4(post, b, wq);
+  const int64_t D = g.D;
+  const T* Hb = H + b * g.S * 4 * D;
+  for (uint32_t tile = blockIdx.x; tile < g.ntiles; tile += gridDim.x) {
+    float h[U][4][W];
+    float bv[U][W];
+    int64_t s_[U], cw[U];
+    bool ok[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const uint32_t i = tile * (kThreads * U) + u * kThreads + threadIdx.x;
+      ok[u] = i < g.items;
+      const uint32_t s = ok[u] ? i / g.nch : 0;
+      const uint32_t c = ok[u] ? i - s * g.nch : 0;
+      s_[u] = s;
+      cw[u] = (int64_t)c * W;
+      if (ok[u]) {
+        const T* hp = Hb + s_[u] * 4 * D + cw[u];
+#pragma unroll
+        for (int n = 0; n < 4; ++n) ld<T, W>(hp + n * D, h[u][n]);
+        if constexpr (ADD_BO) ld<TB, W>(bo + b * g.S * D + s_[u] * D + cw[u], bv[u]);
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      if (!ok[u]) continue;
+      if constexpr (BI) {
+        float r[W];
+#pragma unroll
+        for (int e = 0; e < W; ++e)
+          r[e] = wp[0] * h[u][0][e] + wp[1] * h[u][1][e] + wp[2] * h[u][2][e] + wp[3] * h[u][3][e];
+        st<T, W>(bi + b * g.S * D + s_[u] * D + cw[u], r);
+      }
+      if constexpr (RES) {
+        T* op = out + b * g.S * 4 * D + s_[u] * 4 * D + cw[u];
+#pragma unroll
+        for (int n = 0; n < 4; ++n) {
+          float r[W];
+#pragma unroll
+          for (int e = 0; e < W; ++e) {
+            float v = wr[4 * n] * h[u][0][e] + wr[4 * n + 1] * h[u][1][e] + wr[4 * n + 2] * h[u][2][e] +
+                      wr[4 * n + 3] * h[u][3][e];
+            if constexpr (ADD_BO) v += wq[n] * bv[u][e];
+            r[e] = v;
+          }
+          st<T, W>(op + n * D, r);
+        }
+      }
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Add residual forward from a materialised H_residual (fused_add_residual):
+//   out[s,n,:] = hr[s,n,:] + post[n] bo[s,:]
+// ---------------------------------------------------------------------------
+template <typename T, typename TB, int W, int U>
+__global__ __launch_bounds__(kThreads) void add_residual_fwd_kernel(const T* __restrict__ hr,
+                                                                    const TB* __restrict__ bo, WRow post,
+                                                                    T* __restrict__ out, Geom g) {
+  const int64_t b = g.b0 + blockIdx.y;
+  float wq[4];
+  load_w4(post, b, wq);
+  const int64_t D = g.D;
+  for (uint32_t tile = blockIdx.x; tile < g.ntiles; tile += gridDim.x) {
+    float h[U][4][W];
+    float bv[U][W];
+    int64_t hoff[U];
+    bool ok[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const uint32_t i = tile * (kThreads * U) + u * kThreads + threadIdx.x;
+      ok[u] = i < g.items;
+      const uint32_t s = ok[u] ? i / g.nch : 0;
+      const uint32_t c = ok[u] ? i - s * g.nch : 0;
+      hoff[u] = b * g.S * 4 * D + (int64_t)s * 4 * D + (int64_t)c * W;
+      if (ok[u]) {
+#pragma unroll
+        for (int n = 0; n < 4; ++n) ld<T, W>(hr + hoff[u] + n * D, h[u][n]);
+        ld<TB, W>(bo + b * g.S * D + (int64_t)s * D + (int64_t)c * W, bv[u]);
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      if (!ok[u]) continue;
+#pragma unroll
+      for (int n = 0; n < 4; ++n) {
+        float r[W];
+#pragma unroll
+        for (int e = 0; e < W; ++e) r[e] = h[u][n][e] + wq[n] * bv[u][e];
+        st<T, W>(out + hoff[u] + n * D, r);
+      }
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Add residual backward (fused_add_residual, and the layer closure):
+//   d_bo[s,:] = sum_n post[n] dHn[s,n,:]              (written, dtype TB)
+//   part[k]   = sum dHn[s,k,:] * bo[s,:]   k < 4      (reduced -> dH_post)
+// ---------------------------------------------------------------------------
+template <typename T, typename TB, int W, int U>
+__global__ __launch_bounds__(kThreads) void add_residual_bwd_kernel(const T* __restrict__ dhn,
+                                                                    const TB* __restrict__ bo, WRow post,
+                                                                    TB* __restrict__ dbo, float* __restrict__ part,
+                                                                    Geom g) {
+  __shared__ float lds[4 * 4];
+  const int64_t b = g.b0 + blockIdx.y;
+  float wq[4];
+  load_w4(post, b, wq);
+  const int64_t D = g.D;
+  float acc[4] = {0.f, 0.f, 0.f, 0.f};
+  for (uint32_t tile = blockIdx.x; tile < g.ntiles; tile += gridDim.x) {
+    float h[U][4][W];
+    float bv[U][W];
+    int64_t boff[U];
+    bool ok[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const uint32_t i = tile * (kThreads * U) + u * kThreads + threadIdx.x;
+      ok[u] = i < g.items;
+      const uint32_t s = ok[u] ? i / g.nch : 0;
+      const uint32_t c = ok[u] ? i - s * g.nch : 0;
+      boff[u] = b * g.S * D + (int64_t)s * D + (int64_t)c * W;
+      if (ok[u]) {
+        const T* hp = dhn + b * g.S * 4 * D + (int64_t)s * 4 * D + (int64_t)c * W;
+#pragma unroll
+        for (int n = 0; n < 4; ++n) ld<T, W>(hp + n * D, h[u][n]);
+        ld<TB, W>(bo + boff[u], bv[u]);
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      if (!ok[u]) continue;
+      float r[W];
+#pragma unroll
+      for (int e = 0; e < W; ++e) {
+        r[e] = wq[0] * h[u][0][e] + wq[1] * h[u][1][e] + wq[2] * h[u][2][e] + wq[3] * h[u][3][e];
+#pragma unroll
+        for (int n = 0; n < 4; ++n) acc[n] += h[u][n][e] * bv[u][e];
+      }
+      st<TB, W>(dbo + boff[u], r);
+    }
+  }
+  block_sum<4>(acc, lds);
+  if (threadIdx.x == 0) {
+    float* pp = part + (b * gridDim.x + blockIdx.x) * 4;
+#pragma unroll
+    for (int k = 0; k < 4; ++k) pp[k] = acc[k];
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Mixing backward.  With dbi = d branch_input, dhn = d H_residual (or d H_new
+// in the layer path, where dH_residual = dH_new):
+//   WRITE_DH: dH[s,m,:] = pre[m] dbi + sum_n res[n,m] dhn[s,n,:] (+ gx[m,:] * inv_S)
+//   REDUCE:   part[0:4]  = sum dbi * H[s,n,:]          -> dH_pre
+//             part[4:20] = sum dhn[s,n,:] * H[s,m,:]   -> dH_res (n-major)
+// HAS_DHN = false treats dhn as zero (H_new / H_residual got no gradient).
+// HAS_GX adds the mean-pool backward term grad_x[b, m*D + d] / S.
+// ---------------------------------------------------------------------------
+template <typename T, int W, int U, bool HAS_DHN, bool REDUCE, bool WRITE_DH, bool HAS_GX>
+__global__ __launch_bounds__(kThreads) void mix_bwd_kernel(const T* __restrict__ dbi, const T* __restrict__ dhn,
+                                                           const T* __restrict__ H, const float* __restrict__ gx,
+                                                           float inv_S, WRow pre, WRow res, T* __restrict__ dH,
+                                                           float* __restrict__ part, Geom g) {
+  __shared__ float lds[4 * 20];
+  const int64_t b = g.b0 + blockIdx.y;
+  float wp[4], wr[16];
+  if constexpr (WRITE_DH) {
+    load_w4(pre, b, wp);
+    if constexpr (HAS_DHN) load_w16(res, b, wr);
+  }
+  const int64_t D = g.D;
+  float acc[20];
+#pragma unroll
+  for (int k = 0; k < 20; ++k) acc[k] = 0.f;
+  for (uint32_t tile = blockIdx.x; tile < g.ntiles; tile += gridDim.x) {
+    float db[U][W];
+    float dn[U][4][W];
+    float h[U][4][W];
+    float gv[U][4][W];
+    int64_t off[U];  // offset of (s, n=0, c*W) in the [S,4,D] plane
+    int64_t cw[U];
+    int64_t s_[U];
+    bool ok[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const uint32_t i = tile * (kThreads * U) + u * kThreads + threadIdx.x;
+      ok[u] = i < g.items;
+      const uint32_t s = ok[u] ? i / g.nch : 0;
+      const uint32_t c = ok[u] ? i - s * g.nch : 0;
+      s_[u] = s;
+      cw[u] = (int64_t)c * W;
+      off[u] = b * g.S * 4 * D + (int64_t)s * 4 * D + cw[u];
+      if (ok[u]) {
+        ld<T, W>(dbi + b * g.S * D + (int64_t)s * D + cw[u], db[u]);
+        if constexpr (HAS_DHN) {
+#pragma unroll
+          for (int n = 0; n < 4; ++n) ld<T, W>(dhn + off[u] + n * D, dn[u][n]);
+        }
+        if constexpr (REDUCE) {
+#pragma unroll
+          for (int n = 0; n < 4; ++n) ld<T, W>(H + off[u] + n * D, h[u][n]);
+        }
+        if constexpr (HAS_GX) {
+#pragma unroll
+          for (int n = 0; n < 4; ++n) ld<float, W>(gx + b * 4 * D + n * D + cw[u], gv[u][n]);
+        }
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      if (!ok[u]) continue;
+      if constexpr (REDUCE) {
+#pragma unroll
+        for (int e = 0; e < W; ++e) {
+#pragma unroll
+          for (int n = 0; n < 4; ++n) acc[n] += db[u][e] * h[u][n][e];
+          if constexpr (HAS_DHN) {
+#pragma unroll
+            for (int n = 0; n < 4; ++n)
+#pragma unroll
+              for (int m = 0; m < 4; ++m) acc[4 + 4 * n + m] += dn[u][n][e] * h[u][m][e];
+          }
+        }
+      }
+      if constexpr (WRITE_DH) {
+#pragma unroll
+        for (int m = 0; m < 4; ++m) {
+          float r[W];
+#pragma unroll
+          for (int e = 0; e < W; ++e) {
+            float v = wp[m] * db[u][e];
+            if constexpr (HAS_DHN)
+              v += wr[m] * dn[u][0][e] + wr[4 + m] * dn[u][1][e] + wr[8 + m] * dn[u][2][e] +
+                   wr[12 + m] * dn[u][3][e];
+            if constexpr (HAS_GX) v += gv[u][m][e] * inv_S;
+            r[e] = v;
+          }
+          st<T, W>(dH + off[u] + m * D, r);
+        }
+      }
+    }
+  }
+  if constexpr (REDUCE) {
+    block_sum<20>(acc, lds);
+    if (threadIdx.x == 0) {
+      float* pp = part + (b * gridDim.x + blockIdx.x) * 20;
+#pragma unroll
+      for (int k = 0; k < 20; ++k) pp[k] = acc[k];
+    }
+  }
+}
+
+// Final reduction of [B][nblk][NV] partials into up to two outputs:
+// out0[b*SPLIT + k] for k < SPLIT, out1[b*(NV-SPLIT) + k-SPLIT] otherwise.
+template <int NV, int SPLIT>
+__global__ __launch_bounds__(kThreads) void reduce_split_kernel(const float* __restrict__ part,
+                                                                float* __restrict__ out0,
+                                                                float* __restrict__ out1, int nblk) {
+  __shared__ float lds[4 * NV];
+  const int64_t b = blockIdx.x;
+  const float* p = part + b * nblk * NV;
+  float acc[NV];
+#pragma unroll
+  for (int i = 0; i < NV; ++i) acc[i] = 0.f;
+  for (int k = threadIdx.x; k < nblk; k += kThreads) {
+#pragma unroll
+    for (int i = 0; i < NV; ++i) acc[i] += p[(int64_t)k * NV + i];
+  }
+  block_sum<NV>(acc, lds);
+  if (threadIdx.x == 0) {
+#pragma unroll
+    for (int i = 0; i < NV; ++i) {
+      if (i < SPLIT) out0[b * SPLIT + i] = acc[i];
+      else out1[b * (NV - SPLIT) + (i - SPLIT)] = acc[i];
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Host-side launch helpers.
+// ---------------------------------------------------------------------------
+
+// True when every pointer is 16-byte aligned and D splits into whole 16-byte
+// vectors of every dtype involved.
+inline bool vec_ok(int64_t D, int W, std::initializer_list<const void*> ptrs) {
+  if (D % W != 0) return false;
+  for (const void* p : ptrs)
+    if (p && !aligned16(p)) return false;
+  return true;
+}
+
+// Workgroups per batch for a reduction kernel: about kRedBlocks in total
+// (8 per CU on a 256-CU MI355X), never more than there are tiles.  The cap is
+// a constant so workspace sizes do not depend on the device.
+constexpr int64_t kRedBlocks = 2048;
+
+inline uint32_t reduce_blocks(uint32_t ntiles, int64_t B) {
+  int64_t per_b = kRedBlocks / (B > 0 ? B : 1);
+  if (per_b > (int64_t)ntiles) per_b = ntiles;
+  if (per_b < 1) per_b = 1;
+  return (uint32_t)per_b;
+}
+
+// Bytes of partial sums a reduction kernel over B batches may write.
+inline size_t partial_bytes(int64_t B, int nv) {
+  const int64_t per_b = kRedBlocks / (B > 0 ? B : 1) > 1 ? kRedBlocks / (B > 0 ? B : 1) : 1;
+  return (size_t)(B * per_b * nv) * sizeof(float);
+}
+
+// Launch fn(b0, nb) for consecutive batch chunks that fit grid.y.
+template <class F>
+inline int for_batch_chunks(int64_t B, F&& fn) {
+  for (int64_t b0 = 0; b0 < B; b0 += kMaxGridY) {
+    const int64_t nb = (B - b0) < kMaxGridY ? (B - b0) : kMaxGridY;
+    if (int rc = fn(b0, nb)) return rc;
+  }
+  return MHC_OK;
+}
+
+// Checks the common (B, S, D) constraints of the streaming kernels.
+inline int check_bsd(const char* who, int64_t B, int64_t S, int64_t D) {
+  if (B < 0 || S < 0 || D < 0) {
+    set_error("%s: negative size (B=%lld S=%lld D=%lld)", who, (long long)B, (long long)S, (long long)D);
+    return MHC_ERR_ARG;
+  }
+  if (S * D >= (int64_t)1 << 32) {
+    set_error("%s: S*D = %lld exceeds the 2^32 per-batch item limit", who, (long long)(S * D));
+    return MHC_ERR_ARG;
+  }
+  return MHC_OK;
+}
+
+}  // namespace mhc
+
+// Nested dispatch over two bulk dtypes: T for the stream tensor, TB for
+// branch_output.
+#define MHC_DISPATCH_DTYPE2(dtype_a, dtype_b, ...)                      \
+  MHC_DISPATCH_DTYPE(dtype_a, [&] {                                     \
+    using TA_ = T;                                                      \
+    return MHC_DISPATCH_DTYPE(dtype_b, [&] {                            \
+      using TB = T;                                                     \
+      using TH = TA_;                                                   \
+      return __VA_ARGS__();                                             \
+    });                                                                 \
+  })

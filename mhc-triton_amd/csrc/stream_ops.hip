@@ -1,0 +1,192 @@
+// Entry points of the low-level stream ops: fused_stream_mix and
+// fused_add_residual, forward and backward (reference src/mhc/_kernels.py:617-687,
+// src/mhc/_backward.py:533-626).
+#include "stream_kernels.hpp"
+
+namespace mhc {
+
+constexpr int kU = 2;  // items per lane per tile
+
+template <typename T, int W>
+static int stream_mix_fwd(const T* H, const float* pre, const float* res, T* bi, T* out, int64_t B, int64_t S,
+                          int64_t D, hipStream_t st) {
+  return for_batch_chunks(B, [&](int64_t b0, int64_t nb) {
+    const Geom g = make_geom<W, kU>(S, D, b0);
+    if (g.ntiles == 0) return (int)MHC_OK;
+    mix_fwd_kernel<T, T, W, kU, true, true, false><<<dim3(g.ntiles, nb), kThreads, 0, st>>>(
+        H, (const T*)nullptr, WRow{pre, 4}, WRow{res, 16}, WRow{nullptr, 0}, bi, out, g);
+    return hip_status(hipGetLastError(), "stream_mix_forward launch");
+  });
+}
+
+template <typename T, int W>
+static int stream_mix_bwd(const T* dbi, const T* dhr, const T* H, const float* pre, const float* res, T* dH,
+                          float* dpre, float* dres, int64_t B, int64_t S, int64_t D, float* part,
+                          hipStream_t st) {
+  const Geom g0 = make_geom<W, kU>(S, D, 0);
+  const uint32_t nblk = reduce_blocks(g0.ntiles, B);
+  int rc = for_batch_chunks(B, [&](int64_t b0, int64_t nb) {
+    const Geom g = make_geom<W, kU>(S, D, b0);
+    mix_bwd_kernel<T, W, kU, true, true, true, false><<<dim3(nblk, nb), kThreads, 0, st>>>(
+        dbi, dhr, H, nullptr, 0.f, WRow{pre, 4}, WRow{res, 16}, dH, part, g);
+    return hip_status(hipGetLastError(), "stream_mix_backward launch");
+  });
+  if (rc) return rc;
+  reduce_split_kernel<20, 4><<<dim3((unsigned)B), kThreads, 0, st>>>(part, dpre, dres, (int)nblk);
+  return hip_status(hipGetLastError(), "stream_mix_backward reduce launch");
+}
+
+template <typename TH, typename TB, int W>
+static int add_res_fwd(const TH* hr, const TB* bo, const float* post, TH* out, int64_t B, int64_t S, int64_t D,
+                       hipStream_t st) {
+  return for_batch_chunks(B, [&](int64_t b0, int64_t nb) {
+    const Geom g = make_geom<W, kU>(S, D, b0);
+    if (g.ntiles == 0) return (int)MHC_OK;
+    add_residual_fwd_kernel<TH, TB, W, kU><<<dim3(g.ntiles, nb), kThreads, 0, st>>>(hr, bo, WRow{post, 4}, out, g);
+    return hip_status(hipGetLastError(), "add_residual_forward launch");
+  });
+}
+
+template <typename TH, typename TB, int W>
+static int add_res_bwd(const TH* dhn, const TB* bo, WRow post, TB* dbo, float* dpost, int64_t B, int64_t S,
+                       int64_t D, float* part, hipStream_t st) {
+  const Geom g0 = make_geom<W, kU>(S, D, 0);
+  const uint32_t nblk = reduce_blocks(g0.ntiles, B);
+  int rc = for_batch_chunks(B, [&](int64_t b0, int64_t nb) {
+    const Geom g = make_geom<W, kU>(S, D, b0);
+    add_residual_bwd_kernel<TH, TB, W, kU><<<dim3(nblk, nb), kThreads, 0, st>>>(dhn, bo, post, dbo, part, g);
+    return hip_status(hipGetLastError(), "add_residual_backward launch");
+  });
+  if (rc) return rc;
+  reduce_split_kernel<4, 4><<<dim3((unsigned)B), kThreads, 0, st>>>(part, dpost, nullptr, (int)nblk);
+  return hip_status(hipGetLastError(), "add_residual_backward reduce launch");
+}
+
+template <typename TH, typename TB>
+static constexpr int wide_w() {
+  return Vec<TH>::N > Vec<TB>::N ? Vec<TH>::N : Vec<TB>::N;
+}
+
+int check_workspace(const char* who, const void* ws, size_t have, size_t need) {
+  if (need == 0) return MHC_OK;
+  if (!ws || have < need) {
+    set_error("%s: workspace of %zu bytes required, %zu given", who, need, ws ? have : (size_t)0);
+    return MHC_ERR_WORKSPACE;
+  }
+  if ((reinterpret_cast<uintptr_t>(ws) & 255u) != 0) {
+    set_error("%s: workspace must be 256-byte aligned", who);
+    return MHC_ERR_WORKSPACE;
+  }
+  return MHC_OK;
+}
+
+// Exposed to the layer entry points (layer.hip).
+template <typename TH, typename TB>
+int add_residual_backward_t(const void* dhn, const void* bo, WRow post, void* dbo, float* dpost, int64_t B,
+                            int64_t S, int64_t D, float* part, hipStream_t st) {
+  constexpr int WV = wide_w<TH, TB>();
+  if (vec_ok(D, WV, {dhn, bo, dbo}))
+    return add_res_bwd<TH, TB, WV>((const TH*)dhn, (const TB*)bo, post, (TB*)dbo, dpost, B, S, D, part, st);
+  return add_res_bwd<TH, TB, 1>((const TH*)dhn, (const TB*)bo, post, (TB*)dbo, dpost, B, S, D, part, st);
+}
+
+int add_residual_backward_any(const void* dhn, int dtype_h, const void* bo, int dtype_bo, WRow post, void* dbo,
+                              float* dpost, int64_t B, int64_t S, int64_t D, float* part, hipStream_t st) {
+  return MHC_DISPATCH_DTYPE2(dtype_h, dtype_bo, [&] {
+    return add_residual_backward_t<TH, TB>(dhn, bo, post, dbo, dpost, B, S, D, part, st);
+  });
+}
+
+}  // namespace mhc
+
+using namespace mhc;
+
+extern "C" int mhc_stream_mix_forward(const void* H, const float* H_pre, const float* H_res, void* branch_input,
+                                      void* H_residual, int64_t B, int64_t S, int64_t D, int dtype,
+                                      mhc_stream_t stream) {
+  if (int rc = check_bsd("stream_mix_forward", B, S, D)) return rc;
+  if (B * S * D == 0) return MHC_OK;
+  if (!H || !H_pre || !H_res || !branch_input || !H_residual) {
+    set_error("stream_mix_forward: null pointer");
+    return MHC_ERR_ARG;
+  }
+  hipStream_t st = (hipStream_t)stream;
+  return MHC_DISPATCH_DTYPE(dtype, [&] {
+    constexpr int WV = Vec<T>::N;
+    if (vec_ok(D, WV, {H, branch_input, H_residual}))
+      return stream_mix_fwd<T, WV>((const T*)H, H_pre, H_res, (T*)branch_input, (T*)H_residual, B, S, D, st);
+    return stream_mix_fwd<T, 1>((const T*)H, H_pre, H_res, (T*)branch_input, (T*)H_residual, B, S, D, st);
+  });
+}
+
+extern "C" size_t mhc_stream_mix_backward_workspace_bytes(int64_t B, int64_t S, int64_t D, int dtype) {
+  (void)S; (void)D; (void)dtype;
+  return partial_bytes(B, 20);
+}
+
+extern "C" int mhc_stream_mix_backward(const void* d_branch_input, const void* dH_residual, const void* H,
+                                       const float* H_pre, const float* H_res, void* dH, float* dH_pre,
+                                       float* dH_res, int64_t B, int64_t S, int64_t D, int dtype, void* workspace,
+                                       size_t workspace_bytes, mhc_stream_t stream) {
+  if (int rc = check_bsd("stream_mix_backward", B, S, D)) return rc;
+  if (B == 0) return MHC_OK;
+  if (!d_branch_input || !dH_residual || !H || !H_pre || !H_res || !dH || !dH_pre || !dH_res) {
+    set_error("stream_mix_backward: null pointer");
+    return MHC_ERR_ARG;
+  }
+  if (int rc = check_workspace("stream_mix_backward", workspace, workspace_bytes,
+                               mhc_stream_mix_backward_workspace_bytes(B, S, D, dtype)))
+    return rc;
+  hipStream_t st = (hipStream_t)stream;
+  float* part = (float*)workspace;
+  return MHC_DISPATCH_DTYPE(dtype, [&] {
+    constexpr int WV = Vec<T>::N;
+    if (vec_ok(D, WV, {d_branch_input, dH_residual, H, dH}))
+      return stream_mix_bwd<T, WV>((const T*)d_branch_input, (const T*)dH_residual, (const T*)H, H_pre, H_res,
+                                   (T*)dH, dH_pre, dH_res, B, S, D, part, st);
+    return stream_mix_bwd<T, 1>((const T*)d_branch_input, (const T*)dH_residual, (const T*)H, H_pre, H_res,
+                                (T*)dH, dH_pre, dH_res, B, S, D, part, st);
+  });
+}
+
+extern "C" int mhc_add_residual_forward(const void* H_residual, int dtype_h, const void* branch_output,
+                                        int dtype_bo, const float* H_post, void* H_new, int64_t B, int64_t S,
+                                        int64_t D, mhc_stream_t stream) {
+  if (int rc = check_bsd("add_residual_forward", B, S, D)) return rc;
+  if (B * S * D == 0) return MHC_OK;
+  if (!H_residual || !branch_output || !H_post || !H_new) {
+    set_error("add_residual_forward: null pointer");
+    return MHC_ERR_ARG;
+  }
+  hipStream_t st = (hipStream_t)stream;
+  return MHC_DISPATCH_DTYPE2(dtype_h, dtype_bo, [&] {
+    constexpr int WV = wide_w<TH, TB>();
+    if (vec_ok(D, WV, {H_residual, branch_output, H_new}))
+      return add_res_fwd<TH, TB, WV>((const TH*)H_residual, (const TB*)branch_output, H_post, (TH*)H_new, B, S, D,
+                                     st);
+    return add_res_fwd<TH, TB, 1>((const TH*)H_residual, (const TB*)branch_output, H_post, (TH*)H_new, B, S, D,
+                                  st);
+  });
+}
+
+extern "C" size_t mhc_add_residual_backward_workspace_bytes(int64_t B, int64_t S, int64_t D, int dtype_h) {
+  (void)S; (void)D; (void)dtype_h;
+  return partial_bytes(B, 4);
+}
+
+extern "C" int mhc_add_residual_backward(const void* dH_new, int dtype_h, const void* branch_output, int dtype_bo,
+                                         const float* H_post, void* d_branch_output, float* dH_post, int64_t B,
+                                         int64_t S, int64_t D, void* workspace, size_t workspace_bytes,
+                                         mhc_stream_t stream) {
+  if (int rc = check_bsd("add_residual_backward", B, S, D)) return rc;
+  if (B == 0) return MHC_OK;
+  if (!dH_new || !branch_output || !H_post || !d_branch_output || !dH_post) {
+    set_error("add_residual_backward: null pointer");
+    return MHC_ERR_ARG;
+  }
+  if (int rc = check_workspace("add_residual_backward", workspace, workspace_bytes,
+                               mhc_add_residual_backward_workspace_bytes(B, S, D, dtype_h)))
+    return rc;
+  return add_residual_backward_any(dH_new, dtype_h, branch_output, dtype_bo, WRow{H_post, 4}, d_branch_output,
+                                   dH_post, B, S, D, (float*)workspace, (hipStream_t)stream);
+}

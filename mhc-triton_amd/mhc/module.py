@@ -1,0 +1,179 @@
+"""HyperConnection module (reference src/mhc/module.py).
+
+Same constructor arguments, parameter names / shapes / initialisation
+(state_dict-compatible with the reference and with ``HyperConnectionTorch``),
+and the same ``forward(H) -> (branch_input, add_residual)`` contract.  The
+forward runs on the layer-level HIP path of ``_layer.py``.
+"""
+
+from __future__ import annotations
+
+from typing import Callable, Tuple
+
+import torch
+import torch.nn as nn
+
+from . import _layer
+from ._kernels import mean_pool
+from .ops import sinkhorn_knopp
+
+
+class HyperConnection(nn.Module):
+    """Manifold-constrained hyper-connection over 4 residual streams.
+
+    Args:
+        dim: hidden dimension of each stream
+        num_streams: number of streams (must be 4)
+        layer_idx: layer index, selects the initial ``H_pre_base`` one-hot
+        dynamic: compute input-dependent weights
+        sinkhorn_iters: Sinkhorn-Knopp iterations for ``H_res``
+        init_scale: initial value of the alpha / scale parameters
+        eps: numerical-stability constant of the dynamic path
+        use_fused_weights: use the fused Eq. 14-19 weights (else three Linears)
+
+    Example::
+
+        hc = HyperConnection(dim=512).cuda()
+        H = torch.randn(2, 128, 4, 512, device="cuda")
+        branch_input, add_residual = hc(H)
+        H_new = add_residual(my_layer(branch_input))
+    """
+
+    def __init__(
+        self,
+        dim: int,
+        num_streams: int = 4,
+        layer_idx: int = 0,
+        dynamic: bool = True,
+        sinkhorn_iters: int = 20,
+        init_scale: float = 0.1,
+        eps: float = 1e-6,
+        use_fused_weights: bool = True,
+    ):
+        super().__init__()
+        if num_streams != 4:
+            raise ValueError("HIP kernels require num_streams=4")
+        self.dim = dim
+        self.num_streams = num_streams
+        self.dynamic = dynamic
+        self.sinkhorn_iters = sinkhorn_iters
+        self.init_scale = init_scale
+        self.layer_idx = layer_idx
+        self.eps = eps
+        self.use_fused_weights = use_fused_weights and dynamic
+
+        n = num_streams
+        in_dim = n * dim
+        out_dim = n * n + 2 * n
+
+        self.H_post_base = nn.Parameter(torch.ones(n))
+        pre = torch.zeros(n)
+        pre[layer_idx % n] = 1.0
+        self.H_pre_base = nn.Parameter(pre)
+        self.H_res_base = nn.Parameter(torch.eye(n))
+
+        if dynamic:
+            if use_fused_weights:
+                # phi [in_dim, 24], columns: H_pre (4), H_post (4), H_res (16, row-major)
+                self.phi = nn.Parameter(torch.zeros(in_dim, out_dim))
+                # 1-element tensors (FSDP / fully_shard friendly, as in the reference)
+                self.alpha_pre = nn.Parameter(torch.tensor([init_scale]))
+                self.alpha_post = nn.Parameter(torch.tensor([init_scale]))
+                self.alpha_res = nn.Parameter(torch.tensor([init_scale]))
+            else:
+                self.W_post = nn.Linear(in_dim, n, bias=False)
+                self.W_pre = nn.Linear(in_dim, n, bias=False)
+                self.W_res = nn.Linear(in_dim, n * n, bias=False)
+                nn.init.zeros_(self.W_post.weight)
+                nn.init.zeros_(self.W_pre.weight)
+                nn.init.zeros_(self.W_res.weight)
+                self.scale_post = nn.Parameter(torch.tensor([init_scale]))
+                self.scale_pre = nn.Parameter(torch.tensor([init_scale]))
+                self.scale_res = nn.Parameter(torch.tensor([init_scale]))
+
+    def _check_input(self, H: torch.Tensor) -> None:
+        if H.dim() != 4 or H.shape[2] != self.num_streams or H.shape[3] != self.dim:
+            raise ValueError(f"H must be (batch, seq, {self.num_streams}, {self.dim}), got {tuple(H.shape)}")
+
+    def _unfused_weights(self, H: torch.Tensor) -> torch.Tensor:
+        """Packed weights [B,24] of the unfused dynamic path (reference
+        src/mhc/module.py:179-201): RMS-normalised mean, three Linears, sigmoid
+        (no x2 on H_post), normalisation with 1e-8 and Sinkhorn with eps 1e-8."""
+        B = H.shape[0]
+        n = self.num_streams
+        x = _MeanPool.apply(H).to(self.W_pre.weight.dtype)
+        rms = torch.sqrt((x * x).mean(dim=-1, keepdim=True) + self.eps)
+        x = x / rms
+        delta_post = self.W_post(x) * self.scale_post
+        delta_pre = self.W_pre(x) * self.scale_pre
+        delta_res = self.W_res(x).reshape(B, n, n) * self.scale_res
+        H_post = torch.sigmoid(self.H_post_base + delta_post)
+        H_pre = torch.sigmoid(self.H_pre_base + delta_pre)
+        H_pre = H_pre / (H_pre.sum(dim=-1, keepdim=True) + 1e-8)
+        H_res = sinkhorn_knopp((self.H_res_base + delta_res).contiguous(), self.sinkhorn_iters)
+        return torch.cat([H_pre, H_post, H_res.reshape(B, n * n)], dim=1)
+
+    def forward(self, H: torch.Tensor) -> Tuple[torch.Tensor, Callable[[torch.Tensor], torch.Tensor]]:
+        """H (batch, seq, 4, dim) -> (branch_input (batch, seq, dim), add_residual)."""
+        self._check_input(H)
+        stash = _layer._Stash()
+        if not self.dynamic:
+            bi, w = _layer._StaticLayer.apply(H, self.H_pre_base, self.H_post_base, self.H_res_base, stash,
+                                              self.sinkhorn_iters)
+        elif self.use_fused_weights:
+            bi, w = _layer._DynamicLayer.apply(H, self.phi, self.H_pre_base, self.H_post_base, self.H_res_base,
+                                               self.alpha_pre, self.alpha_post, self.alpha_res, stash,
+                                               self.sinkhorn_iters, self.eps)
+        else:
+            bi, w = _layer._GenericLayer.apply(H, self._unfused_weights(H), stash)
+
+        def add_residual(branch_output: torch.Tensor) -> torch.Tensor:
+            return _layer._LayerAdd.apply(H, branch_output, w, stash)
+
+        return bi, add_residual
+
+    def extra_repr(self) -> str:
+        return (
+            f"dim={self.dim}, num_streams={self.num_streams}, "
+            f"dynamic={self.dynamic}, sinkhorn_iters={self.sinkhorn_iters}, "
+            f"use_fused_weights={self.use_fused_weights}"
+        )
+
+    def init_weights(self, layer_idx=None):
+        """Re-initialise every parameter, optionally moving to a new layer index
+        (reference src/mhc/module.py:191-224)."""
+        n = self.num_streams
+        if layer_idx is not None:
+            self.layer_idx = layer_idx
+        nn.init.ones_(self.H_post_base)
+        nn.init.zeros_(self.H_pre_base)
+        with torch.no_grad():
+            self.H_pre_base[self.layer_idx % n] = 1.0
+        nn.init.eye_(self.H_res_base)
+        if self.dynamic:
+            if self.use_fused_weights:
+                nn.init.zeros_(self.phi)
+                nn.init.constant_(self.alpha_pre, self.init_scale)
+                nn.init.constant_(self.alpha_post, self.init_scale)
+                nn.init.constant_(self.alpha_res, self.init_scale)
+            else:
+                nn.init.zeros_(self.W_post.weight)
+                nn.init.zeros_(self.W_pre.weight)
+                nn.init.zeros_(self.W_res.weight)
+
+
+class _MeanPool(torch.autograd.Function):
+    """x = mean over the sequence, [B, 4*dim] f32, on the HIP mean-pool kernel.
+    Backward is the broadcast grad_x / S (a stride-0 view, no copy)."""
+
+    @staticmethod
+    def forward(ctx, H):
+        ctx.shape = H.shape
+        ctx.dtype = H.dtype
+        return mean_pool(H)
+
+    @staticmethod
+    def backward(ctx, gx):
+        B, S, n, D = ctx.shape
+        g = (gx / S).to(ctx.dtype).reshape(B, 1, n, D)
+        return g.expand(B, S, n, D)

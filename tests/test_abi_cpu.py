@@ -1,0 +1,114 @@
+"""The C-ABI boundary, checked without a GPU: the library loads, exports every
+function include/mhc_abi.h declares, the ctypes binding agrees with the header
+on arity, and host-side argument validation returns the documented status
+codes before any device work.
+"""
+
+import ctypes
+import os
+import re
+
+import pytest
+import torch
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "mhc_abi.h")
+
+
+def _declared():
+    """{name: n_args} for every function prototype in the header."""
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    out = {}
+    for m in re.finditer(r"\b(?:int|size_t|const char\*)\s+(mhc_\w+)\s*\(([^)]*)\)\s*;", text):
+        args = m.group(2).strip()
+        out[m.group(1)] = 0 if args in ("", "void") else len(args.split(","))
+    return out
+
+
+@pytest.fixture(scope="module")
+def lib():
+    from mhc import _lib
+
+    if not os.path.exists(_lib.LIB_PATH):
+        import __graft_entry__
+
+        __graft_entry__.build()
+    return _lib.load()
+
+
+def test_header_declares_the_expected_surface():
+    names = set(_declared())
+    for op in ("sinkhorn_forward", "sinkhorn_backward", "stream_mix_forward", "stream_mix_backward",
+               "add_residual_forward", "add_residual_backward", "dynamic_weights_forward",
+               "dynamic_weights_backward", "layer_dynamic_forward", "layer_dynamic_backward"):
+        assert "mhc_" + op in names
+
+
+def test_library_exports_every_declared_symbol(lib):
+    for name in _declared():
+        assert hasattr(lib, name), name
+
+
+def test_ctypes_binding_matches_header_arity():
+    from mhc import _lib
+
+    decl = _declared()
+    assert set(decl) == set(_lib._SIGNATURES)
+    for name, n in decl.items():
+        assert len(_lib._SIGNATURES[name][1]) == n, name
+
+
+def test_version_and_workspace_queries(lib):
+    from mhc import _lib
+
+    assert lib.mhc_abi_version() == _lib.ABI_VERSION
+    assert lib.mhc_stream_mix_backward_workspace_bytes(4, 4096, 4096, 1) > 0
+    assert lib.mhc_add_residual_backward_workspace_bytes(4, 4096, 4096, 1) > 0
+    assert lib.mhc_dynamic_weights_workspace_bytes(0, 16384) == 0
+    ws = lib.mhc_layer_workspace_bytes(4, 4096, 4096, 1)
+    # grad_x [B, 4D] f32 dominates: at least 256 KiB here, and 256-byte granular
+    assert ws >= 4 * 4 * 4096 * 4 and ws % 256 == 0
+
+
+def test_host_side_validation_without_gpu(lib):
+    # negative sizes, bad dtype codes, missing workspace: rejected before any launch
+    assert lib.mhc_sinkhorn_forward(None, None, -1, 0, 20, 1e-8, None) == 1
+    assert lib.mhc_sinkhorn_forward(None, None, 0, 0, 20, 1e-8, None) == 0  # empty is a no-op
+    assert lib.mhc_sinkhorn_forward(None, None, 4, 0, -3, 1e-8, None) == 1
+    assert lib.mhc_stream_mix_forward(None, None, None, None, None, 2, 3, 4, 0, None) == 1  # null pointers
+    assert lib.mhc_stream_mix_forward(None, None, None, None, None, 0, 3, 4, 0, None) == 0
+    assert lib.mhc_stream_mix_forward(16, 16, 16, 16, 16, 2, 3, 4, 7, None) == 2  # dtype 7
+    assert b"dtype" in lib.mhc_last_error()
+    assert lib.mhc_stream_mix_backward(16, 16, 16, 16, 16, 16, 16, 16, 2, 3, 4, 0, None, 0, None) == 3
+    assert b"workspace" in lib.mhc_last_error()
+    assert lib.mhc_stream_mix_forward(16, 16, 16, 16, 16, 1, 1 << 20, 1 << 13, 0, None) == 1  # S*D >= 2^32
+    assert lib.mhc_layer_dynamic_forward(None, 0, *([None] * 11), 1, 1, 1, -1, 1e-6, None, 0, None) == 1
+
+
+def test_ops_reject_cpu_tensors():
+    import mhc
+
+    M = torch.randn(2, 4, 4)
+    with pytest.raises(RuntimeError, match="ROCm GPU"):
+        mhc.sinkhorn_knopp(M)
+    H = torch.randn(1, 2, 4, 8)
+    with pytest.raises(RuntimeError, match="ROCm GPU"):
+        mhc.fused_stream_mix(H, torch.rand(1, 4), torch.rand(1, 4, 4))
+    hc = mhc.HyperConnection(8)
+    with pytest.raises(RuntimeError, match="ROCm GPU"):
+        hc(H)
+
+
+def test_shape_errors_are_assertion_compatible():
+    import mhc
+
+    with pytest.raises(AssertionError):
+        mhc.sinkhorn_knopp(torch.zeros(2, 4, 5))
+    with pytest.raises(AssertionError):
+        mhc.fused_dynamic_weights(torch.zeros(2, 8), torch.zeros(8, 23), torch.zeros(24),
+                                  torch.ones(1), torch.ones(1), torch.ones(1))
+    with pytest.raises(ValueError):
+        mhc.HyperConnection(8, num_streams=3)
+    with pytest.raises(ValueError):
+        mhc.HyperConnection(8)(torch.zeros(1, 2, 4, 9))

@@ -1,0 +1,194 @@
+"""GPU parity of mhc.HyperConnection (forward and every gradient) against the
+float64 oracle layer, plus the closure / autograd edge cases.
+
+Inputs follow one draw order from a CPU generator seeded with 0:
+H, phi, H_res_base, branch_output, dH_new, d_branch_input.
+"""
+
+import numpy as np
+import pytest
+import torch
+
+from helpers import rel_err, to_np
+from oracle import mhc_oracle as O
+
+pytestmark = pytest.mark.gpu
+
+DEV = "cuda"
+
+
+def make_case(B, S, D, dtype, dynamic=True, fused=True, phi_std=None, res_std=None, seed=0, layer_idx=0):
+    import mhc
+
+    g = torch.Generator()
+    g.manual_seed(seed)
+    H = torch.randn((B, S, 4, D), generator=g).to(dtype)
+    hc = mhc.HyperConnection(D, dynamic=dynamic, use_fused_weights=fused, layer_idx=layer_idx)
+    if phi_std is not None and dynamic and fused:
+        phi_t = torch.randn((24, 4 * D), generator=g) * phi_std  # [24, 4D], transposed to the API layout
+        with torch.no_grad():
+            hc.phi.copy_(phi_t.T)
+    if phi_std is not None and dynamic and not fused:
+        with torch.no_grad():
+            for lin in (hc.W_pre, hc.W_post, hc.W_res):
+                lin.weight.copy_(torch.randn(lin.weight.shape, generator=g) * phi_std)
+    if res_std is not None:
+        with torch.no_grad():
+            hc.H_res_base.copy_(torch.randn((4, 4), generator=g) * res_std)
+    bo = torch.randn((B, S, D), generator=g).to(dtype)
+    dHn = torch.randn((B, S, 4, D), generator=g).to(dtype)
+    dbi = torch.randn((B, S, D), generator=g).to(dtype)
+    return hc.to(DEV), H.to(DEV), bo.to(DEV), dHn.to(DEV), dbi.to(DEV)
+
+
+def params_np(hc):
+    return {n.replace(".weight", ""): to_np(p) for n, p in hc.named_parameters()}
+
+
+def run_gpu(hc, H, bo, dHn, dbi):
+    Hl = H.clone().requires_grad_(True)
+    bol = bo.clone().requires_grad_(True)
+    hc.zero_grad(set_to_none=True)
+    bi, add = hc(Hl)
+    Hn = add(bol)
+    torch.autograd.backward([Hn, bi], [dHn, dbi])
+    grads = {n.replace(".weight", ""): p.grad for n, p in hc.named_parameters()}
+    grads["H"] = Hl.grad
+    grads["bo"] = bol.grad
+    return bi, Hn, grads
+
+
+def check_layer(hc, H, bo, dHn, dbi, fwd_tol, h_tol, p_tol):
+    bi, Hn, grads = run_gpu(hc, H, bo, dHn, dbi)
+    p = params_np(hc)
+    obi, oHn, cache = O.layer_forward(p, to_np(H), to_np(bo), hc.dynamic, hc.use_fused_weights or not hc.dynamic,
+                                      hc.sinkhorn_iters, hc.eps)
+    og = {k.replace(".weight", ""): v for k, v in O.layer_backward(p, cache, to_np(dHn), to_np(dbi)).items()}
+    errs = {"bi": rel_err(to_np(bi), obi), "H_new": rel_err(to_np(Hn), oHn)}
+    for k, v in og.items():
+        errs["d" + k] = rel_err(to_np(grads[k]).reshape(np.shape(v)), v)
+    assert bi.dtype == H.dtype and Hn.dtype == H.dtype
+    assert errs["bi"] < fwd_tol and errs["H_new"] < fwd_tol, errs
+    assert errs["dH"] < h_tol and errs["dbo"] < h_tol, errs
+    for k, e in errs.items():
+        if k not in ("bi", "H_new", "dH", "dbo"):
+            assert e < p_tol, (k, errs)
+    return errs
+
+
+@pytest.mark.parametrize("phi_std", [None, 0.02])
+def test_config1_fp32_dynamic(phi_std):
+    """Config 1: dim 512, fp32, H (2, 128, 4, 512); default init (phi = 0, the
+    sgn(0) case in the Sinkhorn backward) and phi ~ N(0, 0.02)."""
+    hc, H, bo, dHn, dbi = make_case(2, 128, 512, torch.float32, phi_std=phi_std)
+    check_layer(hc, H, bo, dHn, dbi, 1e-5, 1e-4, 1e-4)
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_dynamic_low_precision(dtype):
+    """Config 3 / 4 at reduced size: bf16 / fp16 H, fp32 parameters."""
+    hc, H, bo, dHn, dbi = make_case(2, 96, 448, dtype, phi_std=0.02)
+    check_layer(hc, H, bo, dHn, dbi, 2e-2, 2e-2, 1e-3)
+
+
+def test_static_fp16():
+    """Config 5 at reduced size: dynamic=False, fp16 H, H_res_base ~ N(0, 1)."""
+    hc, H, bo, dHn, dbi = make_case(4, 64, 256, torch.float16, dynamic=False, res_std=1.0)
+    check_layer(hc, H, bo, dHn, dbi, 2e-2, 2e-2, 1e-3)
+
+
+def test_static_fp32():
+    hc, H, bo, dHn, dbi = make_case(2, 33, 96, torch.float32, dynamic=False, res_std=1.0, layer_idx=2)
+    check_layer(hc, H, bo, dHn, dbi, 1e-5, 1e-4, 1e-4)
+
+
+def test_unfused_dynamic_fp32():
+    hc, H, bo, dHn, dbi = make_case(2, 40, 64, torch.float32, fused=False, phi_std=0.05)
+    check_layer(hc, H, bo, dHn, dbi, 1e-5, 1e-4, 1e-4)
+
+
+def test_ragged_dim_bf16():
+    """D not a multiple of the 8-element vector: the scalar-path kernels."""
+    hc, H, bo, dHn, dbi = make_case(3, 17, 100, torch.bfloat16, phi_std=0.02)
+    check_layer(hc, H, bo, dHn, dbi, 2e-2, 2e-2, 1e-3)
+
+
+# --------------------------------------------------------------------------- closure edge cases
+
+def _oracle_grads(hc, H, bo, dHn, dbi):
+    p = params_np(hc)
+    _, _, cache = O.layer_forward(p, to_np(H), to_np(bo), hc.dynamic, True, hc.sinkhorn_iters, hc.eps)
+    return O.layer_backward(p, cache, dHn, dbi)
+
+
+def test_closure_called_twice():
+    hc, H, bo, dHn, dbi = make_case(2, 16, 64, torch.float32, phi_std=0.05)
+    Hl = H.clone().requires_grad_(True)
+    bi, add = hc(Hl)
+    bo2 = torch.randn_like(bo)
+    Hn1, Hn2 = add(bo), add(bo2)
+    torch.autograd.backward([Hn1, Hn2, bi], [dHn, dHn, dbi])
+    g1 = _oracle_grads(hc, H, bo, to_np(dHn), to_np(dbi))
+    g2 = _oracle_grads(hc, H, bo2, to_np(dHn), np.zeros_like(to_np(dbi)))
+    # the loss is additive over the two closure outputs, so the gradient is the
+    # sum of two single-call oracle gradients (the second with no branch_input term)
+    assert rel_err(to_np(Hl.grad), g1["H"] + g2["H"]) < 1e-4
+    assert rel_err(to_np(hc.phi.grad), g1["phi"] + g2["phi"]) < 1e-4
+
+
+def test_closure_never_called_and_bi_only():
+    hc, H, bo, dHn, dbi = make_case(2, 16, 64, torch.float32, phi_std=0.05)
+    Hl = H.clone().requires_grad_(True)
+    bi, _ = hc(Hl)
+    bi.backward(dbi)
+    g = _oracle_grads(hc, H, bo, np.zeros(H.shape), to_np(dbi))
+    assert rel_err(to_np(Hl.grad), g["H"]) < 1e-4
+    assert rel_err(to_np(hc.phi.grad), g["phi"]) < 1e-4
+    assert rel_err(to_np(hc.H_post_base.grad), g["H_post_base"]) < 1e-4
+
+
+def test_h_new_only_and_h_without_grad():
+    hc, H, bo, dHn, dbi = make_case(2, 16, 64, torch.float32, phi_std=0.05)
+    bol = bo.clone().requires_grad_(True)
+    bi, add = hc(H)  # H does not require grad
+    add(bol).backward(dHn)
+    g = _oracle_grads(hc, H, bo, to_np(dHn), np.zeros(bo.shape))
+    assert rel_err(to_np(bol.grad), g["bo"]) < 1e-4
+    assert rel_err(to_np(hc.phi.grad), g["phi"]) < 1e-4
+    assert rel_err(to_np(hc.alpha_res.grad), g["alpha_res"]) < 1e-4
+
+
+def test_no_grad_forward_matches():
+    hc, H, bo, dHn, dbi = make_case(2, 16, 64, torch.bfloat16, phi_std=0.02)
+    with torch.no_grad():
+        bi, add = hc(H)
+        Hn = add(bo)
+    obi, oHn, _ = O.layer_forward(params_np(hc), to_np(H), to_np(bo))
+    assert rel_err(to_np(bi), obi) < 2e-2 and rel_err(to_np(Hn), oHn) < 2e-2
+
+
+def test_state_dict_roundtrip_with_torch_baseline():
+    import mhc
+
+    hc = mhc.HyperConnection(64, layer_idx=3)
+    ref = mhc.HyperConnectionTorch(64, layer_idx=3)
+    ref.load_state_dict(hc.state_dict())
+    assert set(hc.state_dict()) == set(ref.state_dict())
+
+
+def test_training_steps_change_parameters():
+    import mhc
+
+    torch.manual_seed(42)
+    hc = mhc.HyperConnection(dim=128, dynamic=True).to(DEV)
+    layer = torch.nn.Linear(128, 128, device=DEV)
+    opt = torch.optim.Adam(list(hc.parameters()) + list(layer.parameters()))
+    init = {n: p.detach().clone() for n, p in hc.named_parameters()}
+    for _ in range(3):
+        opt.zero_grad()
+        H = torch.randn(2, 32, 4, 128, device=DEV, requires_grad=True)
+        bi, add = hc(H)
+        add(layer(bi)).sum().backward()
+        opt.step()
+    changed = sum(1 for n, p in hc.named_parameters() if not torch.allclose(p, init[n]))
+    assert changed > 0

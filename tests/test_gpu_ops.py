@@ -1,0 +1,241 @@
+"""GPU parity of the low-level ops (mhc.sinkhorn_knopp, fused_stream_mix,
+fused_add_residual, fused_dynamic_weights) against the float64 oracle.
+
+Tolerances (normwise relative error, max|y - y_ref| / max|y_ref|):
+  fp32 forward 1e-5, fp32 gradients 1e-4, outputs from bf16/fp16 inputs 2e-2
+(the oracle is fed the same bf16/fp16 values, upcast).
+"""
+
+import numpy as np
+import pytest
+import torch
+
+from helpers import rel_err, to_np
+from oracle import mhc_oracle as O
+
+pytestmark = pytest.mark.gpu
+
+DEV = "cuda"
+TOL = {torch.float32: 1e-5, torch.bfloat16: 2e-2, torch.float16: 2e-2}
+GTOL = {torch.float32: 1e-4, torch.bfloat16: 2e-2, torch.float16: 2e-2}
+
+
+def gen(seed=0):
+    g = torch.Generator()
+    g.manual_seed(seed)
+    return g
+
+
+def randn(shape, g, dtype=torch.float32, scale=1.0):
+    return (torch.randn(shape, generator=g, dtype=torch.float32) * scale).to(dtype).to(DEV)
+
+
+# --------------------------------------------------------------------------- Sinkhorn
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16, torch.float16])
+def test_sinkhorn_forward(dtype):
+    import mhc
+
+    g = gen(0)
+    M = randn((1000, 4, 4), g, dtype)
+    P = mhc.sinkhorn_knopp(M, 20)
+    assert P.dtype == dtype and P.shape == M.shape
+    assert rel_err(to_np(P), O.sinkhorn(to_np(M), 20, 1e-8)) < TOL[dtype]
+
+
+@pytest.mark.parametrize("iters", [0, 1, 7, 20, 33])
+def test_sinkhorn_forward_backward_iters(iters):
+    import mhc
+
+    g = gen(1)
+    M = randn((300, 4, 4), g)
+    M[0, 0, 0] = 0.0  # exercise sgn(0) = 0
+    M[7, 2, 1] = 0.0
+    dP = randn((300, 4, 4), g)
+    Ml = M.clone().requires_grad_(True)
+    P = mhc.sinkhorn_knopp(Ml, iters, 1e-8)
+    P.backward(dP)
+    assert rel_err(to_np(P), O.sinkhorn(to_np(M), iters, 1e-8)) < 1e-5
+    ref = O.sinkhorn_backward(to_np(M), to_np(dP), iters, 1e-8)
+    assert rel_err(to_np(Ml.grad), ref) < 1e-4
+    assert Ml.grad[0, 0, 0].item() == 0.0 and Ml.grad[7, 2, 1].item() == 0.0
+
+
+def test_sinkhorn_config2_column_sums_and_oracle():
+    """Config 2: 2^20 log-normal fp32 matrices, 20 iterations, N(0,1) upstream gradient."""
+    import mhc
+
+    g = gen(0)
+    n = 1 << 20
+    M = torch.exp(torch.randn((n, 4, 4), generator=g)).to(DEV)
+    dP = torch.randn((n, 4, 4), generator=g).to(DEV)
+    Ml = M.clone().requires_grad_(True)
+    P = mhc.sinkhorn_knopp(Ml, 20)
+    P.backward(dP)
+    Pn = to_np(P)
+    # columns: last step of every round, so |colsum - 1| <= 1e-5 for every matrix
+    assert np.abs(Pn.sum(-2) - 1).max() < 1e-5
+    Mn = to_np(M)
+    ref = O.sinkhorn(Mn, 20, 1e-8)
+    assert rel_err(Pn, ref) < 1e-5
+    # rows: the reference algorithm itself leaves some rows unconverged at 20
+    # iterations; row sums must match the oracle's, not 1
+    assert np.abs(Pn.sum(-1) - ref.sum(-1)).max() < 1e-5
+    sub = slice(0, 1 << 16)
+    gref = O.sinkhorn_backward(Mn[sub], to_np(dP)[sub], 20, 1e-8)
+    assert rel_err(to_np(Ml.grad)[sub], gref) < 1e-4
+
+
+def test_sinkhorn_edge_cases():
+    import mhc
+
+    empty = torch.empty(0, 4, 4, device=DEV)
+    assert mhc.sinkhorn_knopp(empty).shape == (0, 4, 4)
+    g = gen(2)
+    base = randn((65, 4, 4), g)
+    # unaligned view (offset of one element) takes the scalar path
+    flat = torch.cat([torch.zeros(1, device=DEV), base.reshape(-1)])
+    M = flat[1:].view(65, 4, 4)
+    assert M.data_ptr() % 16 != 0
+    P = mhc.sinkhorn_knopp(M)
+    assert rel_err(to_np(P), O.sinkhorn(to_np(base), 20, 1e-8)) < 1e-5
+    # non-contiguous input
+    Mt = base.transpose(1, 2)
+    P = mhc.sinkhorn_knopp(Mt)
+    assert rel_err(to_np(P), O.sinkhorn(to_np(Mt), 20, 1e-8)) < 1e-5
+    with pytest.raises(AssertionError):
+        mhc.sinkhorn_knopp(torch.zeros(3, 4, 5, device=DEV))
+
+
+# --------------------------------------------------------------------------- stream mix
+
+MIX_SHAPES = [(2, 64, 256), (3, 7, 100), (1, 5, 130), (2, 1, 8)]
+
+
+def _weights(B, g):
+    H_pre = torch.softmax(torch.randn((B, 4), generator=g), -1).to(DEV)
+    H_res = torch.tensor(O.sinkhorn(torch.randn((B, 4, 4), generator=g).numpy(), 20, 1e-8),
+                         dtype=torch.float32).to(DEV)
+    return H_pre, H_res
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("shape", MIX_SHAPES)
+def test_stream_mix_forward_backward(dtype, shape):
+    import mhc
+
+    B, S, D = shape
+    g = gen(3)
+    H = randn((B, S, 4, D), g, dtype)
+    H_pre, H_res = _weights(B, g)
+    d_bi = randn((B, S, D), g, dtype)
+    d_hr = randn((B, S, 4, D), g, dtype)
+    Hl, pl, rl = (t.clone().requires_grad_(True) for t in (H, H_pre, H_res))
+    bi, hr = mhc.fused_stream_mix(Hl, pl, rl)
+    assert bi.dtype == dtype and hr.dtype == dtype
+    torch.autograd.backward([bi, hr], [d_bi, d_hr])
+    obi, ohr = O.stream_mix(to_np(H), to_np(H_pre), to_np(H_res))
+    assert rel_err(to_np(bi), obi) < TOL[dtype]
+    assert rel_err(to_np(hr), ohr) < TOL[dtype]
+    dH, dpre, dres = O.stream_mix_backward(to_np(d_bi), to_np(d_hr), to_np(H), to_np(H_pre), to_np(H_res))
+    assert rel_err(to_np(Hl.grad), dH) < GTOL[dtype]
+    assert pl.grad.dtype == torch.float32 and rl.grad.dtype == torch.float32
+    assert rel_err(to_np(pl.grad), dpre) < 1e-4
+    assert rel_err(to_np(rl.grad), dres) < 1e-4
+
+
+# --------------------------------------------------------------------------- add residual
+
+@pytest.mark.parametrize("dtype,bo_dtype", [(torch.float32, torch.float32), (torch.bfloat16, torch.bfloat16),
+                                            (torch.float16, torch.float16), (torch.bfloat16, torch.float32),
+                                            (torch.float32, torch.bfloat16)])
+@pytest.mark.parametrize("shape", MIX_SHAPES)
+def test_add_residual_forward_backward(dtype, bo_dtype, shape):
+    import mhc
+
+    B, S, D = shape
+    g = gen(4)
+    hr = randn((B, S, 4, D), g, dtype)
+    bo = randn((B, S, D), g, bo_dtype)
+    H_post = torch.sigmoid(torch.randn((B, 4), generator=g)).to(DEV) * 2
+    dHn = randn((B, S, 4, D), g, dtype)
+    hl, bl, pl = (t.clone().requires_grad_(True) for t in (hr, bo, H_post))
+    Hn = mhc.fused_add_residual(hl, bl, pl)
+    assert Hn.dtype == dtype
+    Hn.backward(dHn)
+    tol = max(TOL[dtype], TOL[bo_dtype])
+    assert rel_err(to_np(Hn), O.add_residual(to_np(hr), to_np(bo), to_np(H_post))) < tol
+    _, dbo, dpost = O.add_residual_backward(to_np(dHn), to_np(bo), to_np(H_post))
+    assert torch.equal(hl.grad, dHn)
+    assert bl.grad.dtype == bo_dtype
+    assert rel_err(to_np(bl.grad), dbo) < max(GTOL[dtype], GTOL[bo_dtype])
+    assert rel_err(to_np(pl.grad), dpost) < 1e-4
+
+
+# --------------------------------------------------------------------------- dynamic weights
+
+@pytest.mark.parametrize("R,K,xdtype", [(4, 16384, torch.float32), (1, 28672, torch.float32),
+                                        (37, 1000, torch.float32), (4, 16384, torch.bfloat16),
+                                        (300, 2048, torch.float16)])
+def test_dynamic_weights_forward_backward(R, K, xdtype):
+    import mhc
+
+    g = gen(5)
+    # x as a sequence mean of unit normals (std ~ 1/64), phi ~ N(0, 0.02)
+    x = randn((R, K), g, xdtype, scale=1 / 64)
+    phi = randn((K, 24), g, scale=0.02)
+    bias = torch.cat([torch.tensor([1.0, 0, 0, 0]), torch.ones(4), torch.eye(4).flatten()]).to(DEV)
+    bias = bias + randn((24,), g, scale=0.1)
+    alphas = [torch.tensor([v], device=DEV) for v in (0.1, 0.2, 0.3)]
+    gp, gq, gr = randn((R, 4), g), randn((R, 4), g), randn((R, 4, 4), g)
+    leaves = [t.clone().requires_grad_(True) for t in (x, phi, bias, *alphas)]
+    H_pre, H_post, H_res = mhc.fused_dynamic_weights(*leaves, 20, 1e-6)
+    assert H_pre.dtype == H_post.dtype == H_res.dtype == torch.float32
+    torch.autograd.backward([H_pre, H_post, H_res], [gp, gq, gr])
+    args = [to_np(x), to_np(phi), to_np(bias)] + [a.item() for a in alphas]
+    oq, op, orr = O.dynamic_weights(*args, 20, 1e-6)
+    assert rel_err(to_np(H_pre), oq) < 1e-5
+    assert rel_err(to_np(H_post), op) < 1e-5
+    assert rel_err(to_np(H_res), orr) < 1e-5
+    gx, gphi, gbias, ga = O.dynamic_weights_backward(*args, to_np(gp), to_np(gq), to_np(gr), 20, 1e-6)
+    assert leaves[0].grad.dtype == xdtype
+    assert rel_err(to_np(leaves[0].grad), gx) < GTOL[xdtype]
+    assert rel_err(to_np(leaves[1].grad), gphi) < 1e-4
+    assert rel_err(to_np(leaves[2].grad), gbias) < 1e-4
+    assert rel_err(np.array([a.grad.item() for a in leaves[3:]]), np.array(ga)) < 1e-4
+
+
+def test_dynamic_weights_default_init_sgn_zero():
+    """phi = 0 with the module's default bias: scaled_res has 12 exact zeros,
+    whose gradient follows torch (sgn(0) = 0)."""
+    import mhc
+
+    R, K = 4, 2048
+    g = gen(6)
+    x = randn((R, K), g, scale=1 / 64)
+    phi = torch.zeros(K, 24, device=DEV)
+    bias = torch.cat([torch.tensor([1.0, 0, 0, 0]), torch.ones(4), torch.eye(4).flatten()]).to(DEV)
+    alphas = [torch.tensor([0.1], device=DEV) for _ in range(3)]
+    leaves = [t.clone().requires_grad_(True) for t in (x, phi, bias, *alphas)]
+    outs = mhc.fused_dynamic_weights(*leaves)
+    gs = [randn(o.shape, g) for o in outs]
+    torch.autograd.backward(list(outs), gs)
+    args = [to_np(x), to_np(phi), to_np(bias)] + [0.1, 0.1, 0.1]
+    gx, gphi, gbias, ga = O.dynamic_weights_backward(*args, *[to_np(t) for t in gs], 20, 1e-6)
+    assert torch.count_nonzero(leaves[0].grad).item() == 0  # grad_x == 0 exactly
+    assert rel_err(to_np(leaves[1].grad), gphi) < 1e-4
+    assert rel_err(to_np(leaves[2].grad), gbias) < 1e-4
+    zero_res = (np.eye(4).reshape(16) == 0)
+    assert np.all(to_np(leaves[2].grad)[8:24][zero_res] == 0.0)
+
+
+def test_mean_pool_matches_oracle():
+    from mhc._kernels import mean_pool
+
+    g = gen(7)
+    for dtype, shape in [(torch.float32, (2, 128, 4, 512)), (torch.bfloat16, (3, 77, 4, 100)),
+                         (torch.float16, (1, 300, 4, 64))]:
+        H = randn(shape, g, dtype)
+        x = mean_pool(H)
+        assert x.dtype == torch.float32
+        assert rel_err(to_np(x), O.mean_pool(to_np(H))) < 1e-5

@@ -1,0 +1,352 @@
+"""Pins the CPU oracle (oracle/mhc_oracle.py) before anything is checked against it.
+
+Each function is pinned by something other than its own formula:
+closed forms and known answers, invariants the mathematics fixes,
+an independent algorithm (Sinkhorn scaling vectors), central finite
+differences in float64, and torch autograd of the independent torch
+restatement in oracle/torch_path.py.  Each check is chosen so that a plausible
+slip (eps in the wrong place, sum instead of mean in the RMS, swapped groups,
+a missing x2, a transposed H_res, sgn(0) = +1) fails it.
+"""
+
+import numpy as np
+import pytest
+import torch
+
+from helpers import rel_err
+from oracle import mhc_oracle as O
+from oracle import torch_path as TP
+
+RNG = np.random.default_rng(1234)
+
+
+def _fd(f, x, h=1e-6):
+    """Central finite-difference gradient of scalar f at x (float64)."""
+    g = np.zeros_like(x)
+    it = np.nditer(x, flags=["multi_index"])
+    for _ in it:
+        i = it.multi_index
+        old = x[i]
+        x[i] = old + h
+        fp = f(x)
+        x[i] = old - h
+        fm = f(x)
+        x[i] = old
+        g[i] = (fp - fm) / (2 * h)
+    return g
+
+
+# --------------------------------------------------------------------------- Sinkhorn forward
+
+def test_sinkhorn_rank_one_gives_uniform():
+    u = RNG.uniform(0.1, 3, size=(8, 4, 1))
+    v = RNG.uniform(0.1, 3, size=(8, 1, 4))
+    P = O.sinkhorn(u * v, iters=1, eps=0.0)
+    assert np.abs(P - 0.25).max() < 1e-15
+    P = O.sinkhorn(u * v, iters=1, eps=1e-8)
+    assert np.abs(P - 0.25).max() < 1e-7
+
+
+@pytest.mark.parametrize("eps", [1e-2, 1e-8])
+def test_sinkhorn_all_equal_closed_form(eps):
+    # M = c J: every entry follows a -> a/(4a + eps) twice per round, starting at |c| + eps.
+    c = -1.7
+    iters = 5
+    a = abs(c) + eps
+    for _ in range(iters):
+        a = a / (4 * a + eps)
+        a = a / (4 * a + eps)
+    P = O.sinkhorn(np.full((1, 4, 4), c), iters, eps)
+    assert np.abs(P - a).max() < 1e-15
+
+
+def test_sinkhorn_doubly_stochastic_fixed_point():
+    I = np.eye(4)
+    perm = np.roll(I, 1, axis=1)
+    A = 0.5 * I + 0.3 * perm + 0.2 * (perm @ perm)
+    P = O.sinkhorn(A[None], iters=7, eps=0.0)
+    assert np.abs(P[0] - A).max() < 1e-15
+
+
+def test_sinkhorn_permutation_equivariance():
+    M = RNG.standard_normal((16, 4, 4))
+    p, q = RNG.permutation(4), RNG.permutation(4)
+    P1 = O.sinkhorn(M[:, p][:, :, q], 20, 1e-3)
+    P2 = O.sinkhorn(M, 20, 1e-3)[:, p][:, :, q]
+    assert np.abs(P1 - P2).max() < 1e-13
+
+
+def test_sinkhorn_matches_scaling_vector_algorithm():
+    # Classic Sinkhorn on the scaling vectors: r = 1/(A c), c = 1/(A^T r);
+    # after t rounds the normalised matrix is diag(r) A diag(c) (eps = 0).
+    A = np.abs(RNG.standard_normal((32, 4, 4))) + 0.05
+    iters = 9
+    r = np.ones((32, 4))
+    c = np.ones((32, 4))
+    for _ in range(iters):
+        r = 1.0 / np.einsum("bij,bj->bi", A, c)
+        c = 1.0 / np.einsum("bij,bi->bj", A, r)
+    ref = r[:, :, None] * A * c[:, None, :]
+    assert rel_err(O.sinkhorn(A, iters, 0.0), ref) < 1e-12
+
+
+def test_sinkhorn_columns_exact_rows_not_always_converged():
+    M = np.exp(RNG.standard_normal((1 << 15, 4, 4)))
+    P = O.sinkhorn(M, 20, 1e-8)
+    # the last step normalises columns: column sums are (s / (s + eps)) ~ 1
+    assert np.abs(P.sum(-2) - 1).max() < 1e-7
+    # rows are not: a fraction of log-normal matrices is still off by > 1e-5
+    frac = float((np.abs(P.sum(-1) - 1).max(-1) > 1e-5).mean())
+    assert 0.0 < frac < 0.05
+
+
+# --------------------------------------------------------------------------- Sinkhorn backward
+
+def test_sinkhorn_backward_finite_differences():
+    M = RNG.standard_normal((3, 4, 4))
+    M += np.sign(M) * 0.05  # keep away from the |.| kink
+    dP = RNG.standard_normal((3, 4, 4))
+    g = O.sinkhorn_backward(M, dP, 6, 1e-3)
+    fd = _fd(lambda m: float((O.sinkhorn(m, 6, 1e-3) * dP).sum()), M.copy())
+    assert rel_err(g, fd) < 1e-7
+
+
+def test_sinkhorn_backward_matches_torch_autograd_including_zeros():
+    M = RNG.standard_normal((64, 4, 4))
+    M[0, 1, 2] = 0.0
+    M[5, 3, 3] = 0.0
+    dP = RNG.standard_normal((64, 4, 4))
+    Mt = torch.tensor(M, requires_grad=True)
+    TP.sinkhorn(Mt, 20, 1e-8).backward(torch.tensor(dP))
+    g = O.sinkhorn_backward(M, dP, 20, 1e-8)
+    assert rel_err(g, Mt.grad.numpy()) < 1e-10
+    # sgn(0) = 0, as torch's abs backward
+    assert g[0, 1, 2] == 0.0 and g[5, 3, 3] == 0.0
+
+
+# --------------------------------------------------------------------------- dynamic weights
+
+def _sig(z):
+    return 1.0 / (1.0 + np.exp(-z))
+
+
+def test_dynamic_weights_phi_zero_known_answer():
+    R, K = 3, 64
+    x = RNG.standard_normal((R, K))
+    bias = RNG.standard_normal(24)
+    eps = 1e-6
+    H_pre, H_post, H_res = O.dynamic_weights(x, np.zeros((K, 24)), bias, 0.3, 0.4, 0.5, 20, eps)
+    sp = _sig(bias[0:4])
+    assert np.abs(H_pre - sp / (sp.sum() + eps)).max() < 1e-15
+    assert np.abs(H_post - 2 * _sig(bias[4:8])).max() < 1e-15
+    assert np.abs(H_res - O.sinkhorn(bias[8:24].reshape(1, 4, 4), 20, eps)).max() < 1e-15
+
+
+def test_dynamic_weights_constant_x_known_answer():
+    # x = c * ones(K), phi[:, j] = (j + 1) / K  =>  raw_j = c (j + 1),
+    # rms = sqrt(mean(x^2) + eps) = sqrt(c^2 + eps) (a mean, not a sum, over K).
+    R, K, c, eps = 2, 32, 2.5, 1e-6
+    x = np.full((R, K), c)
+    phi = np.tile((np.arange(24) + 1.0) / K, (K, 1))
+    bias = np.linspace(-1, 1, 24)
+    alphas = (0.3, 0.7, 1.1)
+    H_pre, H_post, H_res = O.dynamic_weights(x, phi, bias, *alphas, iters=3, eps=eps)
+    inv = 1.0 / np.sqrt(c * c + eps)
+    s = np.array([alphas[0 if j < 4 else (1 if j < 8 else 2)] * inv * c * (j + 1) + bias[j] for j in range(24)])
+    sp = _sig(s[0:4])
+    assert np.abs(H_pre[0] - sp / (sp.sum() + eps)).max() < 1e-14
+    assert np.abs(H_post[1] - 2 * _sig(s[4:8])).max() < 1e-14
+    assert np.abs(H_res[0] - O.sinkhorn(s[8:24].reshape(4, 4), 3, eps)).max() < 1e-14
+
+
+def _dyn_inputs(R=3, K=16):
+    x = RNG.standard_normal((R, K))
+    phi = 0.3 * RNG.standard_normal((K, 24))
+    bias = RNG.standard_normal(24)
+    return x, phi, bias, (0.7, -0.4, 1.3)
+
+
+def test_dynamic_weights_backward_finite_differences():
+    x, phi, bias, al = _dyn_inputs()
+    R = x.shape[0]
+    gp, gq, gr = RNG.standard_normal((R, 4)), RNG.standard_normal((R, 4)), RNG.standard_normal((R, 4, 4))
+    iters, eps = 5, 1e-3
+
+    def loss(x_, phi_, bias_, a_):
+        hp, hq, hr = O.dynamic_weights(x_, phi_, bias_, *a_, iters=iters, eps=eps)
+        return float((hp * gp).sum() + (hq * gq).sum() + (hr * gr).sum())
+
+    gx, gphi, gbias, ga = O.dynamic_weights_backward(x, phi, bias, *al, gp, gq, gr, iters, eps)
+    assert rel_err(gx, _fd(lambda v: loss(v, phi, bias, al), x.copy())) < 1e-6
+    assert rel_err(gphi, _fd(lambda v: loss(x, v, bias, al), phi.copy())) < 1e-6
+    assert rel_err(gbias, _fd(lambda v: loss(x, phi, v, al), bias.copy())) < 1e-6
+    ga_fd = _fd(lambda v: loss(x, phi, bias, tuple(v)), np.array(al, dtype=np.float64))
+    assert rel_err(np.array(ga), ga_fd) < 1e-6
+
+
+def test_dynamic_weights_backward_matches_torch_autograd():
+    x, phi, bias, al = _dyn_inputs(R=5, K=40)
+    R = x.shape[0]
+    gp, gq, gr = RNG.standard_normal((R, 4)), RNG.standard_normal((R, 4)), RNG.standard_normal((R, 4, 4))
+    t = [torch.tensor(v, requires_grad=True) for v in (x, phi, bias)]
+    ta = [torch.tensor([a], dtype=torch.float64, requires_grad=True) for a in al]
+    outs = TP.dynamic_weights(*t, *ta, iters=20, eps=1e-6)
+    torch.autograd.backward(list(outs), [torch.tensor(gp), torch.tensor(gq), torch.tensor(gr)])
+    gx, gphi, gbias, ga = O.dynamic_weights_backward(x, phi, bias, *al, gp, gq, gr, 20, 1e-6)
+    assert rel_err(gx, t[0].grad.numpy()) < 1e-10
+    assert rel_err(gphi, t[1].grad.numpy()) < 1e-10
+    assert rel_err(gbias, t[2].grad.numpy()) < 1e-10
+    assert rel_err(np.array(ga), np.array([a.grad.item() for a in ta])) < 1e-10
+
+
+def test_dynamic_weights_backward_default_init_zeros():
+    # phi = 0: raw = 0, so the alpha and x gradients vanish exactly.
+    R, K = 4, 32
+    x = RNG.standard_normal((R, K))
+    bias = np.concatenate([[1, 0, 0, 0], np.ones(4), np.eye(4).reshape(16)])
+    g = [RNG.standard_normal((R, 4)), RNG.standard_normal((R, 4)), RNG.standard_normal((R, 4, 4))]
+    gx, gphi, gbias, ga = O.dynamic_weights_backward(x, np.zeros((K, 24)), bias, .1, .1, .1, *g, 20, 1e-6)
+    assert np.all(gx == 0) and all(v == 0 for v in ga)
+    assert np.abs(gphi).max() > 0
+
+
+# --------------------------------------------------------------------------- stream mix / add residual
+
+def _mix_inputs(B=2, S=5, D=6):
+    H = RNG.standard_normal((B, S, 4, D))
+    H_pre = RNG.uniform(0, 1, (B, 4))
+    H_res = RNG.uniform(0, 1, (B, 4, 4))
+    return H, H_pre, H_res
+
+
+def test_stream_mix_identities():
+    H, H_pre, H_res = _mix_inputs()
+    B = H.shape[0]
+    bi, hr = O.stream_mix(H, np.tile(np.eye(4)[2], (B, 1)), np.tile(np.eye(4), (B, 1, 1)))
+    assert np.array_equal(bi, H[:, :, 2]) and np.array_equal(hr, H)
+    perm = np.eye(4)[[3, 0, 2, 1]]  # row n selects stream perm_idx[n]
+    _, hr = O.stream_mix(H, H_pre, np.tile(perm, (B, 1, 1)))
+    assert np.array_equal(hr, H[:, :, [3, 0, 2, 1]])
+
+
+def test_stream_mix_backward_adjoint():
+    H, H_pre, H_res = _mix_inputs()
+    d_bi = RNG.standard_normal(H.shape[:2] + H.shape[3:])
+    d_hr = RNG.standard_normal(H.shape)
+    dH, dpre, dres = O.stream_mix_backward(d_bi, d_hr, H, H_pre, H_res)
+    # linear in H:  <d_bi, bi(X)> + <d_hr, hr(X)> = <dH, X>
+    X = RNG.standard_normal(H.shape)
+    bi, hr = O.stream_mix(X, H_pre, H_res)
+    assert abs((d_bi * bi).sum() + (d_hr * hr).sum() - (dH * X).sum()) < 1e-10
+    # linear in the weights
+    dq, dr = RNG.standard_normal(H_pre.shape), RNG.standard_normal(H_res.shape)
+    bi, hr = O.stream_mix(H, dq, dr)
+    assert abs((d_bi * bi).sum() - (dpre * dq).sum()) < 1e-10
+    assert abs((d_hr * hr).sum() - (dres * dr).sum()) < 1e-10
+
+
+def test_add_residual_identity_and_backward_adjoint():
+    H, _, _ = _mix_inputs()
+    B, S, _, D = H.shape
+    bo = RNG.standard_normal((B, S, D))
+    H_post = RNG.uniform(0, 2, (B, 4))
+    assert np.array_equal(O.add_residual(H, bo, np.zeros((B, 4))), H)
+    out = O.add_residual(np.zeros_like(H), bo, np.ones((B, 4)))
+    assert np.array_equal(out, np.repeat(bo[:, :, None, :], 4, axis=2))
+    dHn = RNG.standard_normal(H.shape)
+    dHr, dbo, dpost = O.add_residual_backward(dHn, bo, H_post)
+    assert dHr is not None and np.array_equal(dHr, dHn)
+    X = RNG.standard_normal(bo.shape)
+    assert abs((dHn * O.add_residual(np.zeros_like(H), X, H_post)).sum() - (dbo * X).sum()) < 1e-10
+    Y = RNG.standard_normal(H_post.shape)
+    assert abs((dHn * O.add_residual(np.zeros_like(H), bo, Y)).sum() - (dpost * Y).sum()) < 1e-10
+
+
+# --------------------------------------------------------------------------- whole layer
+
+def _layer_params(dynamic, fused, D, rng, zero_phi=False):
+    p = {
+        "H_pre_base": rng.standard_normal(4),
+        "H_post_base": rng.standard_normal(4),
+        "H_res_base": rng.standard_normal((4, 4)),
+    }
+    if dynamic and fused:
+        p["phi"] = np.zeros((4 * D, 24)) if zero_phi else 0.2 * rng.standard_normal((4 * D, 24))
+        for k in ("alpha_pre", "alpha_post", "alpha_res"):
+            p[k] = np.array([rng.uniform(0.05, 0.5)])
+    elif dynamic:
+        for k in ("W_pre", "W_post", "W_res"):
+            p[k] = 0.2 * rng.standard_normal(((16 if k == "W_res" else 4), 4 * D))
+        for k in ("scale_pre", "scale_post", "scale_res"):
+            p[k] = np.array([rng.uniform(0.05, 0.5)])
+    return p
+
+
+def _torch_params(p):
+    out = {}
+    for k, v in p.items():
+        out[k + ".weight" if k.startswith("W_") else k] = torch.tensor(v)
+    return out
+
+
+@pytest.mark.parametrize("dynamic,fused", [(True, True), (True, False), (False, True)])
+def test_layer_matches_torch_autograd(dynamic, fused):
+    B, S, D = 2, 5, 6
+    p = _layer_params(dynamic, fused, D, RNG)
+    H = RNG.standard_normal((B, S, 4, D))
+    bo = RNG.standard_normal((B, S, D))
+    dHn = RNG.standard_normal((B, S, 4, D))
+    dbi = RNG.standard_normal((B, S, D))
+    bi, Hn, cache = O.layer_forward(p, H, bo, dynamic, fused, iters=20, eps=1e-6)
+    g = O.layer_backward(p, cache, dHn, dbi)
+    tbi, tHn, tg = TP.layer_grads(_torch_params(p), torch.tensor(H), torch.tensor(bo), torch.tensor(dHn),
+                                  torch.tensor(dbi), dynamic, fused, 20, 1e-6, torch.float64)
+    assert rel_err(bi, tbi.numpy()) < 1e-12
+    assert rel_err(Hn, tHn.numpy()) < 1e-12
+    for k, v in tg.items():
+        key = k if k in g else k.replace(".weight", "")
+        assert rel_err(np.asarray(g[key]).reshape(v.shape), v.numpy()) < 1e-9, k
+
+
+def test_layer_backward_finite_differences_dynamic():
+    B, S, D = 2, 3, 2
+    p = _layer_params(True, True, D, RNG)
+    H = RNG.standard_normal((B, S, 4, D))
+    bo = RNG.standard_normal((B, S, D))
+    dHn = RNG.standard_normal((B, S, 4, D))
+    dbi = RNG.standard_normal((B, S, D))
+
+    def loss(pp, HH):
+        bi, Hn, _ = O.layer_forward(pp, HH, bo, True, True, iters=4, eps=1e-6)
+        return float((bi * dbi).sum() + (Hn * dHn).sum())
+
+    _, _, cache = O.layer_forward(p, H, bo, True, True, iters=4, eps=1e-6)
+    g = O.layer_backward(p, cache, dHn, dbi)
+    assert rel_err(g["H"], _fd(lambda v: loss(p, v), H.copy())) < 1e-6
+    for k in ("phi", "H_pre_base", "H_post_base", "H_res_base", "alpha_pre", "alpha_post", "alpha_res"):
+        def f(v, k=k):
+            q = dict(p)
+            q[k] = v
+            return loss(q, H)
+        assert rel_err(np.asarray(g[k]).reshape(p[k].shape), _fd(f, p[k].astype(np.float64).copy())) < 1e-6, k
+
+
+# --------------------------------------------------------------------------- product torch baselines
+
+def test_product_torch_baselines_match_oracle():
+    import mhc
+
+    B, S, D = 2, 4, 8
+    for dynamic, fused in [(True, True), (True, False), (False, True)]:
+        hc = mhc.HyperConnectionTorch(D, dynamic=dynamic, use_fused_weights=fused).double()
+        p = _layer_params(dynamic, fused, D, RNG)
+        with torch.no_grad():
+            for name, prm in hc.named_parameters():
+                prm.copy_(torch.tensor(p[name.replace(".weight", "")]).reshape(prm.shape))
+        H = RNG.standard_normal((B, S, 4, D))
+        bo = RNG.standard_normal((B, S, D))
+        bi, add = hc(torch.tensor(H))
+        Hn = add(torch.tensor(bo))
+        obi, oHn, _ = O.layer_forward(p, H, bo, dynamic, fused)
+        assert rel_err(bi.detach().numpy(), obi) < 1e-12
+        assert rel_err(Hn.detach().numpy(), oHn) < 1e-12
