@@ -1,0 +1,301 @@
+#!/usr/bin/env python3
+"""mHC layer forward+backward throughput on one MI355X.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload config3]
+
+One "step" is the HyperConnection layer's forward and backward over one
+synthetic batch, exactly as a transformer block uses it:
+
+    bi, add = hc(H); H_new = add(bo)
+    torch.autograd.backward([H_new, bi], [dH_new, d_bi])
+
+with ``H`` and ``bo`` leaves (so dH and d_bo are produced) and every parameter
+gradient computed.  Gradients are reset to None before each step, as an
+optimizer's ``zero_grad(set_to_none=True)`` would, so no step pays for gradient
+accumulation.  Inputs are resident in HBM before the timed region.
+
+Printed: one JSON line (metric, value = tokens/s of the whole job, roofline of
+the dominant kernel measured with HIP events on the stream it runs on, the CPU
+baseline of the reference's PyTorch path timed on this host).
+
+Workloads (reference benchmark shapes, src/mhc/module.py layer):
+  config3  dim 4096 bf16, B=4 S=4096, dynamic fused weights (the headline)
+  config4  dim 7168 bf16, B=1 S=8192, dynamic fused weights
+  config5  dim 2048 fp16, B=16 S=2048, static weights
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+for _p in (os.path.join(ROOT, "mhc-triton_amd"), ROOT):
+    if _p not in sys.path:
+        sys.path.insert(0, _p)
+
+METRIC = "mHC layer fwd+bwd tokens/sec at dim 4096 bf16; achieved HBM GB/s vs roofline"
+HBM_PEAK_GBS = 8000.0  # MI355X HBM3E, GB/s
+
+WORKLOADS = {
+    "config3": dict(B=4, S=4096, D=4096, dtype="bf16", dynamic=True),
+    "config4": dict(B=1, S=8192, D=7168, dtype="bf16", dynamic=True),
+    "config5": dict(B=16, S=2048, D=2048, dtype="fp16", dynamic=False),
+}
+
+# Algorithmic HBM bytes per token, in units of D * e (e = element size of H):
+# the dependency-forced minimum of the layer behind this API.
+#   dynamic forward 18: mean-pool reads H (4); branch_input reads H (4), writes
+#       bi (1); H_new reads H (4) and bo (1), writes H_new (4)
+#   dynamic backward 24: closure backward reads dH_new (4) and bo (1), writes
+#       d_bo (1); weight-gradient pass reads d_bi (1), dH_new (4), H (4);
+#       dH pass reads d_bi (1), dH_new (4), writes dH (4)
+#   static: no mean-pool (14 forward) and one backward pass for the weight
+#       gradients and dH (19).
+ALGO_UNITS = {True: (18, 24), False: (14, 19)}
+
+
+def _log(msg: str) -> None:
+    print(msg, file=sys.stderr, flush=True)
+
+
+def _parse():
+    ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--workload", default="config3", choices=sorted(WORKLOADS))
+    ap.add_argument("--cpu-seconds", type=float, default=12.0,
+                    help="target CPU time of the cpu_baseline sample (0 disables it)")
+    return ap.parse_args()
+
+
+def _build_inputs(cfg, dev):
+    import torch
+
+    import mhc
+
+    B, S, D = cfg["B"], cfg["S"], cfg["D"]
+    dt = {"bf16": torch.bfloat16, "fp16": torch.float16, "fp32": torch.float32}[cfg["dtype"]]
+    g = torch.Generator(device=dev)
+    g.manual_seed(0)
+    hc = mhc.HyperConnection(D, dynamic=cfg["dynamic"]).to(dev)
+    H = torch.randn((B, S, 4, D), generator=g, device=dev, dtype=torch.float32).to(dt)
+    with torch.no_grad():
+        if cfg["dynamic"]:
+            hc.phi.copy_(torch.randn((24, 4 * D), generator=g, device=dev).T * 0.02)
+        else:
+            hc.H_res_base.copy_(torch.randn((4, 4), generator=g, device=dev))
+    bo = torch.randn((B, S, D), generator=g, device=dev, dtype=torch.float32).to(dt)
+    dH_new = torch.randn((B, S, 4, D), generator=g, device=dev, dtype=torch.float32).to(dt)
+    d_bi = torch.randn((B, S, D), generator=g, device=dev, dtype=torch.float32).to(dt)
+    H.requires_grad_(True)
+    bo.requires_grad_(True)
+    return hc, H, bo, dH_new, d_bi
+
+
+def _gpu_leg(cfg, steps, warmup):
+    import torch
+
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    hc, H, bo, dH_new, d_bi = _build_inputs(cfg, dev)
+    params = list(hc.parameters())
+    stream = torch.cuda.current_stream(dev)
+
+    def step(ev=None):
+        H.grad = None
+        bo.grad = None
+        for p in params:
+            p.grad = None
+        bi, add = hc(H)
+        if ev is not None:
+            ev[0].record(stream)
+        H_new = add(bo)  # one kernel: H_new = H_res @ H + H_post * bo
+        if ev is not None:
+            ev[1].record(stream)
+        torch.autograd.backward([H_new, bi], [dH_new, d_bi])
+
+    for _ in range(warmup):
+        step()
+    torch.cuda.synchronize()
+
+    # Forward-only rate (no autograd graph), same inputs.
+    with torch.no_grad():
+        for _ in range(3):
+            bi, add = hc(H)
+            add(bo)
+        torch.cuda.synchronize()
+        f0 = torch.cuda.Event(enable_timing=True)
+        f1 = torch.cuda.Event(enable_timing=True)
+        f0.record(stream)
+        for _ in range(steps):
+            bi, add = hc(H)
+            add(bo)
+        f1.record(stream)
+        torch.cuda.synchronize()
+    fwd_ms = f0.elapsed_time(f1) / steps
+    del bi, add
+
+    kev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(steps)]
+    t0 = torch.cuda.Event(enable_timing=True)
+    t1 = torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    wall0 = time.perf_counter()
+    t0.record(stream)
+    for i in range(steps):
+        step(kev[i])
+    t1.record(stream)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - wall0
+    ms = t0.elapsed_time(t1) / steps
+    add_ms = sum(a.elapsed_time(b) for a, b in kev) / steps
+    return dict(ms=ms, wall_ms=wall * 1e3 / steps, fwd_ms=fwd_ms, add_ms=add_ms,
+                elem=H.element_size(), device=torch.cuda.get_device_name(dev))
+
+
+def _cpu_leg(cfg, target_s):
+    """The reference's pure-PyTorch layer (restated in oracle/torch_path.py),
+    forward + autograd backward on the host cores, fp32-upcast (the reference's
+    own torch path raises on bf16 H with fp32 weights), on a bounded sample of
+    the workload: the same dim, batch rows of a shorter sequence."""
+    import torch
+
+    from oracle import torch_path
+
+    B, D = cfg["B"], cfg["D"]
+    S = 64
+    g = torch.Generator()
+    g.manual_seed(0)
+    p = {
+        "H_pre_base": torch.nn.functional.one_hot(torch.tensor(0), 4).float(),
+        "H_post_base": torch.ones(4),
+        "H_res_base": torch.eye(4) if cfg["dynamic"] else torch.randn((4, 4), generator=g),
+    }
+    if cfg["dynamic"]:
+        p["phi"] = torch.randn((24, 4 * D), generator=g).T.contiguous() * 0.02
+        for k in ("alpha_pre", "alpha_post", "alpha_res"):
+            p[k] = torch.tensor([0.1])
+    H = torch.randn((B, S, 4, D), generator=g)
+    bo = torch.randn((B, S, D), generator=g)
+    dHn = torch.randn((B, S, 4, D), generator=g)
+    dbi = torch.randn((B, S, D), generator=g)
+
+    def once():
+        torch_path.layer_grads(p, H, bo, dHn, dbi, dynamic=cfg["dynamic"], fused=True)
+
+    once()  # warm-up
+    n, t = 0, time.perf_counter()
+    while n < 3 or time.perf_counter() - t < 1.0:
+        once()
+        n += 1
+    one = (time.perf_counter() - t) / n
+    reps = max(1, int(target_s / max(one, 1e-6)))
+    t = time.perf_counter()
+    for _ in range(reps):
+        once()
+    el = time.perf_counter() - t
+    tokens = B * S * reps
+    return {
+        "value": round(tokens / el, 1),
+        "unit": "tokens/s",
+        "cores": torch.get_num_threads(),
+        "kind": "port",
+        "sample": (f"torch CPU fp32 restatement of the reference's pure-PyTorch layer fwd+bwd, "
+                   f"B={B} S={S} D={D} ({'dynamic' if cfg['dynamic'] else 'static'}), "
+                   f"{reps} reps in {el:.1f} s"),
+    }
+
+
+def main() -> int:
+    args = _parse()
+    world = int(os.environ.get("WORLD_SIZE", "1"))
+    if args.gpus != 1 or world != 1:
+        print(f"bench.py: this build measures one GPU only (asked for --gpus {args.gpus}, WORLD_SIZE={world}); "
+              "the mHC layer path has no multi-GPU leg here", file=sys.stderr, flush=True)
+        return 2
+    if args.steps < 1 or args.warmup < 0:
+        print("bench.py: --steps must be >= 1 and --warmup >= 0", file=sys.stderr)
+        return 2
+
+    import torch
+
+    if not torch.cuda.is_available():
+        print("bench.py: no ROCm GPU visible", file=sys.stderr)
+        return 1
+    from mhc import _lib
+
+    _lib.load()  # fails loudly when the HIP library is not built
+
+    cfg = WORKLOADS[args.workload]
+    B, S, D = cfg["B"], cfg["S"], cfg["D"]
+    T = B * S
+    _log(f"bench: {args.workload} B={B} S={S} D={D} {cfg['dtype']} warmup={args.warmup} steps={args.steps}")
+    r = _gpu_leg(cfg, args.steps, args.warmup)
+    e = r["elem"]
+    fu, bu = ALGO_UNITS[cfg["dynamic"]]
+    step_bytes = (fu + bu) * D * e * T
+    fwd_bytes = fu * D * e * T
+    add_bytes = 9 * D * e * T  # H_new kernel: reads H (4) + bo (1), writes H_new (4)
+    _log(f"bench: gpu {r['ms']:.4f} ms/step (wall {r['wall_ms']:.4f}), fwd {r['fwd_ms']:.4f} ms, "
+         f"H_new kernel {r['add_ms'] * 1e3:.1f} us")
+
+    cpu = None
+    if args.cpu_seconds > 0:
+        _log("bench: cpu baseline ...")
+        cpu = _cpu_leg(cfg, args.cpu_seconds)
+        _log(f"bench: cpu {cpu['value']} tokens/s on {cpu['cores']} threads")
+
+    add_gbs = add_bytes / (r["add_ms"] * 1e-3) / 1e9
+    step_gbs = step_bytes / (r["ms"] * 1e-3) / 1e9
+    out = {
+        "metric": METRIC,
+        "value": round(T / (r["ms"] * 1e-3), 1),
+        "unit": "tokens/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(r["ms"], 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": cfg["dtype"],
+        "data": "synthetic (N(0,1) inputs, phi ~ N(0, 0.02), seed 0; generated on the GPU)",
+        "config": {
+            "workload": f"{args.workload}: HyperConnection layer fwd+bwd, dim={D}, num_streams=4, "
+                        f"{'dynamic fused' if cfg['dynamic'] else 'static'} weights, sinkhorn_iters=20",
+            "B": B, "S": S, "D": D, "tokens_per_step": T, "parallelism": "single GPU",
+        },
+        "roofline": {
+            "bound": "hbm",
+            "kernel": "H_new = H_res @ H + H_post * bo (mix_fwd_kernel, closure forward)",
+            "achieved": round(add_gbs, 1),
+            "peak": HBM_PEAK_GBS,
+            "unit": "GB/s",
+            "frac": round(add_gbs / HBM_PEAK_GBS, 4),
+            "traffic": None,
+        },
+        "layer_roofline": {
+            "algorithmic_bytes_per_step": step_bytes,
+            "achieved_GBps": round(step_gbs, 1),
+            "frac": round(step_gbs / HBM_PEAK_GBS, 4),
+        },
+        "fwd_only": {
+            "ms_per_step": round(r["fwd_ms"], 5),
+            "tokens_per_s": round(T / (r["fwd_ms"] * 1e-3), 1),
+            "frac": round(fwd_bytes / (r["fwd_ms"] * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+        },
+        "wall_ms_per_step": round(r["wall_ms"], 5),
+        "compute_dtype": "fp32 arithmetic on bf16/fp16 storage",
+        "device": r["device"],
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(out), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

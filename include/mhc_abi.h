@@ -166,7 +166,7 @@ int mhc_dynamic_weights_backward(const void* x, int dtype_x, const float* phi, c
                                  mhc_stream_t stream);
 
 /* ------------------------------------------------------------------------
- * HyperConnection layer path (reference src/mhc/module.py:141-220).
+ * HyperConnection layer path (reference src/mhc/module.py:103-182).
  *
  * The module's forward H.mean(1) -> fused_dynamic_weights -> fused_stream_mix
  * and its closure fused_add_residual are regrouped so that H_residual is never
@@ -177,12 +177,12 @@ int mhc_dynamic_weights_backward(const void* x, int dtype_x, const float* phi, c
 
 size_t mhc_layer_workspace_bytes(int64_t B, int64_t S, int64_t D, int dtype);
 
-/* Mean over the sequence, module.py:161 (H.mean(dim=1).reshape(B, 4D)),
+/* Mean over the sequence, module.py:123 (H.mean(dim=1).reshape(B, 4D)),
  * accumulated and returned in f32: x [B, 4D]. */
 int mhc_mean_pool(const void* H, int dtype, float* x, int64_t B, int64_t S, int64_t D,
                   void* workspace, size_t workspace_bytes, mhc_stream_t stream);
 
-/* Dynamic layer forward (module.py:157-177 + 214-215): mean-pool, Eq. 14-19
+/* Dynamic layer forward (module.py:119-139 + 177): mean-pool, Eq. 14-19
  * with bias = [H_pre_base, H_post_base, H_res_base], then branch_input.
  * Outputs: branch_input [B,S,D] (dtype), x [B,4D] f32, w [B,24] f32,
  * aux [B,25] f32. */
@@ -194,7 +194,7 @@ int mhc_layer_dynamic_forward(const void* H, int dtype, const float* phi,
                               int64_t B, int64_t S, int64_t D, int iters, float eps,
                               void* workspace, size_t workspace_bytes, mhc_stream_t stream);
 
-/* Static layer forward (module.py:146-155 + 214-215): w from the base
+/* Static layer forward (module.py:108-117 + 177): w from the base
  * parameters (H_post = sigmoid, H_pre = sigmoid/(sum+1e-8), H_res = Sinkhorn
  * with eps 1e-8), then branch_input. */
 int mhc_layer_static_forward(const void* H, int dtype, const float* H_pre_base,
@@ -204,8 +204,8 @@ int mhc_layer_static_forward(const void* H, int dtype, const float* H_pre_base,
                              mhc_stream_t stream);
 
 /* branch_input[b,s,:] = sum_n w[b,n] H[b,s,n,:] from packed weights w [B,24]
- * (module.py:215 for weights computed outside the library, the unfused
- * dynamic path module.py:179-201). */
+ * (module.py:177 for weights computed outside the library, the unfused
+ * dynamic path module.py:141-163). */
 int mhc_layer_branch_input(const void* H, int dtype, const float* w, void* branch_input,
                            int64_t B, int64_t S, int64_t D, mhc_stream_t stream);
 
@@ -217,7 +217,7 @@ int mhc_layer_mix_backward(const void* H, int dtype, const void* d_branch_input,
                            int64_t B, int64_t S, int64_t D,
                            void* workspace, size_t workspace_bytes, mhc_stream_t stream);
 
-/* Layer closure forward (module.py:217-218 with H_residual recomputed):
+/* Layer closure forward (module.py:179-180 with H_residual recomputed):
  * H_new[n] = sum_m H_res[n,m] H[m] + H_post[n] bo, H_new in dtype_h. */
 int mhc_layer_add_forward(const void* H, int dtype_h, const void* branch_output, int dtype_bo,
                           const float* w, void* H_new, int64_t B, int64_t S, int64_t D,

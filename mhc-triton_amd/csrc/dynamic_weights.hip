@@ -1,6 +1,6 @@
 // Entry points: fused_dynamic_weights forward / backward and the sequence
 // mean-pool (reference src/mhc/_kernels.py:690-752, src/mhc/ops.py:72-228,
-// src/mhc/module.py:161).
+// src/mhc/module.py:123).
 #include "dynw_kernels.hpp"
 #include "stream_kernels.hpp"
 

@@ -293,7 +293,7 @@ __global__ __launch_bounds__(kThreads) void dynw_bwd_sum_kernel(const float* __r
 }
 
 // ---------------------------------------------------------------------------
-// Sequence mean-pool, module.py:161: x[b, c] = (1/S) sum_s H[b, s, c] over the
+// Sequence mean-pool, module.py:123: x[b, c] = (1/S) sum_s H[b, s, c] over the
 // flattened [S, 4D] view (c = n*D + d).  One workgroup owns a chunk of
 // CW = LPR*W columns of one batch for all S rows: LPR lanes span a row chunk
 // (16 bytes each), 256/LPR row groups walk down the sequence, UN rows in flight

@@ -1,4 +1,4 @@
-// HyperConnection layer path (reference src/mhc/module.py:141-220 composed with
+// HyperConnection layer path (reference src/mhc/module.py:103-182 composed with
 // ops.py / _kernels.py / _backward.py).
 //
 // Forward, dynamic:   meanpool<PROJ> (reads H)  -> finalize (weights w[B,24])
@@ -76,7 +76,7 @@ static int branch_input_any(const void* H, int dtype, const float* w, void* bi, 
   });
 }
 
-// Static weights (module.py:146-155), replicated for every batch row:
+// Static weights (module.py:108-117), replicated for every batch row:
 // H_post = sigmoid(b_post), H_pre = sigmoid(b_pre)/(sum + 1e-8),
 // H_res = Sinkhorn(H_res_base, iters, eps = 1e-8).
 __global__ __launch_bounds__(kThreads) void static_weights_kernel(const float* __restrict__ bpre,

@@ -149,7 +149,7 @@ def fused_dynamic_weights_forward(
 
 def mean_pool(H: torch.Tensor) -> torch.Tensor:
     """x[b, n*D + d] = mean_s H[b, s, n, d] in fp32 (the reference's
-    ``H.mean(dim=1).reshape(B, 4*D)``, src/mhc/module.py:161, without rounding
+    ``H.mean(dim=1).reshape(B, 4*D)``, src/mhc/module.py:123, without rounding
     x to H's dtype)."""
     if H.dim() != 4 or H.shape[2] != 4:
         raise ShapeError(f"H must be (batch, seq, 4, dim), got {tuple(H.shape)}")

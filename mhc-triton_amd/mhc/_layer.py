@@ -1,4 +1,4 @@
-"""Layer-level autograd for ``HyperConnection`` (reference src/mhc/module.py:141-220).
+"""Layer-level autograd for ``HyperConnection`` (reference src/mhc/module.py:103-182).
 
 The reference composes ``H.mean`` -> ``fused_dynamic_weights`` ->
 ``fused_stream_mix`` and returns a closure over ``H_residual`` that calls
@@ -68,7 +68,7 @@ def _grad_like(g: torch.Tensor, p: torch.Tensor) -> torch.Tensor:
 
 
 class _DynamicLayer(torch.autograd.Function):
-    """Node A, dynamic fused weights (module.py:157-177 + 214-215)."""
+    """Node A, dynamic fused weights (module.py:119-139 + 177)."""
 
     @staticmethod
     def forward(ctx, H, phi, H_pre_base, H_post_base, H_res_base, alpha_pre, alpha_post, alpha_res,
@@ -130,7 +130,7 @@ class _DynamicLayer(torch.autograd.Function):
 
 
 class _StaticLayer(torch.autograd.Function):
-    """Node A, static weights (module.py:146-155 + 214-215)."""
+    """Node A, static weights (module.py:108-117 + 177)."""
 
     @staticmethod
     def forward(ctx, H, H_pre_base, H_post_base, H_res_base, stash: _Stash, iters: int):
@@ -180,7 +180,7 @@ class _StaticLayer(torch.autograd.Function):
 
 class _GenericLayer(torch.autograd.Function):
     """Node A for weights produced by torch ops (the unfused dynamic path,
-    module.py:179-201): (H, w) -> (branch_input, w), differentiable in w."""
+    module.py:141-163): (H, w) -> (branch_input, w), differentiable in w."""
 
     @staticmethod
     def forward(ctx, H, w_in, stash: _Stash):
@@ -232,7 +232,7 @@ class _GenericLayer(torch.autograd.Function):
 
 class _LayerAdd(torch.autograd.Function):
     """Node B, the closure: H_new = H_res @ H + H_post * branch_output
-    (module.py:217-218 with H_residual recomputed from H)."""
+    (module.py:179-180 with H_residual recomputed from H)."""
 
     @staticmethod
     def forward(ctx, H, branch_output, w, stash: _Stash):

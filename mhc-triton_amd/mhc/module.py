@@ -97,7 +97,7 @@ class HyperConnection(nn.Module):
 
     def _unfused_weights(self, H: torch.Tensor) -> torch.Tensor:
         """Packed weights [B,24] of the unfused dynamic path (reference
-        src/mhc/module.py:179-201): RMS-normalised mean, three Linears, sigmoid
+        src/mhc/module.py:141-163): RMS-normalised mean, three Linears, sigmoid
         (no x2 on H_post), normalisation with 1e-8 and Sinkhorn with eps 1e-8."""
         B = H.shape[0]
         n = self.num_streams

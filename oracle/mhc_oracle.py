@@ -174,7 +174,7 @@ def add_residual_backward(dH_new, bo, H_post, dt=F64):
 
 
 # ---------------------------------------------------------------------------
-# Mean-pool (module.py:161) and static / unfused weights (module.py:146-155,179-201)
+# Mean-pool (module.py:123) and static / unfused weights (module.py:108-117,141-163)
 # ---------------------------------------------------------------------------
 
 def mean_pool(H, dt=F64):
@@ -265,7 +265,7 @@ def unfused_weights_backward(x, W_pre, W_post, W_res, s_pre, s_post, s_res, H_pr
 
 
 # ---------------------------------------------------------------------------
-# Whole HyperConnection layer (module.py:141-220 == _torch_baseline.py:169-336)
+# Whole HyperConnection layer (module.py:103-182 == _torch_baseline.py:169-336)
 # ---------------------------------------------------------------------------
 
 def layer_forward(p, H, bo, dynamic=True, fused=True, iters=20, eps=1e-6, dt=F64):
