@@ -177,8 +177,11 @@ int mhc_dynamic_weights_backward(const void* x, int dtype_x, const float* phi, c
 
 size_t mhc_layer_workspace_bytes(int64_t B, int64_t S, int64_t D, int dtype);
 
+size_t mhc_mean_pool_workspace_bytes(int64_t B, int64_t S, int64_t D, int dtype);
+
 /* Mean over the sequence, module.py:123 (H.mean(dim=1).reshape(B, 4D)),
- * accumulated and returned in f32: x [B, 4D]. */
+ * accumulated and returned in f32: x [B, 4D].  Two launches: split-S column
+ * sums into the workspace, then a fixed-order reduce over the S chunks. */
 int mhc_mean_pool(const void* H, int dtype, float* x, int64_t B, int64_t S, int64_t D,
                   void* workspace, size_t workspace_bytes, mhc_stream_t stream);
 

@@ -48,9 +48,18 @@ template <> __device__ __forceinline__ _Float16 from_f32<_Float16>(float v) { re
 // ---------------------------------------------------------------------------
 template <typename T> struct Io;
 
+// `NT` loads and stores carry the non-temporal hint (streamed data that this
+// kernel touches once): on gfx950 they are issued with the streaming cache
+// policy, which measurably raises HBM throughput of pure streaming kernels.
+template <typename V>
+__device__ __forceinline__ V vload(const V* p, bool nt) {
+  return nt ? __builtin_nontemporal_load(p) : *p;
+}
+
 template <> struct Io<float> {
+  template <bool NT = false>
   __device__ __forceinline__ static void load(const float* p, float* f) {
-    f32x4 v = *reinterpret_cast<const f32x4*>(p);
+    f32x4 v = vload(reinterpret_cast<const f32x4*>(p), NT);
     f[0] = v.x; f[1] = v.y; f[2] = v.z; f[3] = v.w;
   }
   template <bool NT>
@@ -62,8 +71,9 @@ template <> struct Io<float> {
 };
 
 template <> struct Io<__bf16> {
+  template <bool NT = false>
   __device__ __forceinline__ static void load(const __bf16* p, float* f) {
-    u32x4 r = *reinterpret_cast<const u32x4*>(p);
+    u32x4 r = vload(reinterpret_cast<const u32x4*>(p), NT);
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       f[2 * i] = __uint_as_float(r[i] << 16);
@@ -84,8 +94,9 @@ template <> struct Io<__bf16> {
 };
 
 template <> struct Io<_Float16> {
+  template <bool NT = false>
   __device__ __forceinline__ static void load(const _Float16* p, float* f) {
-    const f16x8 v = *reinterpret_cast<const f16x8*>(p);
+    const f16x8 v = vload(reinterpret_cast<const f16x8*>(p), NT);
     const f32x8 w = __builtin_convertvector(v, f32x8);
 #pragma unroll
     for (int i = 0; i < 8; ++i) f[i] = w[i];
@@ -103,12 +114,12 @@ template <> struct Io<_Float16> {
 
 // Load W consecutive elements when W is a multiple of the 16-byte vector
 // width of T (several 16-byte loads), or W == 1.
-template <typename T, int W>
+template <typename T, int W, bool NT = false>
 __device__ __forceinline__ void ld(const T* p, float* f) {
   constexpr int N = Vec<T>::N;
   if constexpr (W >= N) {
 #pragma unroll
-    for (int q = 0; q < W / N; ++q) Io<T>::load(p + q * N, f + q * N);
+    for (int q = 0; q < W / N; ++q) Io<T>::template load<NT>(p + q * N, f + q * N);
   } else {
 #pragma unroll
     for (int i = 0; i < W; ++i) f[i] = to_f32(p[i]);

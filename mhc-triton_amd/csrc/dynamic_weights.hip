@@ -139,58 +139,91 @@ extern "C" int mhc_dynamic_weights_backward(const void* x, int dtype_x, const fl
 // ---------------------------------------------------------------------------
 namespace mhc {
 
-constexpr int kPoolUN = 8;
+constexpr int kPoolUN = 4;  // rows in flight per lane in colsum_kernel
 
-template <typename T, int W, int LPR, bool PROJ>
-int launch_meanpool(const T* H, float* x, const float* phi, float* part, int64_t B, int64_t S, int64_t K,
-                    hipStream_t st) {
-  constexpr int CW = LPR * W;
-  const unsigned nchunk = (unsigned)((K + CW - 1) / CW);
+template <typename T, int W, bool PROJ>
+static int launch_meanpool(const T* H, float* x, const float* phi, float* projpart, float* colpart, int64_t B,
+                           int64_t S, int64_t K, hipStream_t st) {
+  const PoolPlan p = pool_plan(B, S, K, W);
   const float inv_S = S > 0 ? 1.f / (float)S : __builtin_nanf("");
   const bool phi_vec = phi ? aligned16(phi) : false;
-  return for_batch_chunks(B, [&](int64_t b0, int64_t nb) {
-    meanpool_kernel<T, W, LPR, kPoolUN, PROJ><<<dim3(nchunk, nb), kThreads, 0, st>>>(H, x, phi, part, S, K, inv_S,
-                                                                                     b0, phi_vec);
-    return hip_status(hipGetLastError(), "mean_pool launch");
-  });
+  for (int64_t b0 = 0; b0 < B; b0 += kMaxGridY) {
+    const int64_t nb = (B - b0) < kMaxGridY ? (B - b0) : kMaxGridY;
+    colsum_kernel<T, W, kPoolUN><<<dim3((unsigned)p.ncc, (unsigned)p.nS, (unsigned)nb), kThreads, 0, st>>>(
+        H, colpart, S, K, p.SC, p.nS, b0);
+    if (int rc = hip_status(hipGetLastError(), "mean_pool column-sum launch")) return rc;
+    colsum_reduce_kernel<PROJ><<<dim3((unsigned)p.nrc, (unsigned)nb), kThreads, 0, st>>>(
+        colpart, x, phi, projpart, K, p.nS, inv_S, b0, phi_vec);
+    if (int rc = hip_status(hipGetLastError(), "mean_pool reduce launch")) return rc;
+  }
+  return MHC_OK;
 }
 
-// Lanes per row: 8 lanes x 16 bytes = 128-byte row segments per workgroup
-// column chunk, which gives B*4D/(8W) workgroups (1024 at B=4, D=4096 bf16).
-constexpr int kPoolLPR = 8;
-
-int meanpool_columns(int dtype, int64_t D) {
+static bool pool_vec(int dtype, int64_t K, const void* H) {
   const int W = dtype == MHC_DTYPE_F32 ? 4 : 8;
-  (void)D;
-  return kPoolLPR * W;
+  return K % W == 0 && aligned16(H);
 }
 
-int mean_pool_any(const void* H, int dtype, float* x, const float* phi, float* part, int64_t B, int64_t S,
-                  int64_t D, hipStream_t st) {
+PoolPlan mean_pool_plan(int dtype, int64_t B, int64_t S, int64_t D, const void* H) {
   const int64_t K = 4 * D;
+  const int W = (H == nullptr || pool_vec(dtype, K, H)) ? (dtype == MHC_DTYPE_F32 ? 4 : 8) : 1;
+  return pool_plan(B, S, K, W);
+}
+
+// Column-partial workspace of the mean-pool: the largest plan over the vector
+// and scalar paths (the scalar path has more, narrower column chunks but the
+// same S split or a finer one).
+size_t mean_pool_colpart_bytes(int dtype, int64_t B, int64_t S, int64_t D) {
+  const int64_t K = 4 * D;
+  size_t best = 0;
+  for (int W : {dtype == MHC_DTYPE_F32 ? 4 : 8, 1}) {
+    const PoolPlan p = pool_plan(B, S, K, W);
+    const size_t v = (size_t)B * p.nS * K * sizeof(float);
+    if (v > best) best = v;
+  }
+  return best;
+}
+
+// x [B, 4D] f32 (and with phi, the projection partials [B][nrc][25]); returns
+// the number of projection chunks through *nrc.
+int mean_pool_any(const void* H, int dtype, float* x, const float* phi, float* projpart, float* colpart,
+                  int64_t B, int64_t S, int64_t D, int* nrc, hipStream_t st) {
+  const int64_t K = 4 * D;
+  const bool vec = pool_vec(dtype, K, H);
+  if (nrc) *nrc = (int)pool_plan(B, S, K, 1).nrc;
   return MHC_DISPATCH_DTYPE(dtype, [&] {
     constexpr int WV = Vec<T>::N;
-    const bool vec = (K % WV == 0) && aligned16(H);
     if (phi) {
-      if (vec) return launch_meanpool<T, WV, kPoolLPR, true>((const T*)H, x, phi, part, B, S, K, st);
-      return launch_meanpool<T, 1, kPoolLPR * WV, true>((const T*)H, x, phi, part, B, S, K, st);
+      if (vec) return launch_meanpool<T, WV, true>((const T*)H, x, phi, projpart, colpart, B, S, K, st);
+      return launch_meanpool<T, 1, true>((const T*)H, x, phi, projpart, colpart, B, S, K, st);
     }
-    if (vec) return launch_meanpool<T, WV, kPoolLPR, false>((const T*)H, x, nullptr, nullptr, B, S, K, st);
-    return launch_meanpool<T, 1, kPoolLPR * WV, false>((const T*)H, x, nullptr, nullptr, B, S, K, st);
+    if (vec) return launch_meanpool<T, WV, false>((const T*)H, x, nullptr, nullptr, colpart, B, S, K, st);
+    return launch_meanpool<T, 1, false>((const T*)H, x, nullptr, nullptr, colpart, B, S, K, st);
   });
 }
+
+static size_t al256(size_t v) { return (v + 255) & ~(size_t)255; }
 
 }  // namespace mhc
 
+extern "C" size_t mhc_mean_pool_workspace_bytes(int64_t B, int64_t S, int64_t D, int dtype) {
+  if (B <= 0 || D <= 0) return 0;
+  return al256(mean_pool_colpart_bytes(dtype, B, S, D));
+}
+
 extern "C" int mhc_mean_pool(const void* H, int dtype, float* x, int64_t B, int64_t S, int64_t D, void* workspace,
                              size_t workspace_bytes, mhc_stream_t stream) {
-  (void)workspace;
-  (void)workspace_bytes;
   if (int rc = check_bsd("mean_pool", B, S, D)) return rc;
   if (B * D == 0) return MHC_OK;
   if (!H || !x) {
     set_error("mean_pool: null pointer");
     return MHC_ERR_ARG;
   }
-  return mean_pool_any(H, dtype, x, nullptr, nullptr, B, S, D, (hipStream_t)stream);
+  if (dtype != MHC_DTYPE_F32 && dtype != MHC_DTYPE_BF16 && dtype != MHC_DTYPE_F16) {
+    set_error("unsupported dtype code %d", dtype);
+    return MHC_ERR_DTYPE;
+  }
+  if (int rc = check_workspace("mean_pool", workspace, workspace_bytes, mhc_mean_pool_workspace_bytes(B, S, D, dtype)))
+    return rc;
+  return mean_pool_any(H, dtype, x, nullptr, nullptr, (float*)workspace, B, S, D, nullptr, (hipStream_t)stream);
 }

@@ -8,9 +8,9 @@
 //   dynw_finalize_kernel  per row: fixed-order sum of the K-chunk partials,
 //                         inv_rms, scale + bias, sigmoid / normalise, 2*sigmoid
 //                         and the register-resident Sinkhorn of H_res.
-// Layer path: meanpool_kernel<PROJ=true> produces the same 25 partials per
-// column chunk straight from H while it forms the sequence mean, so the
-// projection costs no extra pass over HBM.
+// Layer path: colsum_reduce_kernel<PROJ=true> produces the same 25 partials
+// per column chunk while it finishes the sequence mean, so the projection
+// costs no extra pass over HBM.
 //
 // Backward (reference src/mhc/_kernels.py ops.py:110-228):
 //   dynw_bwd_rows_kernel  per row: Sinkhorn backward, sigmoid / normalise
@@ -116,29 +116,35 @@ __device__ __forceinline__ void dyn_scaled(const DynParams& P, const float (&raw
   for (int j = 0; j < 16; ++j) s[8 + j] = inv_rms * ar * raw[8 + j] + P.bias_res[j];
 }
 
-// One wave per row.  Lanes 0..24 sum one partial each over the nK chunks in
-// chunk order; lane 0 then runs the epilogue.
+// One wave per row.  Lane l sums the partial records l, l+64, l+128, ... (25
+// floats each) in chunk order, the wave then adds the 64 lane sums with a
+// fixed butterfly, and lane 0 runs the epilogue.  Keeping 64 independent load
+// streams per row instead of one serial chain matters: R is the batch (4 at
+// dim 4096) and this kernel sits between two full passes over H.
 template <int = 0>
 __global__ __launch_bounds__(kThreads) void dynw_finalize_kernel(const float* __restrict__ part, int nK, int64_t R,
                                                                  int64_t K, DynParams P, OutRow o_pre,
                                                                  OutRow o_post, OutRow o_res,
                                                                  float* __restrict__ aux, int iters, float eps) {
-  __shared__ float sh[4][kPart];
   const int wave = threadIdx.x >> 6;
   const int lane = threadIdx.x & 63;
   const int64_t r = (int64_t)blockIdx.x * 4 + wave;
-  if (r < R && lane < kPart) {
-    const float* p = part + r * nK * kPart + lane;
-    float v = 0.f;
-    for (int k = 0; k < nK; ++k) v += p[(int64_t)k * kPart];
-    sh[wave][lane] = v;
+  if (r >= R) return;
+  float acc[kPart];
+#pragma unroll
+  for (int j = 0; j < kPart; ++j) acc[j] = 0.f;
+  for (int k = lane; k < nK; k += 64) {
+    const float* p = part + (r * nK + k) * kPart;
+#pragma unroll
+    for (int j = 0; j < kPart; ++j) acc[j] += p[j];
   }
-  __syncthreads();
-  if (r >= R || lane != 0) return;
+#pragma unroll
+  for (int j = 0; j < kPart; ++j) acc[j] = wave_sum(acc[j]);
+  if (lane != 0) return;
   float raw[kOut];
 #pragma unroll
-  for (int j = 0; j < kOut; ++j) raw[j] = sh[wave][j];
-  const float inv_rms = 1.f / sqrtf(sh[wave][kOut] / (float)K + eps);
+  for (int j = 0; j < kOut; ++j) raw[j] = acc[j];
+  const float inv_rms = 1.f / sqrtf(acc[kOut] / (float)K + eps);
   float s[kOut];
   dyn_scaled(P, raw, inv_rms, s);
   // Eq. 17: H_pre = sigmoid / (sum + eps)
@@ -194,7 +200,7 @@ __global__ __launch_bounds__(kThreads) void dynw_bwd_rows_kernel(const float* __
       m[j] = s[8 + j];
       d[j] = g_res.p ? g_res.p[r * g_res.stride + j] : 0.f;
     }
-    sk_backward(m, d, iters, eps);
+    sk_backward<10>(m, d, iters, eps);
 #pragma unroll
     for (int j = 0; j < 16; ++j) gs[8 + j] = d[j];
   }
@@ -294,81 +300,116 @@ __global__ __launch_bounds__(kThreads) void dynw_bwd_sum_kernel(const float* __r
 
 // ---------------------------------------------------------------------------
 // Sequence mean-pool, module.py:123: x[b, c] = (1/S) sum_s H[b, s, c] over the
-// flattened [S, 4D] view (c = n*D + d).  One workgroup owns a chunk of
-// CW = LPR*W columns of one batch for all S rows: LPR lanes span a row chunk
-// (16 bytes each), 256/LPR row groups walk down the sequence, UN rows in flight
-// per lane; the row groups are summed through LDS in a fixed order.  With
-// PROJ the workgroup also emits the 25 projection partials of its columns
-// (x . phi[c,:] and x^2), replacing dynw_partial_kernel in the layer path.
+// flattened [S, K = 4D] view (c = n*D + d), in two launches.
+//
+// colsum_kernel: grid (column chunks, S chunks, batch).  A workgroup owns
+//   256*W columns (one 16-byte vector per lane: the workgroup reads 4 KiB of a
+//   row contiguously) and SC consecutive rows, which it walks with UN rows in
+//   flight per lane; each lane sums its own W columns, so no cross-lane step
+//   is needed, and the fp32 sums of the chunk go to colpart[b][sc][c].
+//   Splitting S gives enough workgroups at B = 1, but not too many: on MI355X
+//   this read peaks (80% of 8 TB/s) with about 1.5 workgroups x 4 rows in
+//   flight per CU; twice that loses 10%.
+// colsum_reduce_kernel: one thread per column sums the S-chunk partials in
+//   chunk order, scales by 1/S and writes x; with PROJ it also forms the 25
+//   projection partials of its 256 columns (x . phi[c,:] and x^2), so the
+//   dynamic-weight projection needs no extra pass over x.
 // ---------------------------------------------------------------------------
-template <typename T, int W, int LPR, int UN, bool PROJ>
-__global__ __launch_bounds__(kThreads) void meanpool_kernel(const T* __restrict__ H, float* __restrict__ x,
-                                                            const float* __restrict__ phi,
-                                                            float* __restrict__ part, int64_t S, int64_t K,
-                                                            float inv_S, int64_t b0, bool phi_vec) {
-  constexpr int RPP = kThreads / LPR;  // row groups
-  constexpr int CW = LPR * W;          // columns per workgroup
-  __shared__ float lds[RPP * CW];
-  __shared__ float red[4 * kPart];
-  const int64_t b = b0 + blockIdx.y;
-  const int64_t col0 = (int64_t)blockIdx.x * CW;
-  const int lc = threadIdx.x % LPR;
-  const int rg = threadIdx.x / LPR;
-  const int64_t col = col0 + (int64_t)lc * W;
-  const bool colok = col < K;
+template <typename T, int W, int UN>
+__global__ __launch_bounds__(kThreads) void colsum_kernel(const T* __restrict__ H, float* __restrict__ colpart,
+                                                          int64_t S, int64_t K, int64_t SC, int nS, int64_t b0) {
+  const int64_t b = b0 + blockIdx.z;
+  const int sc = blockIdx.y;
+  const int64_t col = (int64_t)blockIdx.x * (kThreads * W) + (int64_t)threadIdx.x * W;
+  if (col >= K) return;
+  const int64_t sbeg = (int64_t)sc * SC;
+  const int64_t send = sbeg + SC < S ? sbeg + SC : S;
   float acc[W];
 #pragma unroll
   for (int e = 0; e < W; ++e) acc[e] = 0.f;
-  if (colok) {
-    const T* p = H + b * S * K + col;
-    int64_t s = rg;
-    for (; s + (UN - 1) * RPP < S; s += UN * RPP) {
-      float v[UN][W];
+  const T* p = H + b * S * K + col;
+  int64_t s = sbeg;
+  for (; s + (UN - 1) < send; s += UN) {
+    float v[UN][W];
 #pragma unroll
-      for (int u = 0; u < UN; ++u) ld<T, W>(p + (s + u * RPP) * K, v[u]);
+    for (int u = 0; u < UN; ++u) ld<T, W>(p + (s + u) * K, v[u]);
 #pragma unroll
-      for (int u = 0; u < UN; ++u)
+    for (int u = 0; u < UN; ++u)
 #pragma unroll
-        for (int e = 0; e < W; ++e) acc[e] += v[u][e];
-    }
-    for (; s < S; s += RPP) {
-      float v[W];
-      ld<T, W>(p + s * K, v);
-#pragma unroll
-      for (int e = 0; e < W; ++e) acc[e] += v[e];
-    }
+      for (int e = 0; e < W; ++e) acc[e] += v[u][e];
   }
+  for (; s < send; ++s) {
+    float v[W];
+    ld<T, W>(p + s * K, v);
 #pragma unroll
-  for (int e = 0; e < W; ++e) lds[rg * CW + lc * W + e] = acc[e];
-  __syncthreads();
+    for (int e = 0; e < W; ++e) acc[e] += v[e];
+  }
+  st<float, W>(colpart + ((b * nS + sc) * K + col), acc);
+}
+
+template <bool PROJ>
+__global__ __launch_bounds__(kThreads) void colsum_reduce_kernel(const float* __restrict__ colpart,
+                                                                 float* __restrict__ x,
+                                                                 const float* __restrict__ phi,
+                                                                 float* __restrict__ projpart, int64_t K, int nS,
+                                                                 float inv_S, int64_t b0, bool phi_vec) {
+  __shared__ float red[4 * kPart];
+  const int64_t b = b0 + blockIdx.y;
+  const int64_t c = (int64_t)blockIdx.x * kThreads + threadIdx.x;
   float pv[kPart];
 #pragma unroll
   for (int j = 0; j < kPart; ++j) pv[j] = 0.f;
-  for (int c = threadIdx.x; c < CW; c += kThreads) {
+  if (c < K) {
+    const float* p = colpart + b * nS * K + c;
     float v = 0.f;
 #pragma unroll 8
-    for (int g = 0; g < RPP; ++g) v += lds[g * CW + c];
+    for (int k = 0; k < nS; ++k) v += p[(int64_t)k * K];
     v *= inv_S;
-    const int64_t cc = col0 + c;
-    if (cc < K) {
-      x[b * K + cc] = v;
-      if constexpr (PROJ) {
-        float ph[kOut];
-        load_phi_row(phi, cc, phi_vec, ph);
+    x[b * K + c] = v;
+    if constexpr (PROJ) {
+      float ph[kOut];
+      load_phi_row(phi, c, phi_vec, ph);
 #pragma unroll
-        for (int j = 0; j < kOut; ++j) pv[j] += v * ph[j];
-        pv[kOut] += v * v;
-      }
+      for (int j = 0; j < kOut; ++j) pv[j] = v * ph[j];
+      pv[kOut] = v * v;
     }
   }
   if constexpr (PROJ) {
     block_sum<kPart>(pv, red);
     if (threadIdx.x == 0) {
-      float* pp = part + (b * gridDim.x + blockIdx.x) * kPart;
+      float* pp = projpart + (b * gridDim.x + blockIdx.x) * kPart;
 #pragma unroll
       for (int j = 0; j < kPart; ++j) pp[j] = pv[j];
     }
   }
+}
+
+// Launch plan of the two mean-pool kernels; depends only on the shape, so
+// workspace sizes can be queried without a device.
+struct PoolPlan {
+  int W;         // elements per lane (16 bytes, or 1 on the unaligned path)
+  int64_t ncc;   // column chunks of 256*W
+  int64_t SC;    // rows per S chunk
+  int nS;        // S chunks
+  int64_t nrc;   // column chunks of the reduce kernel (256 columns)
+};
+
+constexpr int kPoolWG = 384;  // target colsum workgroups: 1.5 per CU on MI355X
+
+__host__ inline PoolPlan pool_plan(int64_t B, int64_t S, int64_t K, int W) {
+  PoolPlan p;
+  p.W = W;
+  p.ncc = (K + kThreads * W - 1) / (kThreads * W);
+  if (p.ncc < 1) p.ncc = 1;
+  const int64_t per = p.ncc * (B > 0 ? B : 1);
+  int64_t ns = (kPoolWG + per - 1) / per;
+  if (ns < 1) ns = 1;
+  int64_t sc = S > 0 ? (S + ns - 1) / ns : 1;
+  p.SC = sc;
+  p.nS = S > 0 ? (int)((S + sc - 1) / sc) : 1;
+  p.nrc = (K + kThreads - 1) / kThreads;
+  if (p.nrc < 1) p.nrc = 1;
+  return p;
 }
 
 }  // namespace mhc

@@ -20,17 +20,19 @@ namespace mhc {
 int check_workspace(const char* who, const void* ws, size_t have, size_t need);
 int add_residual_backward_any(const void* dhn, int dtype_h, const void* bo, int dtype_bo, WRow post, void* dbo,
                               float* dpost, int64_t B, int64_t S, int64_t D, float* part, hipStream_t st);
-int mean_pool_any(const void* H, int dtype, float* x, const float* phi, float* part, int64_t B, int64_t S,
-                  int64_t D, hipStream_t st);
-int meanpool_columns(int dtype, int64_t D);
+int mean_pool_any(const void* H, int dtype, float* x, const float* phi, float* projpart, float* colpart,
+                  int64_t B, int64_t S, int64_t D, int* nrc, hipStream_t st);
+size_t mean_pool_colpart_bytes(int dtype, int64_t B, int64_t S, int64_t D);
 
-constexpr int kLU = 2;
+constexpr int kLU = 1;   // items per lane per tile, streaming passes
+constexpr int kLRU = 2;  // items per lane per tile, the reduction-only pass B
 
 static size_t al(size_t v) { return (v + 255) & ~(size_t)255; }
 
 // Workspace layout shared by all layer entry points (each uses a prefix of it).
 struct LayerWs {
-  size_t pool_part;  // [B][nchunk][25]
+  size_t colpart;    // mean-pool column partials [B][nS][4D]
+  size_t pool_part;  // projection partials [B][nrc][25]
   size_t red_part;   // [B][nblk][20]
   size_t dpre;       // [B][4]
   size_t dres;       // [B][16]
@@ -40,12 +42,11 @@ struct LayerWs {
 };
 
 static LayerWs layer_ws(int64_t B, int64_t S, int64_t D, int dtype) {
-  (void)S;
   LayerWs w;
-  const int64_t cw = meanpool_columns(dtype, D);
-  const int64_t nchunk = (4 * D + cw - 1) / cw;
+  const int64_t nrc = (4 * D + kThreads - 1) / kThreads;
   size_t o = 0;
-  w.pool_part = o; o += al((size_t)B * nchunk * kPart * sizeof(float));
+  w.colpart = o;   o += al(mean_pool_colpart_bytes(dtype, B, S, D));
+  w.pool_part = o; o += al((size_t)B * (nrc > 0 ? nrc : 1) * kPart * sizeof(float));
   w.red_part = o;  o += al(partial_bytes(B, 20));
   w.dpre = o;      o += al((size_t)B * 4 * sizeof(float));
   w.dres = o;      o += al((size_t)B * 16 * sizeof(float));
@@ -60,7 +61,7 @@ static int launch_bi(const T* H, const float* w, T* bi, int64_t B, int64_t S, in
   return for_batch_chunks(B, [&](int64_t b0, int64_t nb) {
     const Geom g = make_geom<W, kLU>(S, D, b0);
     if (g.ntiles == 0) return (int)MHC_OK;
-    mix_fwd_kernel<T, T, W, kLU, true, false, false><<<dim3(g.ntiles, nb), kThreads, 0, st>>>(
+    mix_fwd_kernel<T, T, W, kLU, true, false, false, kNtStores><<<dim3(g.ntiles, nb), kThreads, occupancy_lds(4), st>>>(
         H, (const T*)nullptr, WRow{w, kOut}, WRow{nullptr, 0}, WRow{nullptr, 0}, bi, nullptr, g);
     return hip_status(hipGetLastError(), "layer branch_input launch");
   });
@@ -156,14 +157,18 @@ __global__ __launch_bounds__(kThreads) void static_weights_bwd_kernel(
 template <typename T, int W, bool HAS_DHN, bool REDUCE, bool WRITE_DH, bool HAS_GX>
 static int launch_mix_bwd(const T* dbi, const T* dhn, const T* H, const float* gx, const float* w, T* dH,
                           float* part, int64_t B, int64_t S, int64_t D, uint32_t* nblk_out, hipStream_t st) {
-  const Geom g0 = make_geom<W, kLU>(S, D, 0);
+  // Pass B writes nothing bulk: two items per lane and full occupancy.  The
+  // passes that write dH take one item per lane and capped occupancy.
+  constexpr int U = WRITE_DH ? kLU : kLRU;
+  const size_t lds = WRITE_DH ? occupancy_lds(REDUCE ? 3 : 4) : 0;
+  const Geom g0 = make_geom<W, U>(S, D, 0);
   const uint32_t nblk = REDUCE ? reduce_blocks(g0.ntiles, B) : g0.ntiles;
   if (nblk_out) *nblk_out = nblk;
   if (nblk == 0) return MHC_OK;
   const float inv_S = S > 0 ? 1.f / (float)S : 0.f;
   return for_batch_chunks(B, [&](int64_t b0, int64_t nb) {
-    const Geom g = make_geom<W, kLU>(S, D, b0);
-    mix_bwd_kernel<T, W, kLU, HAS_DHN, REDUCE, WRITE_DH, HAS_GX><<<dim3(nblk, nb), kThreads, 0, st>>>(
+    const Geom g = make_geom<W, U>(S, D, b0);
+    mix_bwd_kernel<T, W, U, HAS_DHN, REDUCE, WRITE_DH, HAS_GX, kNtStores><<<dim3(nblk, nb), kThreads, lds, st>>>(
         dbi, dhn, H, gx, inv_S, WRow{w, kOut}, WRow{w + 8, kOut}, dH, part, g);
     return hip_status(hipGetLastError(), "layer mix backward launch");
   });
@@ -220,9 +225,8 @@ extern "C" int mhc_layer_dynamic_forward(const void* H, int dtype, const float* 
   LAYER_WS_CHECK("layer_dynamic_forward");
   hipStream_t st = (hipStream_t)stream;
   float* part = (float*)(wsb + L.pool_part);
-  if (int rc = mean_pool_any(H, dtype, x, phi, part, B, S, D, st)) return rc;
-  const int64_t cw = meanpool_columns(dtype, D);
-  const int nK = (int)((4 * D + cw - 1) / cw);
+  int nK = 0;
+  if (int rc = mean_pool_any(H, dtype, x, phi, part, (float*)(wsb + L.colpart), B, S, D, &nK, st)) return rc;
   DynParams P{H_pre_base, H_post_base, H_res_base, alpha_pre, alpha_post, alpha_res};
   dynw_finalize_kernel<><<<dim3((unsigned)((B + 3) / 4)), kThreads, 0, st>>>(
       part, nK, B, 4 * D, P, OutRow{w, kOut}, OutRow{w + 4, kOut}, OutRow{w + 8, kOut}, aux, iters, eps);
@@ -263,7 +267,8 @@ extern "C" int mhc_layer_add_forward(const void* H, int dtype_h, const void* bra
       constexpr int W = decltype(wtag)::value;
       return for_batch_chunks(B, [&](int64_t b0, int64_t nb) {
         const Geom g = make_geom<W, kLU>(S, D, b0);
-        mix_fwd_kernel<TH, TB, W, kLU, false, true, true><<<dim3(g.ntiles, nb), kThreads, 0, st>>>(
+        mix_fwd_kernel<TH, TB, W, kLU, false, true, true, kNtStores>
+            <<<dim3(g.ntiles, nb), kThreads, occupancy_lds(2), st>>>(
             (const TH*)H, (const TB*)branch_output, WRow{nullptr, 0}, WRow{w + 8, kOut}, WRow{w + 4, kOut},
             nullptr, (TH*)H_new, g);
         return hip_status(hipGetLastError(), "layer add forward launch");

@@ -7,15 +7,33 @@
 // bf16/fp16; W = 1 on the unaligned / ragged-D path) across all 4 streams.
 // Consecutive lanes take consecutive items, so each wave access is one
 // contiguous 1 KiB span per stream row.  A workgroup processes tiles of
-// 256 * U items; with U = 2 a lane keeps 8 (forward) to 18 (backward)
-// 16-byte loads in flight.  Kernels that reduce over (s, d) stride over tiles
-// and write one partial vector per workgroup; reduce_partials_kernel then sums
-// them in a fixed order (deterministic).
+// 256 * U items (U = 1: a lane keeps 4-5 16-byte loads in flight; the
+// reduction-only pass uses U = 2).  Kernels that reduce over (s, d) stride over
+// tiles and write one partial vector per workgroup; reduce_split_kernel then
+// sums them in a fixed order (deterministic).
 #pragma once
 
 #include "common.hpp"
 
 namespace mhc {
+
+// ---------------------------------------------------------------------------
+// Launch shape of the streaming kernels, measured on MI355X (gfx950: 256 CUs,
+// 160 KiB LDS per CU).  HBM throughput of these kernels peaks with roughly
+// 24-40 KiB of loads in flight per CU; more resident workgroups lower it (the
+// closure forward, 5 loads per lane, runs at 73% of 8 TB/s with 8 workgroups
+// per CU and at 77% with 2).  The kernels use almost no LDS, so the cap is set
+// by reserving dynamic LDS at launch: at most `wg_per_cu` workgroups fit on a
+// CU.  Streamed outputs are written with non-temporal stores (NT = 2), which
+// lifts every write-heavy kernel by 3-6%.
+// ---------------------------------------------------------------------------
+constexpr size_t kLdsPerCu = 160 * 1024;
+
+inline size_t occupancy_lds(int wg_per_cu) {
+  return wg_per_cu <= 0 ? 0 : (kLdsPerCu / (size_t)wg_per_cu - 1024) & ~(size_t)255;
+}
+
+constexpr int kNtStores = 2;
 
 // Per-batch fp32 weight rows: element n of batch b is p[b * stride + n].
 struct WRow {
@@ -61,7 +79,7 @@ __device__ __forceinline__ void load_w16(WRow w, int64_t b, float (&v)[16]) {
 // Used for fused_stream_mix (BI + RES), the layer's branch_input pass (BI)
 // and the layer closure (RES + ADD_BO, H_residual never stored).
 // ---------------------------------------------------------------------------
-template <typename T, typename TB, int W, int U, bool BI, bool RES, bool ADD_BO>
+template <typename T, typename TB, int W, int U, bool BI, bool RES, bool ADD_BO, int NT = 0>
 __global__ __launch_bounds__(kThreads) void mix_fwd_kernel(const T* __restrict__ H, const TB* __restrict__ bo,
                                                            WRow pre, WRow res, WRow post, T* __restrict__ bi,
                                                            T* __restrict__ out, Geom g) {
@@ -88,8 +106,8 @@ __global__ __launch_bounds__(kThreads) void mix_fwd_kernel(const T* __restrict__
       if (ok[u]) {
         const T* hp = Hb + s_[u] * 4 * D + cw[u];
 #pragma unroll
-        for (int n = 0; n < 4; ++n) ld<T, W>(hp + n * D, h[u][n]);
-        if constexpr (ADD_BO) ld<TB, W>(bo + b * g.S * D + s_[u] * D + cw[u], bv[u]);
+        for (int n = 0; n < 4; ++n) ld<T, W, (NT & 1) != 0>(hp + n * D, h[u][n]);
+        if constexpr (ADD_BO) ld<TB, W, (NT & 1) != 0>(bo + b * g.S * D + s_[u] * D + cw[u], bv[u]);
       }
     }
 #pragma unroll
@@ -100,7 +118,7 @@ __global__ __launch_bounds__(kThreads) void mix_fwd_kernel(const T* __restrict__
 #pragma unroll
         for (int e = 0; e < W; ++e)
           r[e] = wp[0] * h[u][0][e] + wp[1] * h[u][1][e] + wp[2] * h[u][2][e] + wp[3] * h[u][3][e];
-        st<T, W>(bi + b * g.S * D + s_[u] * D + cw[u], r);
+        st<T, W, (NT & 2) != 0>(bi + b * g.S * D + s_[u] * D + cw[u], r);
       }
       if constexpr (RES) {
         T* op = out + b * g.S * 4 * D + s_[u] * 4 * D + cw[u];
@@ -114,7 +132,7 @@ __global__ __launch_bounds__(kThreads) void mix_fwd_kernel(const T* __restrict__
             if constexpr (ADD_BO) v += wq[n] * bv[u][e];
             r[e] = v;
           }
-          st<T, W>(op + n * D, r);
+          st<T, W, (NT & 2) != 0>(op + n * D, r);
         }
       }
     }
@@ -125,7 +143,7 @@ __global__ __launch_bounds__(kThreads) void mix_fwd_kernel(const T* __restrict__
 // Add residual forward from a materialised H_residual (fused_add_residual):
 //   out[s,n,:] = hr[s,n,:] + post[n] bo[s,:]
 // ---------------------------------------------------------------------------
-template <typename T, typename TB, int W, int U>
+template <typename T, typename TB, int W, int U, int NT = 0>
 __global__ __launch_bounds__(kThreads) void add_residual_fwd_kernel(const T* __restrict__ hr,
                                                                     const TB* __restrict__ bo, WRow post,
                                                                     T* __restrict__ out, Geom g) {
@@ -147,8 +165,8 @@ __global__ __launch_bounds__(kThreads) void add_residual_fwd_kernel(const T* __r
       hoff[u] = b * g.S * 4 * D + (int64_t)s * 4 * D + (int64_t)c * W;
       if (ok[u]) {
 #pragma unroll
-        for (int n = 0; n < 4; ++n) ld<T, W>(hr + hoff[u] + n * D, h[u][n]);
-        ld<TB, W>(bo + b * g.S * D + (int64_t)s * D + (int64_t)c * W, bv[u]);
+        for (int n = 0; n < 4; ++n) ld<T, W, (NT & 1) != 0>(hr + hoff[u] + n * D, h[u][n]);
+        ld<TB, W, (NT & 1) != 0>(bo + b * g.S * D + (int64_t)s * D + (int64_t)c * W, bv[u]);
       }
     }
 #pragma unroll
@@ -159,7 +177,7 @@ __global__ __launch_bounds__(kThreads) void add_residual_fwd_kernel(const T* __r
         float r[W];
 #pragma unroll
         for (int e = 0; e < W; ++e) r[e] = h[u][n][e] + wq[n] * bv[u][e];
-        st<T, W>(out + hoff[u] + n * D, r);
+        st<T, W, (NT & 2) != 0>(out + hoff[u] + n * D, r);
       }
     }
   }
@@ -170,7 +188,7 @@ __global__ __launch_bounds__(kThreads) void add_residual_fwd_kernel(const T* __r
 //   d_bo[s,:] = sum_n post[n] dHn[s,n,:]              (written, dtype TB)
 //   part[k]   = sum dHn[s,k,:] * bo[s,:]   k < 4      (reduced -> dH_post)
 // ---------------------------------------------------------------------------
-template <typename T, typename TB, int W, int U>
+template <typename T, typename TB, int W, int U, int NT = 0>
 __global__ __launch_bounds__(kThreads) void add_residual_bwd_kernel(const T* __restrict__ dhn,
                                                                     const TB* __restrict__ bo, WRow post,
                                                                     TB* __restrict__ dbo, float* __restrict__ part,
@@ -196,8 +214,8 @@ __global__ __launch_bounds__(kThreads) void add_residual_bwd_kernel(const T* __r
       if (ok[u]) {
         const T* hp = dhn + b * g.S * 4 * D + (int64_t)s * 4 * D + (int64_t)c * W;
 #pragma unroll
-        for (int n = 0; n < 4; ++n) ld<T, W>(hp + n * D, h[u][n]);
-        ld<TB, W>(bo + boff[u], bv[u]);
+        for (int n = 0; n < 4; ++n) ld<T, W, (NT & 1) != 0>(hp + n * D, h[u][n]);
+        ld<TB, W, (NT & 1) != 0>(bo + boff[u], bv[u]);
       }
     }
 #pragma unroll
@@ -210,7 +228,7 @@ __global__ __launch_bounds__(kThreads) void add_residual_bwd_kernel(const T* __r
 #pragma unroll
         for (int n = 0; n < 4; ++n) acc[n] += h[u][n][e] * bv[u][e];
       }
-      st<TB, W>(dbo + boff[u], r);
+      st<TB, W, (NT & 2) != 0>(dbo + boff[u], r);
     }
   }
   block_sum<4>(acc, lds);
@@ -230,7 +248,7 @@ __global__ __launch_bounds__(kThreads) void add_residual_bwd_kernel(const T* __r
 // HAS_DHN = false treats dhn as zero (H_new / H_residual got no gradient).
 // HAS_GX adds the mean-pool backward term grad_x[b, m*D + d] / S.
 // ---------------------------------------------------------------------------
-template <typename T, int W, int U, bool HAS_DHN, bool REDUCE, bool WRITE_DH, bool HAS_GX>
+template <typename T, int W, int U, bool HAS_DHN, bool REDUCE, bool WRITE_DH, bool HAS_GX, int NT = 0>
 __global__ __launch_bounds__(kThreads) void mix_bwd_kernel(const T* __restrict__ dbi, const T* __restrict__ dhn,
                                                            const T* __restrict__ H, const float* __restrict__ gx,
                                                            float inv_S, WRow pre, WRow res, T* __restrict__ dH,
@@ -265,14 +283,14 @@ __global__ __launch_bounds__(kThreads) void mix_bwd_kernel(const T* __restrict__
       cw[u] = (int64_t)c * W;
       off[u] = b * g.S * 4 * D + (int64_t)s * 4 * D + cw[u];
       if (ok[u]) {
-        ld<T, W>(dbi + b * g.S * D + (int64_t)s * D + cw[u], db[u]);
+        ld<T, W, (NT & 1) != 0>(dbi + b * g.S * D + (int64_t)s * D + cw[u], db[u]);
         if constexpr (HAS_DHN) {
 #pragma unroll
-          for (int n = 0; n < 4; ++n) ld<T, W>(dhn + off[u] + n * D, dn[u][n]);
+          for (int n = 0; n < 4; ++n) ld<T, W, (NT & 1) != 0>(dhn + off[u] + n * D, dn[u][n]);
         }
         if constexpr (REDUCE) {
 #pragma unroll
-          for (int n = 0; n < 4; ++n) ld<T, W>(H + off[u] + n * D, h[u][n]);
+          for (int n = 0; n < 4; ++n) ld<T, W, (NT & 1) != 0>(H + off[u] + n * D, h[u][n]);
         }
         if constexpr (HAS_GX) {
 #pragma unroll
@@ -309,7 +327,7 @@ __global__ __launch_bounds__(kThreads) void mix_bwd_kernel(const T* __restrict__
             if constexpr (HAS_GX) v += gv[u][m][e] * inv_S;
             r[e] = v;
           }
-          st<T, W>(dH + off[u] + m * D, r);
+          st<T, W, (NT & 2) != 0>(dH + off[u] + m * D, r);
         }
       }
     }

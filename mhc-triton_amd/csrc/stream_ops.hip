@@ -5,7 +5,8 @@
 
 namespace mhc {
 
-constexpr int kU = 2;  // items per lane per tile
+constexpr int kU = 1;   // items per lane per tile, streaming kernels
+constexpr int kRU = 2;  // items per lane per tile, reduction kernels that write nothing bulk
 
 template <typename T, int W>
 static int stream_mix_fwd(const T* H, const float* pre, const float* res, T* bi, T* out, int64_t B, int64_t S,
@@ -13,7 +14,7 @@ static int stream_mix_fwd(const T* H, const float* pre, const float* res, T* bi,
   return for_batch_chunks(B, [&](int64_t b0, int64_t nb) {
     const Geom g = make_geom<W, kU>(S, D, b0);
     if (g.ntiles == 0) return (int)MHC_OK;
-    mix_fwd_kernel<T, T, W, kU, true, true, false><<<dim3(g.ntiles, nb), kThreads, 0, st>>>(
+    mix_fwd_kernel<T, T, W, kU, true, true, false, kNtStores><<<dim3(g.ntiles, nb), kThreads, occupancy_lds(2), st>>>(
         H, (const T*)nullptr, WRow{pre, 4}, WRow{res, 16}, WRow{nullptr, 0}, bi, out, g);
     return hip_status(hipGetLastError(), "stream_mix_forward launch");
   });
@@ -27,7 +28,7 @@ static int stream_mix_bwd(const T* dbi, const T* dhr, const T* H, const float* p
   const uint32_t nblk = reduce_blocks(g0.ntiles, B);
   int rc = for_batch_chunks(B, [&](int64_t b0, int64_t nb) {
     const Geom g = make_geom<W, kU>(S, D, b0);
-    mix_bwd_kernel<T, W, kU, true, true, true, false><<<dim3(nblk, nb), kThreads, 0, st>>>(
+    mix_bwd_kernel<T, W, kU, true, true, true, false, kNtStores><<<dim3(nblk, nb), kThreads, occupancy_lds(3), st>>>(
         dbi, dhr, H, nullptr, 0.f, WRow{pre, 4}, WRow{res, 16}, dH, part, g);
     return hip_status(hipGetLastError(), "stream_mix_backward launch");
   });
@@ -42,7 +43,8 @@ static int add_res_fwd(const TH* hr, const TB* bo, const float* post, TH* out, i
   return for_batch_chunks(B, [&](int64_t b0, int64_t nb) {
     const Geom g = make_geom<W, kU>(S, D, b0);
     if (g.ntiles == 0) return (int)MHC_OK;
-    add_residual_fwd_kernel<TH, TB, W, kU><<<dim3(g.ntiles, nb), kThreads, 0, st>>>(hr, bo, WRow{post, 4}, out, g);
+    add_residual_fwd_kernel<TH, TB, W, kU, kNtStores><<<dim3(g.ntiles, nb), kThreads, occupancy_lds(2), st>>>(
+        hr, bo, WRow{post, 4}, out, g);
     return hip_status(hipGetLastError(), "add_residual_forward launch");
   });
 }
@@ -54,7 +56,8 @@ static int add_res_bwd(const TH* dhn, const TB* bo, WRow post, TB* dbo, float* d
   const uint32_t nblk = reduce_blocks(g0.ntiles, B);
   int rc = for_batch_chunks(B, [&](int64_t b0, int64_t nb) {
     const Geom g = make_geom<W, kU>(S, D, b0);
-    add_residual_bwd_kernel<TH, TB, W, kU><<<dim3(nblk, nb), kThreads, 0, st>>>(dhn, bo, post, dbo, part, g);
+    add_residual_bwd_kernel<TH, TB, W, kU, kNtStores><<<dim3(nblk, nb), kThreads, occupancy_lds(2), st>>>(
+        dhn, bo, post, dbo, part, g);
     return hip_status(hipGetLastError(), "add_residual_backward launch");
   });
   if (rc) return rc;

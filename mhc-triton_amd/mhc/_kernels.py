@@ -158,7 +158,9 @@ def mean_pool(H: torch.Tensor) -> torch.Tensor:
     H = H.contiguous()
     x = torch.empty(B, 4 * D, device=dev, dtype=torch.float32)
     lib = _lib.load()
+    code = _lib.dtype_code(H)
+    ws = _lib.workspace(lib.mhc_mean_pool_workspace_bytes(B, S, D, code), dev)
     with _lib.on_device(dev):
-        _lib.check(lib.mhc_mean_pool(H.data_ptr(), _lib.dtype_code(H), x.data_ptr(), B, S, D, None, 0,
-                                     _lib.stream(dev)), "mean_pool")
+        _lib.check(lib.mhc_mean_pool(H.data_ptr(), code, x.data_ptr(), B, S, D, _lib.ptr(ws),
+                                     0 if ws is None else ws.numel(), _lib.stream(dev)), "mean_pool")
     return x
