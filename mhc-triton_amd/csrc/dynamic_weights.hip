@@ -117,21 +117,17 @@ extern "C" int mhc_dynamic_weights_backward(const void* x, int dtype_x, const fl
     return rc;
   float* rowbuf = (float*)workspace;
   DynParams P{bias, bias + 4, bias + 8, alpha_pre, alpha_post, alpha_res};
-  dynw_bwd_rows_kernel<><<<dim3((unsigned)((R + kThreads - 1) / kThreads)), kThreads, 0, st>>>(
-      aux, P, InRow{H_pre, 4}, InRow{grad_H_pre, 4}, InRow{grad_H_post, 4}, InRow{grad_H_res, 16}, rowbuf, R, K,
-      iters, eps);
+  dynw_bwd_rows_kernel<><<<dim3((unsigned)((R + 3) / 4)), kThreads, 0, st>>>(
+      aux, P, InRow{H_pre, 4}, InRow{grad_H_pre, 4}, InRow{grad_H_post, 4}, InRow{grad_H_res, 16}, nullptr, 0,
+      rowbuf, R, K, iters, eps);
   if (int rc = hip_status(hipGetLastError(), "dynamic_weights_backward rows launch")) return rc;
-  if (K > 0 && (grad_x || grad_phi)) {
-    const bool phi_vec = aligned16(phi);
-    int rc = MHC_DISPATCH_DTYPE(dtype_x, [&] {
-      dynw_bwd_wide_kernel<T><<<dim3((unsigned)((K + kThreads - 1) / kThreads)), kThreads, 0, st>>>(
-          (const T*)x, phi, rowbuf, grad_x, grad_phi, R, K, phi_vec);
-      return hip_status(hipGetLastError(), "dynamic_weights_backward wide launch");
-    });
-    if (rc) return rc;
-  }
-  dynw_bwd_sum_kernel<><<<1, kThreads, 0, st>>>(rowbuf, R, grad_bias, grad_alpha);
-  return hip_status(hipGetLastError(), "dynamic_weights_backward sum launch");
+  const bool phi_vec = aligned16(phi);
+  const unsigned nwide = K > 0 ? (unsigned)((K + kThreads - 1) / kThreads) : 1u;
+  return MHC_DISPATCH_DTYPE(dtype_x, [&] {
+    dynw_bwd_wide_kernel<T><<<dim3(nwide), kThreads, 0, st>>>((const T*)x, phi, rowbuf, grad_x, grad_phi, grad_bias,
+                                                              grad_alpha, R, K, phi_vec);
+    return hip_status(hipGetLastError(), "dynamic_weights_backward wide launch");
+  });
 }
 
 // ---------------------------------------------------------------------------

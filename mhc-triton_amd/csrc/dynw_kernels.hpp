@@ -18,7 +18,8 @@
 //                         per-row bias / alpha contributions.
 //   dynw_bwd_wide_kernel  per k: grad_x[r,k] = grad_raw[r,:] . phi[k,:] + coef[r] x[r,k]
 //                         and grad_phi[k,:] = sum_r x[r,k] grad_raw[r,:].
-//   dynw_bwd_sum_kernel   grad_bias and grad_alpha: fixed-order sums over rows.
+//                         Workgroup 0 also sums grad_bias and grad_alpha over
+//                         rows in a fixed order.
 #pragma once
 
 #include "sinkhorn.hpp"
@@ -126,48 +127,50 @@ __global__ __launch_bounds__(kThreads) void dynw_finalize_kernel(const float* __
                                                                  int64_t K, DynParams P, OutRow o_pre,
                                                                  OutRow o_post, OutRow o_res,
                                                                  float* __restrict__ aux, int iters, float eps) {
+  __shared__ float tot[4][kPart];
   const int wave = threadIdx.x >> 6;
   const int lane = threadIdx.x & 63;
   const int64_t r = (int64_t)blockIdx.x * 4 + wave;
-  if (r >= R) return;
+  const bool live = r < R;
   float acc[kPart];
 #pragma unroll
   for (int j = 0; j < kPart; ++j) acc[j] = 0.f;
-  for (int k = lane; k < nK; k += 64) {
+  for (int k = lane; live && k < nK; k += 64) {
     const float* p = part + (r * nK + k) * kPart;
 #pragma unroll
     for (int j = 0; j < kPart; ++j) acc[j] += p[j];
   }
 #pragma unroll
   for (int j = 0; j < kPart; ++j) acc[j] = wave_sum(acc[j]);
-  if (lane != 0) return;
-  float raw[kOut];
+  if (lane == 0) {
 #pragma unroll
-  for (int j = 0; j < kOut; ++j) raw[j] = acc[j];
-  const float inv_rms = 1.f / sqrtf(acc[kOut] / (float)K + eps);
-  float s[kOut];
-  dyn_scaled(P, raw, inv_rms, s);
-  // Eq. 17: H_pre = sigmoid / (sum + eps)
-  float sg[4];
-#pragma unroll
-  for (int j = 0; j < 4; ++j) sg[j] = sigmoidf(s[j]);
-  const float den = sg[0] + sg[1] + sg[2] + sg[3] + eps;
-#pragma unroll
-  for (int j = 0; j < 4; ++j) o_pre.p[r * o_pre.stride + j] = sg[j] / den;
-  // Eq. 18: H_post = 2 sigmoid
-#pragma unroll
-  for (int j = 0; j < 4; ++j) o_post.p[r * o_post.stride + j] = 2.f * sigmoidf(s[4 + j]);
+    for (int j = 0; j < kPart; ++j) tot[wave][j] = acc[j];
+  }
+  __syncthreads();
+  // Epilogue on lanes 0..15 in 16-lane form: lane e owns H_res element e;
+  // lanes 0..3 also H_pre[e], lanes 4..7 H_post[e - 4].
+  if (!live || lane >= 16) return;
+  const float* t = tot[wave];
+  const int e = lane;
+  const int j = e & 3;
+  const bool is_pre = e < 4;
+  const float inv_rms = 1.f / sqrtf(t[kOut] / (float)K + eps);
+  const float raw_res = t[8 + e];
+  const float raw_pp = t[e & 7];
   // Eq. 19: H_res = Sinkhorn(|s_res| + eps)
-  float m[16];
-#pragma unroll
-  for (int j = 0; j < 16; ++j) m[j] = s[8 + j];
-  sk_forward(m, iters, eps);
-#pragma unroll
-  for (int j = 0; j < 16; ++j) o_res.p[r * o_res.stride + j] = m[j];
+  const float m = sk16_forward(inv_rms * *P.alpha_res * raw_res + P.bias_res[e], iters, eps);
+  o_res.p[r * o_res.stride + e] = m;
+  // Eq. 17: H_pre = sigmoid / (sum + eps); Eq. 18: H_post = 2 sigmoid
+  const float s_pp = inv_rms * (is_pre ? *P.alpha_pre : *P.alpha_post) * raw_pp +
+                     (is_pre ? P.bias_pre[j] : P.bias_post[j]);
+  const float sg = sigmoidf(s_pp);
+  const float den = sum_row16(sg) + eps;  // quad 0: the four H_pre sigmoids
+  if (is_pre) o_pre.p[r * o_pre.stride + j] = sg / den;
+  else if (e < 8) o_post.p[r * o_post.stride + j] = 2.f * sg;
   if (aux) {
-#pragma unroll
-    for (int j = 0; j < kOut; ++j) aux[r * kPart + j] = raw[j];
-    aux[r * kPart + kOut] = inv_rms;
+    aux[r * kPart + e] = t[e];
+    if (e < 8) aux[r * kPart + 16 + e] = t[16 + e];
+    if (e == 0) aux[r * kPart + kOut] = inv_rms;
   }
 }
 
@@ -177,82 +180,131 @@ __global__ __launch_bounds__(kThreads) void dynw_finalize_kernel(const float* __
 //   [25:49] g_scaled  (-> grad_bias)
 //   [49:52] per-group sum g_scaled * inv_rms * raw (-> grad_alpha)
 // Follows reference src/mhc/ops.py:138-216 with the Sinkhorn part of
-// _backward.py:29-262 (sgn(0) = 0).
+// _backward.py:30-262 (sgn(0) = 0).
+//
+// Four rows per 256-thread workgroup (R is the batch in the layer path, so
+// this is a latency problem).  In the layer path the upstream H_pre / H_res
+// gradients arrive as the weight-gradient pass's per-workgroup partials
+// part20[r][k][0:20] (4 H_pre, 16 H_res) over nblk workgroups: wave w sums row
+// w's partials (64 lanes in chunk order, 16-byte loads, then a fixed
+// butterfly).  The standalone op passes them as rows (g_pre [R,4],
+// g_res [R,16]).  Wave 0 then runs the four rows in 16-lane form: lane e of a
+// group owns H_res element e, lanes 0..3 also H_pre[e], lanes 4..7
+// H_post[e - 4].
+constexpr int kSkSlots = 32;  // Sinkhorn states kept in LDS per lane
+
 template <int = 0>
 __global__ __launch_bounds__(kThreads) void dynw_bwd_rows_kernel(const float* __restrict__ aux, DynParams P,
                                                                  InRow h_pre, InRow g_pre, InRow g_post,
-                                                                 InRow g_res, float* __restrict__ rowbuf,
-                                                                 int64_t R, int64_t K, int iters, float eps) {
-  const int64_t r = (int64_t)blockIdx.x * kThreads + threadIdx.x;
-  if (r >= R) return;
-  float raw[kOut];
+                                                                 InRow g_res, const float* __restrict__ part20,
+                                                                 int nblk, float* __restrict__ rowbuf, int64_t R,
+                                                                 int64_t K, int iters, float eps) {
+  __shared__ float slots[kSkSlots * 64];
+  __shared__ float red[4][20];
+  const int wave = threadIdx.x >> 6;
+  const int lane = threadIdx.x & 63;
+  if (part20) {
+    const int64_t rw = (int64_t)blockIdx.x * 4 + wave;
+    f32x4 acc[5];
 #pragma unroll
-  for (int j = 0; j < kOut; ++j) raw[j] = aux[r * kPart + j];
-  const float inv_rms = aux[r * kPart + kOut];
-  float s[kOut];
-  dyn_scaled(P, raw, inv_rms, s);
-  float gs[kOut];
-  // H_res: Sinkhorn backward w.r.t. scaled_res
-  {
-    float m[16], d[16];
+    for (int q = 0; q < 5; ++q) acc[q] = f32x4{0.f, 0.f, 0.f, 0.f};
+    if (rw < R) {
+#pragma unroll 4
+      for (int k = lane; k < nblk; k += 64) {
+        const f32x4* p = reinterpret_cast<const f32x4*>(part20 + (rw * nblk + k) * 20);
 #pragma unroll
-    for (int j = 0; j < 16; ++j) {
-      m[j] = s[8 + j];
-      d[j] = g_res.p ? g_res.p[r * g_res.stride + j] : 0.f;
+        for (int q = 0; q < 5; ++q) acc[q] += p[q];
+      }
     }
-    sk_backward<10>(m, d, iters, eps);
 #pragma unroll
-    for (int j = 0; j < 16; ++j) gs[8 + j] = d[j];
-  }
-  // H_post = 2 sigmoid: g * 2 sig (1 - sig)
+    for (int q = 0; q < 5; ++q) {
 #pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    const float sg = sigmoidf(s[4 + j]);
-    const float g = g_post.p ? g_post.p[r * g_post.stride + j] : 0.f;
-    gs[4 + j] = g * 2.f * sg * (1.f - sg);
-  }
-  // H_pre = sig / (sum sig + eps)
-  {
-    float sg[4], g[4], hp[4];
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      sg[j] = sigmoidf(s[j]);
-      g[j] = g_pre.p ? g_pre.p[r * g_pre.stride + j] : 0.f;
-      hp[j] = h_pre.p[r * h_pre.stride + j];
+      for (int c = 0; c < 4; ++c) {
+        const float v = wave_sum(acc[q][c]);
+        if (lane == 0) red[wave][4 * q + c] = v;
+      }
     }
-    const float den = sg[0] + sg[1] + sg[2] + sg[3] + eps;
-    const float dot = g[0] * hp[0] + g[1] * hp[1] + g[2] * hp[2] + g[3] * hp[3];
-#pragma unroll
-    for (int j = 0; j < 4; ++j) gs[j] = (g[j] - dot) / den * sg[j] * (1.f - sg[j]);
   }
-  const float al[3] = {*P.alpha_pre, *P.alpha_post, *P.alpha_res};
+  __syncthreads();
+  if (wave != 0) return;
+  const int e = lane & 15;
+  const int j = e & 3;
+  const int64_t r_grp = (int64_t)blockIdx.x * 4 + (lane >> 4);
+  const bool live = r_grp < R;
+  const int64_t r = live ? r_grp : R - 1;  // idle groups redo the last row and store nothing
+  const float gpre = part20 ? red[lane >> 4][j] : (g_pre.p ? g_pre.p[r * g_pre.stride + j] : 0.f);
+  const float gres = part20 ? red[lane >> 4][4 + e] : (g_res.p ? g_res.p[r * g_res.stride + e] : 0.f);
+  const float gpost = g_post.p ? g_post.p[r * g_post.stride + j] : 0.f;
+  const float* a = aux + r * kPart;
+  const float inv_rms = a[kOut];
+  const float ar = *P.alpha_res;
+  const float raw_res = a[8 + e];
+  const float raw_pp = a[e & 7];
+  // H_res = Sinkhorn(|s_res| + eps): gradient w.r.t. s_res.
+  const float gs_res =
+      sk16_backward<kSkSlots>(inv_rms * ar * raw_res + P.bias_res[e], gres, iters, eps, slots + lane, 64);
+  // H_pre = sigmoid / (sum + eps) on lanes 0..3, H_post = 2 sigmoid on lanes 4..7.
+  const bool is_pre = (e & 4) == 0;
+  const float al_pp = is_pre ? *P.alpha_pre : *P.alpha_post;
+  const float sg = sigmoidf(inv_rms * al_pp * raw_pp + (is_pre ? P.bias_pre[j] : P.bias_post[j]));
+  const float hp = h_pre.p[r * h_pre.stride + j];
+  const float den = sum_row16(sg) + eps;   // quad 0: sum of the H_pre sigmoids
+  const float dot = sum_row16(gpre * hp);  // quad 0: <g_pre, H_pre>
+  const float gs_pp = is_pre ? (gpre - dot) / den * sg * (1.f - sg) : gpost * 2.f * sg * (1.f - sg);
+  const bool has_pp = e < 8;
+  // Group sums for grad_alpha and the rms path.
+  const float ga_res = sum_all16(gs_res * inv_rms * raw_res);
+  const float ga_pp = sum_row16(has_pp ? gs_pp * inv_rms * raw_pp : 0.f);  // lane 0: pre, lane 4: post
+  const float g_inv = sum_all16(gs_res * ar * raw_res + (has_pp ? gs_pp * al_pp * raw_pp : 0.f));
+  if (!live) return;
   float* rb = rowbuf + r * kRow;
-  float ga[3] = {0.f, 0.f, 0.f};
-  float g_inv = 0.f;
-#pragma unroll
-  for (int j = 0; j < kOut; ++j) {
-    const int grp = j < 4 ? 0 : (j < 8 ? 1 : 2);
-    rb[j] = gs[j] * inv_rms * al[grp];
-    rb[25 + j] = gs[j];
-    ga[grp] += gs[j] * inv_rms * raw[j];
-    g_inv += gs[j] * al[grp] * raw[j];
+  rb[8 + e] = gs_res * inv_rms * ar;
+  rb[33 + e] = gs_res;
+  if (has_pp) {
+    rb[e] = gs_pp * inv_rms * al_pp;
+    rb[25 + e] = gs_pp;
   }
   // inv_rms = 1/rms, rms = sqrt(sum x^2 / K + eps): d rms / d x = x / (K rms)
-  const float grad_rms = g_inv * (-inv_rms * inv_rms);
-  rb[24] = grad_rms * inv_rms / (float)K;
-#pragma unroll
-  for (int g = 0; g < 3; ++g) rb[49 + g] = ga[g];
+  if (e == 0) {
+    rb[24] = g_inv * (-inv_rms * inv_rms) * inv_rms / (float)K;
+    rb[49] = ga_pp;
+    rb[51] = ga_res;
+  }
+  if (e == 4) rb[50] = ga_pp;
 }
 
-// Thread per k.  grad_x (f32) rows have stride K.
+// Thread per k: grad_x[r,k] = grad_raw[r,:] . phi[k,:] + coef[r] x[r,k] (f32,
+// rows of stride K) and grad_phi[k,:] = sum_r x[r,k] grad_raw[r,:].
+// Workgroup 0 also sums the per-row records into grad_bias [24] and
+// grad_alpha [3] (threads stride over rows, then a fixed-order block sum).
 template <typename TX>
 __global__ __launch_bounds__(kThreads) void dynw_bwd_wide_kernel(const TX* __restrict__ x,
                                                                  const float* __restrict__ phi,
                                                                  const float* __restrict__ rowbuf,
                                                                  float* __restrict__ gx, float* __restrict__ gphi,
-                                                                 int64_t R, int64_t K, bool phi_vec) {
+                                                                 float* __restrict__ gbias,
+                                                                 float* __restrict__ galpha, int64_t R, int64_t K,
+                                                                 bool phi_vec) {
+  if (blockIdx.x == 0 && (gbias || galpha)) {
+    __shared__ float lds[4 * 27];
+    float acc[27];
+#pragma unroll
+    for (int i = 0; i < 27; ++i) acc[i] = 0.f;
+    for (int64_t r = threadIdx.x; r < R; r += kThreads) {
+      const float* rb = rowbuf + r * kRow;
+#pragma unroll
+      for (int i = 0; i < 27; ++i) acc[i] += rb[25 + i];
+    }
+    block_sum<27>(acc, lds);
+    if (threadIdx.x == 0) {
+#pragma unroll
+      for (int j = 0; j < kOut; ++j) if (gbias) gbias[j] = acc[j];
+#pragma unroll
+      for (int g = 0; g < 3; ++g) if (galpha) galpha[g] = acc[24 + g];
+    }
+  }
   const int64_t k = (int64_t)blockIdx.x * kThreads + threadIdx.x;
-  if (k >= K) return;
+  if (k >= K || (!gx && !gphi)) return;
   float ph[kOut], gp[kOut];
   load_phi_row(phi, k, phi_vec, ph);
 #pragma unroll
@@ -272,29 +324,6 @@ __global__ __launch_bounds__(kThreads) void dynw_bwd_wide_kernel(const TX* __res
     float* o = gphi + k * kOut;
 #pragma unroll
     for (int j = 0; j < kOut; ++j) o[j] = gp[j];
-  }
-}
-
-// Single workgroup: grad_bias[24], grad_alpha[3] summed over rows in a fixed order.
-template <int = 0>
-__global__ __launch_bounds__(kThreads) void dynw_bwd_sum_kernel(const float* __restrict__ rowbuf, int64_t R,
-                                                                float* __restrict__ gbias,
-                                                                float* __restrict__ galpha) {
-  __shared__ float lds[4 * 27];
-  float acc[27];
-#pragma unroll
-  for (int i = 0; i < 27; ++i) acc[i] = 0.f;
-  for (int64_t r = threadIdx.x; r < R; r += kThreads) {
-    const float* rb = rowbuf + r * kRow;
-#pragma unroll
-    for (int i = 0; i < 27; ++i) acc[i] += rb[25 + i];
-  }
-  block_sum<27>(acc, lds);
-  if (threadIdx.x == 0) {
-#pragma unroll
-    for (int j = 0; j < kOut; ++j) if (gbias) gbias[j] = acc[j];
-#pragma unroll
-    for (int g = 0; g < 3; ++g) if (galpha) galpha[g] = acc[24 + g];
   }
 }
 

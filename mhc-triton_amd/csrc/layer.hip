@@ -79,38 +79,43 @@ static int branch_input_any(const void* H, int dtype, const float* w, void* bi, 
 
 // Static weights (module.py:108-117), replicated for every batch row:
 // H_post = sigmoid(b_post), H_pre = sigmoid(b_pre)/(sum + 1e-8),
-// H_res = Sinkhorn(H_res_base, iters, eps = 1e-8).
+// H_res = Sinkhorn(H_res_base, iters, eps = 1e-8).  The 24 values are the same
+// for every row: lanes 0..15 of wave 0 form them (16-lane Sinkhorn) in LDS,
+// then the workgroup writes its rows.
 __global__ __launch_bounds__(kThreads) void static_weights_kernel(const float* __restrict__ bpre,
                                                                   const float* __restrict__ bpost,
                                                                   const float* __restrict__ bres,
                                                                   float* __restrict__ w, int64_t B, int iters) {
-  const int64_t b = (int64_t)blockIdx.x * kThreads + threadIdx.x;
-  if (b >= B) return;
-  float* o = w + b * kOut;
-  float sg[4];
-#pragma unroll
-  for (int j = 0; j < 4; ++j) sg[j] = sigmoidf(bpre[j]);
-  const float den = sg[0] + sg[1] + sg[2] + sg[3] + 1e-8f;
-#pragma unroll
-  for (int j = 0; j < 4; ++j) o[j] = sg[j] / den;
-#pragma unroll
-  for (int j = 0; j < 4; ++j) o[4 + j] = sigmoidf(bpost[j]);
-  float m[16];
-#pragma unroll
-  for (int j = 0; j < 16; ++j) m[j] = bres[j];
-  sk_forward(m, iters, 1e-8f);
-#pragma unroll
-  for (int j = 0; j < 16; ++j) o[8 + j] = m[j];
+  __shared__ float vals[kOut];
+  if (threadIdx.x < 16) {
+    const int e = threadIdx.x;
+    const int j = e & 3;
+    vals[8 + e] = sk16_forward(bres[e], iters, 1e-8f);
+    const bool is_pre = (e & 4) == 0;
+    const float sg = sigmoidf(is_pre ? bpre[j] : bpost[j]);
+    const float den = sum_row16(sg) + 1e-8f;  // quad 0: the four H_pre sigmoids
+    if (e < 4) vals[j] = sg / den;
+    else if (e < 8) vals[4 + j] = sg;
+  }
+  __syncthreads();
+  const int64_t b0 = (int64_t)blockIdx.x * kThreads;
+  for (int i = threadIdx.x; i < kThreads * kOut; i += kThreads) {
+    const int64_t b = b0 + i / kOut;
+    if (b < B) w[b0 * kOut + i] = vals[i % kOut];
+  }
 }
 
 // Backward of static_weights_kernel through the batch expand:
 // every cotangent is first summed over b (fixed order), then pushed through
-// sigmoid / normalise / Sinkhorn once (the Sinkhorn VJP is linear in the cotangent).
+// sigmoid / normalise / Sinkhorn once (the Sinkhorn VJP is linear in the
+// cotangent), on lanes 0..15 in 16-lane form.
 __global__ __launch_bounds__(kThreads) void static_weights_bwd_kernel(
     const float* __restrict__ bpre, const float* __restrict__ bpost, const float* __restrict__ bres,
     const float* __restrict__ w, const float* __restrict__ dpre, const float* __restrict__ dpost,
     const float* __restrict__ dres, float* __restrict__ gbias, int64_t B, int iters) {
   __shared__ float lds[4 * kOut];
+  __shared__ float tot[kOut];
+  __shared__ float slots[kSkSlots * 16];
   float acc[kOut];
 #pragma unroll
   for (int j = 0; j < kOut; ++j) acc[j] = 0.f;
@@ -125,31 +130,21 @@ __global__ __launch_bounds__(kThreads) void static_weights_bwd_kernel(
     for (int j = 0; j < 16; ++j) acc[8 + j] += dres[b * 16 + j];
   }
   block_sum<kOut>(acc, lds);
-  if (threadIdx.x != 0) return;
-  // H_pre
-  float sg[4];
+  if (threadIdx.x == 0) {
 #pragma unroll
-  for (int j = 0; j < 4; ++j) sg[j] = sigmoidf(bpre[j]);
-  const float den = sg[0] + sg[1] + sg[2] + sg[3] + 1e-8f;
-  const float dot = acc[0] * w[0] + acc[1] * w[1] + acc[2] * w[2] + acc[3] * w[3];
-#pragma unroll
-  for (int j = 0; j < 4; ++j) gbias[j] = (acc[j] - dot) / den * sg[j] * (1.f - sg[j]);
-  // H_post
-#pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    const float s = sigmoidf(bpost[j]);
-    gbias[4 + j] = acc[4 + j] * s * (1.f - s);
+    for (int j = 0; j < kOut; ++j) tot[j] = acc[j];
   }
-  // H_res
-  float m[16], d[16];
-#pragma unroll
-  for (int j = 0; j < 16; ++j) {
-    m[j] = bres[j];
-    d[j] = acc[8 + j];
-  }
-  sk_backward(m, d, iters, 1e-8f);
-#pragma unroll
-  for (int j = 0; j < 16; ++j) gbias[8 + j] = d[j];
+  __syncthreads();
+  if (threadIdx.x >= 16) return;
+  const int e = threadIdx.x;
+  const int j = e & 3;
+  gbias[8 + e] = sk16_backward<kSkSlots>(bres[e], tot[8 + e], iters, 1e-8f, slots + e, 16);
+  const bool is_pre = (e & 4) == 0;
+  const float sg = sigmoidf(is_pre ? bpre[j] : bpost[j]);
+  const float den = sum_row16(sg) + 1e-8f;
+  const float dot = sum_row16(tot[j] * w[j]);  // quad 0: <g_pre, H_pre>
+  if (e < 4) gbias[j] = (tot[j] - dot) / den * sg * (1.f - sg);
+  else if (e < 8) gbias[4 + j] = tot[4 + j] * sg * (1.f - sg);
 }
 
 // Pass B (REDUCE only), pass C (WRITE_DH + HAS_GX) and the static pass BC
@@ -268,7 +263,7 @@ extern "C" int mhc_layer_add_forward(const void* H, int dtype_h, const void* bra
       return for_batch_chunks(B, [&](int64_t b0, int64_t nb) {
         const Geom g = make_geom<W, kLU>(S, D, b0);
         mix_fwd_kernel<TH, TB, W, kLU, false, true, true, kNtStores>
-            <<<dim3(g.ntiles, nb), kThreads, occupancy_lds(2), st>>>(
+            <<<dim3(g.ntiles, nb), kThreads, occupancy_lds(3), st>>>(
             (const TH*)H, (const TB*)branch_output, WRow{nullptr, 0}, WRow{w + 8, kOut}, WRow{w + 4, kOut},
             nullptr, (TH*)H_new, g);
         return hip_status(hipGetLastError(), "layer add forward launch");
@@ -313,8 +308,6 @@ extern "C" int mhc_layer_dynamic_backward(const void* H, int dtype, const void* 
   LAYER_WS_CHECK("layer_dynamic_backward");
   hipStream_t st = (hipStream_t)stream;
   float* part = (float*)(wsb + L.red_part);
-  float* dpre = (float*)(wsb + L.dpre);
-  float* dres = (float*)(wsb + L.dres);
   float* rowbuf = (float*)(wsb + L.rowbuf);
   float* gx = (float*)(wsb + L.gx);
   // Pass B: dH_pre, dH_res.
@@ -324,21 +317,17 @@ extern "C" int mhc_layer_dynamic_backward(const void* H, int dtype, const void* 
                                                    &nblk, st);
   });
   if (rc) return rc;
-  reduce_split_kernel<20, 4><<<dim3((unsigned)B), kThreads, 0, st>>>(part, dpre, dres, (int)nblk);
-  if ((rc = hip_status(hipGetLastError(), "layer pass B reduce launch"))) return rc;
-  // Weights backward.
+  // Weights backward: the rows kernel sums the pass-B partials itself; the wide
+  // kernel also sums grad_bias / grad_alpha.
   DynParams P{H_pre_base, H_post_base, H_res_base, alpha_pre, alpha_post, alpha_res};
   const int64_t K = 4 * D;
-  dynw_bwd_rows_kernel<><<<dim3((unsigned)((B + kThreads - 1) / kThreads)), kThreads, 0, st>>>(
-      aux, P, InRow{w, kOut}, InRow{dpre, 4}, InRow{dH_post, 4}, InRow{dres, 16}, rowbuf, B, K, iters, eps);
+  dynw_bwd_rows_kernel<><<<dim3((unsigned)((B + 3) / 4)), kThreads, 0, st>>>(
+      aux, P, InRow{w, kOut}, InRow{nullptr, 0}, InRow{dH_post, 4}, InRow{nullptr, 0}, part, (int)nblk, rowbuf, B,
+      K, iters, eps);
   if ((rc = hip_status(hipGetLastError(), "layer weights backward rows launch"))) return rc;
-  if (K > 0) {
-    dynw_bwd_wide_kernel<float><<<dim3((unsigned)((K + kThreads - 1) / kThreads)), kThreads, 0, st>>>(
-        x, phi, rowbuf, dH ? gx : nullptr, grad_phi, B, K, aligned16(phi));
-    if ((rc = hip_status(hipGetLastError(), "layer weights backward wide launch"))) return rc;
-  }
-  dynw_bwd_sum_kernel<><<<1, kThreads, 0, st>>>(rowbuf, B, grad_bias, grad_alpha);
-  if ((rc = hip_status(hipGetLastError(), "layer weights backward sum launch"))) return rc;
+  dynw_bwd_wide_kernel<float><<<dim3(K > 0 ? (unsigned)((K + kThreads - 1) / kThreads) : 1u), kThreads, 0, st>>>(
+      x, phi, rowbuf, dH ? gx : nullptr, grad_phi, grad_bias, grad_alpha, B, K, aligned16(phi));
+  if ((rc = hip_status(hipGetLastError(), "layer weights backward wide launch"))) return rc;
   if (!dH || S * D == 0) return MHC_OK;
   // Pass C: dH.
   return MHC_DISPATCH_DTYPE(dtype, [&] {

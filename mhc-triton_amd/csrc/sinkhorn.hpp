@@ -125,4 +125,84 @@ __device__ __forceinline__ void sk_backward(const float (&mat)[16], float (&d)[1
   }
 }
 
+// ---------------------------------------------------------------------------
+// 16-lane form, for the latency-bound per-row kernels (a handful of matrices,
+// one per batch row): one matrix is spread over 16 consecutive lanes, lane
+// e = 4 i + j holding P[i][j].  Row sums are two quad-permute DPP adds, column
+// sums two row-rotate DPP adds (rotate by 8, then by 4, within the 16 lanes),
+// so a round is about 10 dependent instructions instead of about 70 on one
+// lane.  Both trees add the same pairs in every lane, so all lanes of a row
+// (column) see bit-identical sums.  All 16 lanes of a group must be active.
+// The serial one-matrix-per-lane form above stays the throughput choice for
+// large batches of matrices (fewer instructions per matrix).
+// ---------------------------------------------------------------------------
+template <int CTRL>
+__device__ __forceinline__ float dpp(float v) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, 0xF, 0xF, false));
+}
+
+constexpr int kDppQuadXor1 = 0xB1;  // quad_perm [1,0,3,2]
+constexpr int kDppQuadXor2 = 0x4E;  // quad_perm [2,3,0,1]
+constexpr int kDppRowRor4 = 0x124;  // row_ror:4
+constexpr int kDppRowRor8 = 0x128;  // row_ror:8
+
+// Sum over j of P[i][j] (the 4 lanes of a quad).
+__device__ __forceinline__ float sum_row16(float v) {
+  v += dpp<kDppQuadXor1>(v);
+  return v + dpp<kDppQuadXor2>(v);
+}
+
+// Sum over i of P[i][j] (lanes e, e^4, e^8, e^12 of the 16-lane row).
+__device__ __forceinline__ float sum_col16(float v) {
+  v += dpp<kDppRowRor8>(v);
+  return v + dpp<kDppRowRor4>(v);
+}
+
+__device__ __forceinline__ float sum_all16(float v) { return sum_col16(sum_row16(v)); }
+
+__device__ __forceinline__ float sk16_round(float m, float eps) {
+  m *= fast_rcp(sum_row16(m) + eps);
+  return m * fast_rcp(sum_col16(m) + eps);
+}
+
+__device__ __forceinline__ float sk16_forward(float m, int iters, float eps) {
+  m = __builtin_fabsf(m) + eps;
+  for (int t = 0; t < iters; ++t) m = sk16_round(m, eps);
+  return m;
+}
+
+// Gradient w.r.t. the state m entering a round, given the gradient d w.r.t.
+// the state leaving it (same normalisation backward as sk_round_backward).
+__device__ __forceinline__ float sk16_round_backward(float m, float d, float eps) {
+  const float r = fast_rcp(sum_row16(m) + eps);
+  const float mr = m * r;
+  const float c = fast_rcp(sum_col16(mr) + eps);
+  const float mc = mr * c;
+  d = (d - sum_col16(d * mc)) * c;
+  return (d - sum_row16(d * mr)) * r;
+}
+
+// dM for one matrix in 16-lane form.  The forward states are kept in `slot`
+// (this lane's LDS slots, `stride` floats apart): every state when
+// iters <= NSLOT, otherwise every L-th state with the rest recomputed from the
+// nearest kept one (the recomputed states are bit-identical to the forward's).
+template <int NSLOT>
+__device__ __forceinline__ float sk16_backward(float mat, float d, int iters, float eps, float* slot, int stride) {
+  const int L = iters <= NSLOT ? 1 : (iters + NSLOT - 1) / NSLOT;
+  float m = __builtin_fabsf(mat) + eps;
+  for (int t = 0; t < iters; ++t) {
+    if (t % L == 0) slot[(t / L) * stride] = m;
+    m = sk16_round(m, eps);
+  }
+  for (int t = iters - 1; t >= 0; --t) {
+    const int k = t / L;
+    float st = slot[k * stride];
+    for (int u = k * L; u < t; ++u) st = sk16_round(st, eps);
+    d = sk16_round_backward(st, d, eps);
+  }
+  // d|M|/dM = sgn(M), sgn(0) = 0.
+  const float sg = mat > 0.f ? 1.f : (mat < 0.f ? -1.f : 0.f);
+  return d * sg;
+}
+
 }  // namespace mhc

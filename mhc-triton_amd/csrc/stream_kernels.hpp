@@ -22,7 +22,7 @@ namespace mhc {
 // 160 KiB LDS per CU).  HBM throughput of these kernels peaks with roughly
 // 24-40 KiB of loads in flight per CU; more resident workgroups lower it (the
 // closure forward, 5 loads per lane, runs at 73% of 8 TB/s with 8 workgroups
-// per CU and at 77% with 2).  The kernels use almost no LDS, so the cap is set
+// per CU and at 75-77% with 2-3; the closure backward at 69% and 74%).  The kernels use almost no LDS, so the cap is set
 // by reserving dynamic LDS at launch: at most `wg_per_cu` workgroups fit on a
 // CU.  Streamed outputs are written with non-temporal stores (NT = 2), which
 // lifts every write-heavy kernel by 3-6%.
