@@ -132,6 +132,14 @@ extern "C" int mhc_stream_mix_backward(const void* d_branch_input, const void* d
                                        size_t workspace_bytes, mhc_stream_t stream) {
   if (int rc = check_bsd("stream_mix_backward", B, S, D)) return rc;
   if (B == 0) return MHC_OK;
+  if (S * D == 0) {  // empty sums: zero weight gradients, dH is empty
+    if (!dH_pre || !dH_res) {
+      set_error("stream_mix_backward: null pointer");
+      return MHC_ERR_ARG;
+    }
+    if (int rc = fill_zero(dH_pre, B * 4, (hipStream_t)stream)) return rc;
+    return fill_zero(dH_res, B * 16, (hipStream_t)stream);
+  }
   if (!d_branch_input || !dH_residual || !H || !H_pre || !H_res || !dH || !dH_pre || !dH_res) {
     set_error("stream_mix_backward: null pointer");
     return MHC_ERR_ARG;
@@ -182,6 +190,13 @@ extern "C" int mhc_add_residual_backward(const void* dH_new, int dtype_h, const 
                                          mhc_stream_t stream) {
   if (int rc = check_bsd("add_residual_backward", B, S, D)) return rc;
   if (B == 0) return MHC_OK;
+  if (S * D == 0) {  // empty sums: zero dH_post, d_branch_output is empty
+    if (!dH_post) {
+      set_error("add_residual_backward: null pointer");
+      return MHC_ERR_ARG;
+    }
+    return fill_zero(dH_post, B * 4, (hipStream_t)stream);
+  }
   if (!dH_new || !branch_output || !H_post || !d_branch_output || !dH_post) {
     set_error("add_residual_backward: null pointer");
     return MHC_ERR_ARG;

@@ -239,3 +239,40 @@ def test_mean_pool_matches_oracle():
         x = mean_pool(H)
         assert x.dtype == torch.float32
         assert rel_err(to_np(x), O.mean_pool(to_np(H))) < 1e-5
+
+
+# --------------------------------------------------------------------------- empty inputs
+
+@pytest.mark.parametrize("B,S", [(0, 8), (2, 0)])
+def test_stream_ops_empty(B, S):
+    """Zero-size batch or sequence: empty outputs, zero weight gradients, no launch errors."""
+    import mhc
+
+    D = 16
+    H = torch.zeros((B, S, 4, D), device=DEV, requires_grad=True)
+    pre = torch.full((B, 4), 0.25, device=DEV, requires_grad=True)
+    res = torch.full((B, 4, 4), 0.25, device=DEV, requires_grad=True)
+    bi, hr = mhc.fused_stream_mix(H, pre, res)
+    assert bi.shape == (B, S, D) and hr.shape == (B, S, 4, D)
+    bo = torch.zeros((B, S, D), device=DEV, requires_grad=True)
+    post = torch.ones((B, 4), device=DEV, requires_grad=True)
+    H_new = mhc.fused_add_residual(hr, bo, post)
+    (H_new.sum() + bi.sum()).backward()
+    torch.cuda.synchronize()
+    assert H.grad.shape == H.shape and float(pre.grad.abs().sum()) == 0.0
+    assert float(res.grad.abs().sum()) == 0.0 and float(post.grad.abs().sum()) == 0.0
+
+
+def test_dynamic_weights_zero_rows():
+    import mhc
+
+    K = 32
+    x = torch.zeros((0, K), device=DEV, requires_grad=True)
+    phi = torch.randn((K, 24), device=DEV, requires_grad=True)
+    bias = torch.randn(24, device=DEV, requires_grad=True)
+    al = [torch.tensor([0.1], device=DEV, requires_grad=True) for _ in range(3)]
+    H_pre, H_post, H_res = mhc.fused_dynamic_weights(x, phi, bias, *al)
+    assert H_pre.shape == (0, 4) and H_res.shape == (0, 4, 4)
+    (H_pre.sum() + H_post.sum() + H_res.sum()).backward()
+    torch.cuda.synchronize()
+    assert float(phi.grad.abs().sum()) == 0.0 and float(bias.grad.abs().sum()) == 0.0
