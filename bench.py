@@ -57,6 +57,14 @@ WORKLOADS = {
 #       gradients and dH (19).
 ALGO_UNITS = {True: (18, 24), False: (14, 19)}
 
+# HBM bytes one launch of the closure-forward kernel moves, measured with two
+# rocprofv3 counter passes over this bench (`--pmc FETCH_SIZE`, then
+# `--pmc WRITE_SIZE`), each scaled by what the counter reads for a 512 MiB
+# device copy (`bench.py --calibrate-copy`: FETCH_SIZE x2.0, WRITE_SIZE x1.0 on
+# MI355X).  Against the 1,207,959,552 algorithmic bytes: +0.03%.  None where
+# not measured.
+MEASURED_TRAFFIC = {"config3": 1208302601}
+
 
 def _log(msg: str) -> None:
     print(msg, file=sys.stderr, flush=True)
@@ -70,7 +78,26 @@ def _parse():
     ap.add_argument("--workload", default="config3", choices=sorted(WORKLOADS))
     ap.add_argument("--cpu-seconds", type=float, default=12.0,
                     help="target CPU time of the cpu_baseline sample (0 disables it)")
+    ap.add_argument("--calibrate-copy", action="store_true",
+                    help="only run 3 plain device copies of 512 MiB (the known-size kernel that scales "
+                         "rocprofv3 FETCH_SIZE / WRITE_SIZE readings into bytes) and exit")
     return ap.parse_args()
+
+
+COPY_BYTES = 512 << 20
+
+
+def _calibrate_copy() -> int:
+    import torch
+
+    src = torch.ones(COPY_BYTES // 2, dtype=torch.bfloat16, device="cuda:0")
+    dst = torch.empty_like(src)
+    for _ in range(3):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    print(json.dumps({"calibration": "device copy", "bytes_read": COPY_BYTES, "bytes_written": COPY_BYTES,
+                      "launches": 3}), flush=True)
+    return 0
 
 
 def _build_inputs(cfg, dev):
@@ -226,6 +253,8 @@ def main() -> int:
     if not torch.cuda.is_available():
         print("bench.py: no ROCm GPU visible", file=sys.stderr)
         return 1
+    if args.calibrate_copy:
+        return _calibrate_copy()
     from mhc import _lib
 
     _lib.load()  # fails loudly when the HIP library is not built
@@ -276,7 +305,7 @@ def main() -> int:
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
             "frac": round(add_gbs / HBM_PEAK_GBS, 4),
-            "traffic": None,
+            "traffic": MEASURED_TRAFFIC.get(args.workload),
         },
         "layer_roofline": {
             "algorithmic_bytes_per_step": step_bytes,
