@@ -32,14 +32,53 @@ static DynPlan dyn_plan(int64_t R, int64_t K) {
 
 static size_t align256(size_t v) { return (v + 255) & ~(size_t)255; }
 
+// MFMA plan for bf16 x with many rows: waves of kMfmaTiles 32-row tiles, 4
+// waves per workgroup, and the K steps (16 k each) split into nK chunks so
+// that about 512 workgroups (2 per CU) stream x; at least 16 steps per chunk.
+constexpr int64_t kMfmaMinRows = 64;
+constexpr int kMfmaTiles = 4;
+constexpr int kMfmaUnroll = 2;
+constexpr int64_t kMfmaWgRows = 4 * 32 * kMfmaTiles;
+
+struct MfmaPlan {
+  int64_t nsteps;  // K / 16
+  int64_t spc;     // steps per chunk
+  int nK;          // chunks
+  size_t part_bytes, packed_bytes;
+};
+
+static bool mfma_shape_ok(int64_t R, int64_t K) { return R >= kMfmaMinRows && K > 0 && K % 16 == 0; }
+
+static MfmaPlan mfma_plan(int64_t R, int64_t K) {
+  MfmaPlan p;
+  p.nsteps = K / 16;
+  const int64_t wg_rows = (R + kMfmaWgRows - 1) / kMfmaWgRows;
+  int64_t nk = (512 + wg_rows - 1) / wg_rows;
+  const int64_t max_nk = p.nsteps / 16 > 0 ? p.nsteps / 16 : 1;
+  if (nk > max_nk) nk = max_nk;
+  if (nk < 1) nk = 1;
+  p.spc = (p.nsteps + nk - 1) / nk;
+  p.nK = (int)((p.nsteps + p.spc - 1) / p.spc);
+  p.part_bytes = align256((size_t)R * p.nK * kPart * sizeof(float));
+  p.packed_bytes = (size_t)p.nsteps * 3 * 64 * 16;
+  return p;
+}
+
 }  // namespace mhc
 
 using namespace mhc;
 
+// The largest of the two plans (the dtype and alignment that pick the plan are
+// not arguments of the query).
 extern "C" size_t mhc_dynamic_weights_workspace_bytes(int64_t R, int64_t K) {
   if (R <= 0) return 0;
   const DynPlan p = dyn_plan(R, K);
-  return align256((size_t)R * p.nK * kPart * sizeof(float));
+  size_t need = align256((size_t)R * p.nK * kPart * sizeof(float));
+  if (mfma_shape_ok(R, K)) {
+    const MfmaPlan m = mfma_plan(R, K);
+    if (m.part_bytes + m.packed_bytes > need) need = m.part_bytes + m.packed_bytes;
+  }
+  return need;
 }
 
 extern "C" int mhc_dynamic_weights_forward(const void* x, int dtype_x, const float* phi, const float* bias,
@@ -60,18 +99,34 @@ extern "C" int mhc_dynamic_weights_forward(const void* x, int dtype_x, const flo
                                mhc_dynamic_weights_workspace_bytes(R, K)))
     return rc;
   hipStream_t st = (hipStream_t)stream;
-  const DynPlan p = dyn_plan(R, K);
   float* part = (float*)workspace;
-  const bool phi_vec = aligned16(phi);
-  int rc = MHC_DISPATCH_DTYPE(dtype_x, [&] {
-    dynw_partial_kernel<T, kRT><<<dim3((unsigned)((R + kRT - 1) / kRT), p.nK), kThreads, 0, st>>>(
-        (const T*)x, phi, part, R, K, p.nK, p.KC, phi_vec);
-    return hip_status(hipGetLastError(), "dynamic_weights_forward partial launch");
-  });
-  if (rc) return rc;
+  int nK = 0;
+  if (dtype_x == MHC_DTYPE_BF16 && mfma_shape_ok(R, K) && aligned16(x)) {
+    // bf16 rows in bulk: the projection on MFMA (HBM-bound instead of VALU-bound).
+    const MfmaPlan m = mfma_plan(R, K);
+    u32x4* packed = (u32x4*)((char*)workspace + m.part_bytes);
+    dynw_pack_phi_kernel<><<<dim3((unsigned)((m.nsteps * 64 + kThreads - 1) / kThreads)), kThreads, 0, st>>>(
+        phi, packed, m.nsteps);
+    if (int rc = hip_status(hipGetLastError(), "dynamic_weights_forward pack launch")) return rc;
+    dynw_mfma_kernel<kMfmaTiles, kMfmaUnroll>
+        <<<dim3((unsigned)((R + kMfmaWgRows - 1) / kMfmaWgRows), (unsigned)m.nK), kThreads, 0, st>>>(
+        (const __bf16*)x, packed, part, R, K, m.nK, m.spc);
+    if (int rc = hip_status(hipGetLastError(), "dynamic_weights_forward mfma launch")) return rc;
+    nK = m.nK;
+  } else {
+    const DynPlan p = dyn_plan(R, K);
+    const bool phi_vec = aligned16(phi);
+    int rc = MHC_DISPATCH_DTYPE(dtype_x, [&] {
+      dynw_partial_kernel<T, kRT><<<dim3((unsigned)((R + kRT - 1) / kRT), p.nK), kThreads, 0, st>>>(
+          (const T*)x, phi, part, R, K, p.nK, p.KC, phi_vec);
+      return hip_status(hipGetLastError(), "dynamic_weights_forward partial launch");
+    });
+    if (rc) return rc;
+    nK = p.nK;
+  }
   DynParams P{bias, bias + 4, bias + 8, alpha_pre, alpha_post, alpha_res};
   dynw_finalize_kernel<><<<dim3((unsigned)((R + 3) / 4)), kThreads, 0, st>>>(
-      part, p.nK, R, K, P, OutRow{H_pre, 4}, OutRow{H_post, 4}, OutRow{H_res, 16}, aux, iters, eps);
+      part, nK, R, K, P, OutRow{H_pre, 4}, OutRow{H_post, 4}, OutRow{H_res, 16}, aux, iters, eps);
   return hip_status(hipGetLastError(), "dynamic_weights_forward finalize launch");
 }
 

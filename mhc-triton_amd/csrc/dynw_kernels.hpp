@@ -94,6 +94,137 @@ __global__ __launch_bounds__(kThreads) void dynw_partial_kernel(const TX* __rest
   }
 }
 
+// ---------------------------------------------------------------------------
+// MFMA projection for many bf16 rows (the standalone op at R = tokens): the
+// [R, K] x [K, 24] product on v_mfma_f32_32x32x16_bf16.  Fragment layout of
+// that instruction (gfx950, checked on the device):
+//   A: lane l, element j -> A[l % 32][8 (l / 32) + j]          (x rows)
+//   B: lane l, element j -> B[8 (l / 32) + j][l % 32]          (phi columns)
+//   D: lane l, element i -> D[8 (i / 4) + 4 (l / 32) + i % 4][l % 32]
+// phi (fp32) is split into three bf16 parts, phi = hi + mid + lo +
+// O(2^-27 |phi|), and all three are applied, so the projection keeps fp32
+// accuracy (two parts leave 2^-18, which the 20-round Sinkhorn of H_res
+// amplifies to ~1e-4 relative at K = 16384); columns 24..31 of B are zero.
+// dynw_pack_phi_kernel writes the fragments once per call in the exact order
+// the waves read them: packed[(s * 3 + h) * 64 + lane] (16 bytes) for K step
+// s (16 k values) and part h.
+// ---------------------------------------------------------------------------
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+
+template <int = 0>
+__global__ __launch_bounds__(kThreads) void dynw_pack_phi_kernel(const float* __restrict__ phi,
+                                                                 u32x4* __restrict__ packed, int64_t nsteps) {
+  const int64_t t = (int64_t)blockIdx.x * kThreads + threadIdx.x;  // (step, lane)
+  if (t >= nsteps * 64) return;
+  const int64_t s = t >> 6;
+  const int lane = (int)(t & 63);
+  const int col = lane & 31;
+  const int64_t k0 = s * 16 + (lane >> 5) * 8;
+  bf16x8 hi, mid, lo;
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    const float v = col < kOut ? phi[(k0 + j) * kOut + col] : 0.f;
+    const __bf16 h = (__bf16)v;
+    const float r1 = v - (float)h;  // exact in fp32
+    const __bf16 m = (__bf16)r1;
+    hi[j] = h;
+    mid[j] = m;
+    lo[j] = (__bf16)(r1 - (float)m);
+  }
+  packed[(s * 3) * 64 + lane] = __builtin_bit_cast(u32x4, hi);
+  packed[(s * 3 + 1) * 64 + lane] = __builtin_bit_cast(u32x4, mid);
+  packed[(s * 3 + 2) * 64 + lane] = __builtin_bit_cast(u32x4, lo);
+}
+
+// One wave per RT 32-row tiles and one K chunk: each K step loads the three B
+// fragments once and applies them to the RT tiles (RT x 1 KiB of x per 3 KiB
+// of fragments).  Writes the same 25-float partial records as
+// dynw_partial_kernel: part[r][kc][0:24] and the row's sum of squares [24],
+// which the VALU forms from the A fragments alongside the MFMAs.
+template <int RT, int UNR>
+__global__ __launch_bounds__(kThreads) void dynw_mfma_kernel(const __bf16* __restrict__ x,
+                                                             const u32x4* __restrict__ packed,
+                                                             float* __restrict__ part, int64_t R, int64_t K, int nK,
+                                                             int64_t steps_per_chunk) {
+  const int wave = threadIdx.x >> 6;
+  const int lane = threadIdx.x & 63;
+  const int64_t row0 = ((int64_t)blockIdx.x * 4 + wave) * (32 * RT);
+  if (row0 >= R) return;  // wave-uniform; no barrier follows
+  const int kc = blockIdx.y;
+  const int64_t nsteps = K / 16;
+  const int64_t s_beg = (int64_t)kc * steps_per_chunk;
+  const int64_t s_end = s_beg + steps_per_chunk < nsteps ? s_beg + steps_per_chunk : nsteps;
+  const u32x4* xp[RT];
+  bool rok[RT];
+#pragma unroll
+  for (int t = 0; t < RT; ++t) {
+    const int64_t row = row0 + t * 32 + (lane & 31);
+    rok[t] = row < R;
+    xp[t] = reinterpret_cast<const u32x4*>(x + (rok[t] ? row : row0) * K + (lane >> 5) * 8);
+  }
+  // Each K step's three MFMAs start from zero and the step's 32x32 result is
+  // added into `acc` with ordinary fp32 adds: a long chain of MFMA
+  // accumulations drifts measurably (1e-5 relative over 1024 steps), the
+  // round-to-nearest VALU adds do not.
+  f32x16 acc[RT], zero;
+  float ss[RT];
+#pragma unroll
+  for (int i = 0; i < 16; ++i) zero[i] = 0.f;
+#pragma unroll
+  for (int t = 0; t < RT; ++t) {
+    acc[t] = zero;
+    ss[t] = 0.f;
+  }
+  for (int64_t s = s_beg; s < s_end; s += UNR) {
+    u32x4 a[UNR][RT], b[UNR][3];
+#pragma unroll
+    for (int u = 0; u < UNR; ++u) {
+      if (s + u < s_end) {
+#pragma unroll
+        for (int h = 0; h < 3; ++h) b[u][h] = packed[((s + u) * 3 + h) * 64 + lane];
+#pragma unroll
+        for (int t = 0; t < RT; ++t) a[u][t] = rok[t] ? xp[t][(s + u) * 2] : u32x4{0u, 0u, 0u, 0u};
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < UNR; ++u) {
+      if (s + u < s_end) {
+#pragma unroll
+        for (int t = 0; t < RT; ++t) {
+          const bf16x8 av = __builtin_bit_cast(bf16x8, a[u][t]);
+          // smallest part first: the step sum sees the corrections before the bulk
+          f32x16 st = __builtin_amdgcn_mfma_f32_32x32x16_bf16(av, __builtin_bit_cast(bf16x8, b[u][2]), zero, 0, 0, 0);
+          st = __builtin_amdgcn_mfma_f32_32x32x16_bf16(av, __builtin_bit_cast(bf16x8, b[u][1]), st, 0, 0, 0);
+          st = __builtin_amdgcn_mfma_f32_32x32x16_bf16(av, __builtin_bit_cast(bf16x8, b[u][0]), st, 0, 0, 0);
+          acc[t] += st;
+#pragma unroll
+          for (int q = 0; q < 4; ++q) {
+            const float lo_ = __uint_as_float(a[u][t][q] << 16);
+            const float hi_ = __uint_as_float(a[u][t][q] & 0xffff0000u);
+            ss[t] += lo_ * lo_ + hi_ * hi_;
+          }
+        }
+      }
+    }
+  }
+  const int col = lane & 31;
+#pragma unroll
+  for (int t = 0; t < RT; ++t) {
+    const int64_t tr0 = row0 + t * 32;
+    if (col < kOut) {
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        const int64_t r = tr0 + (i >> 2) * 8 + (lane >> 5) * 4 + (i & 3);
+        if (r < R) part[(r * nK + kc) * kPart + col] = acc[t][i];
+      }
+    }
+    const float sst = ss[t] + __shfl_xor(ss[t], 32, 64);  // the two k halves of one row
+    const int64_t row = tr0 + (lane & 31);
+    if (lane < 32 && row < R) part[(row * nK + kc) * kPart + kOut] = sst;
+  }
+}
+
 struct DynParams {
   const float* bias_pre;   // [4]
   const float* bias_post;  // [4]
