@@ -49,7 +49,7 @@ enum {
   MHC_ERR_HIP = 4        /* a HIP runtime call failed */
 };
 
-/* Version of this ABI (bumped on any signature change). */
+/* Version of this ABI (bumped on any signature or semantic change). */
 int mhc_abi_version(void);
 
 /* Message for the last non-zero status returned on the calling thread. */
@@ -152,14 +152,16 @@ size_t mhc_dynamic_weights_backward_workspace_bytes(int64_t R, int64_t K);
 
 /* Replaces the torch backward of _FusedDynamicWeights (reference
  * src/mhc/ops.py:110-228, Sinkhorn part via _backward.py:503).
- * aux is the forward's aux output.  Gradients are f32:
- * grad_x [R,K], grad_phi [K,24], grad_bias [24], grad_alpha [3] (pre, post, res). */
+ * aux is the forward's aux output.  grad_x [R,K] is written in dtype_x (the
+ * dtype the reference's backward casts it back to, ops.py:218-228); the
+ * parameter gradients are f32: grad_phi [K,24], grad_bias [24],
+ * grad_alpha [3] (pre, post, res). */
 int mhc_dynamic_weights_backward(const void* x, int dtype_x, const float* phi, const float* bias,
                                  const float* alpha_pre, const float* alpha_post,
                                  const float* alpha_res, const float* aux, const float* H_pre,
                                  const float* grad_H_pre, const float* grad_H_post,
                                  const float* grad_H_res,
-                                 float* grad_x, float* grad_phi, float* grad_bias,
+                                 void* grad_x, float* grad_phi, float* grad_bias,
                                  float* grad_alpha,
                                  int64_t R, int64_t K, int iters, float eps,
                                  void* workspace, size_t workspace_bytes,

@@ -130,17 +130,40 @@ extern "C" int mhc_dynamic_weights_forward(const void* x, int dtype_x, const flo
   return hip_status(hipGetLastError(), "dynamic_weights_forward finalize launch");
 }
 
+// Row chunks of the backward's wide pass: one chunk for a batch's worth of
+// rows; for many rows about 1024 workgroups, at least 64 rows each.
+struct WidePlan {
+  int64_t RC;  // rows per chunk
+  int nR;      // chunks
+};
+
+static WidePlan wide_plan(int64_t R, int64_t K) {
+  WidePlan p;
+  const int64_t ncol = K > 0 ? (K + kThreads - 1) / kThreads : 1;
+  int64_t nr = (1024 + ncol - 1) / ncol;
+  const int64_t max_nr = (R + 63) / 64;
+  if (nr > max_nr) nr = max_nr;
+  if (nr < 1) nr = 1;
+  p.RC = (R + nr - 1) / nr;
+  if (p.RC < 1) p.RC = 1;
+  p.nR = (int)((R + p.RC - 1) / p.RC);
+  if (p.nR < 1) p.nR = 1;
+  return p;
+}
+
 extern "C" size_t mhc_dynamic_weights_backward_workspace_bytes(int64_t R, int64_t K) {
-  (void)K;
   if (R <= 0) return 0;
-  return align256((size_t)R * kRow * sizeof(float));
+  const WidePlan w = wide_plan(R, K);
+  size_t need = align256((size_t)R * kRow * sizeof(float));
+  if (w.nR > 1) need += align256((size_t)w.nR * K * kOut * sizeof(float));
+  return need;
 }
 
 extern "C" int mhc_dynamic_weights_backward(const void* x, int dtype_x, const float* phi, const float* bias,
                                             const float* alpha_pre, const float* alpha_post,
                                             const float* alpha_res, const float* aux, const float* H_pre,
                                             const float* grad_H_pre, const float* grad_H_post,
-                                            const float* grad_H_res, float* grad_x, float* grad_phi,
+                                            const float* grad_H_res, void* grad_x, float* grad_phi,
                                             float* grad_bias, float* grad_alpha, int64_t R, int64_t K, int iters,
                                             float eps, void* workspace, size_t workspace_bytes,
                                             mhc_stream_t stream) {
@@ -178,11 +201,19 @@ extern "C" int mhc_dynamic_weights_backward(const void* x, int dtype_x, const fl
   if (int rc = hip_status(hipGetLastError(), "dynamic_weights_backward rows launch")) return rc;
   const bool phi_vec = aligned16(phi);
   const unsigned nwide = K > 0 ? (unsigned)((K + kThreads - 1) / kThreads) : 1u;
-  return MHC_DISPATCH_DTYPE(dtype_x, [&] {
-    dynw_bwd_wide_kernel<T><<<dim3(nwide), kThreads, 0, st>>>((const T*)x, phi, rowbuf, grad_x, grad_phi, grad_bias,
-                                                              grad_alpha, R, K, phi_vec);
+  const WidePlan w = wide_plan(R, K);
+  float* gphi_part =
+      (w.nR > 1 && grad_phi) ? (float*)((char*)workspace + align256((size_t)R * kRow * sizeof(float))) : nullptr;
+  int rc = MHC_DISPATCH_DTYPE(dtype_x, [&] {
+    dynw_bwd_wide_kernel<T, T><<<dim3(nwide, (unsigned)w.nR), kThreads, 0, st>>>(
+        (const T*)x, phi, rowbuf, (T*)grad_x, grad_phi, gphi_part, grad_bias, grad_alpha, R, K, w.RC, phi_vec);
     return hip_status(hipGetLastError(), "dynamic_weights_backward wide launch");
   });
+  if (rc || !gphi_part) return rc;
+  const int64_t n = K * kOut;
+  dynw_gphi_reduce_kernel<><<<dim3((unsigned)((n + kThreads - 1) / kThreads)), kThreads, 0, st>>>(gphi_part, grad_phi,
+                                                                                                n, w.nR);
+  return hip_status(hipGetLastError(), "dynamic_weights_backward grad_phi reduce launch");
 }
 
 // ---------------------------------------------------------------------------

@@ -16,10 +16,11 @@
 //   dynw_bwd_rows_kernel  per row: Sinkhorn backward, sigmoid / normalise
 //                         backward, grad_raw, the rms coefficient and the
 //                         per-row bias / alpha contributions.
-//   dynw_bwd_wide_kernel  per k: grad_x[r,k] = grad_raw[r,:] . phi[k,:] + coef[r] x[r,k]
-//                         and grad_phi[k,:] = sum_r x[r,k] grad_raw[r,:].
-//                         Workgroup 0 also sums grad_bias and grad_alpha over
-//                         rows in a fixed order.
+//   dynw_bwd_wide_kernel  per k and row chunk: grad_x[r,k] = grad_raw[r,:] . phi[k,:]
+//                         + coef[r] x[r,k] and grad_phi[k,:] = sum_r x[r,k] grad_raw[r,:]
+//                         (per-chunk partials + dynw_gphi_reduce_kernel when
+//                         rows are split).  Workgroup (0, 0) also sums
+//                         grad_bias and grad_alpha over rows in a fixed order.
 #pragma once
 
 #include "sinkhorn.hpp"
@@ -404,19 +405,25 @@ __global__ __launch_bounds__(kThreads) void dynw_bwd_rows_kernel(const float* __
   if (e == 4) rb[50] = ga_pp;
 }
 
-// Thread per k: grad_x[r,k] = grad_raw[r,:] . phi[k,:] + coef[r] x[r,k] (f32,
-// rows of stride K) and grad_phi[k,:] = sum_r x[r,k] grad_raw[r,:].
-// Workgroup 0 also sums the per-row records into grad_bias [24] and
-// grad_alpha [3] (threads stride over rows, then a fixed-order block sum).
-template <typename TX>
+// Thread per k over the rows of one row chunk (grid.y):
+//   grad_x[r,k] = grad_raw[r,:] . phi[k,:] + coef[r] x[r,k]   (written as TG)
+//   grad_phi[k,:] (+)= sum_{r in chunk} x[r,k] grad_raw[r,:]
+// With one row chunk grad_phi is written directly; otherwise each chunk
+// writes gphi_part[chunk][k][0:24] and dynw_gphi_reduce_kernel sums the
+// chunks in order.  The per-row record is the same for every thread of the
+// workgroup (scalar loads).  Workgroup (0, 0) also sums the per-row records
+// into grad_bias [24] and grad_alpha [3] (threads stride over rows, then a
+// fixed-order block sum).
+template <typename TX, typename TG>
 __global__ __launch_bounds__(kThreads) void dynw_bwd_wide_kernel(const TX* __restrict__ x,
                                                                  const float* __restrict__ phi,
                                                                  const float* __restrict__ rowbuf,
-                                                                 float* __restrict__ gx, float* __restrict__ gphi,
+                                                                 TG* __restrict__ gx, float* __restrict__ gphi,
+                                                                 float* __restrict__ gphi_part,
                                                                  float* __restrict__ gbias,
                                                                  float* __restrict__ galpha, int64_t R, int64_t K,
-                                                                 bool phi_vec) {
-  if (blockIdx.x == 0 && (gbias || galpha)) {
+                                                                 int64_t RC, bool phi_vec) {
+  if (blockIdx.x == 0 && blockIdx.y == 0 && (gbias || galpha)) {
     __shared__ float lds[4 * 27];
     float acc[27];
 #pragma unroll
@@ -436,11 +443,13 @@ __global__ __launch_bounds__(kThreads) void dynw_bwd_wide_kernel(const TX* __res
   }
   const int64_t k = (int64_t)blockIdx.x * kThreads + threadIdx.x;
   if (k >= K || (!gx && !gphi)) return;
+  const int64_t r_beg = (int64_t)blockIdx.y * RC;
+  const int64_t r_end = r_beg + RC < R ? r_beg + RC : R;
   float ph[kOut], gp[kOut];
   load_phi_row(phi, k, phi_vec, ph);
 #pragma unroll
   for (int j = 0; j < kOut; ++j) gp[j] = 0.f;
-  for (int64_t r = 0; r < R; ++r) {
+  for (int64_t r = r_beg; r < r_end; ++r) {
     const float* rb = rowbuf + r * kRow;
     const float xv = to_f32(x[r * K + k]);
     float v = rb[24] * xv;
@@ -449,13 +458,25 @@ __global__ __launch_bounds__(kThreads) void dynw_bwd_wide_kernel(const TX* __res
       v += rb[j] * ph[j];
       gp[j] += xv * rb[j];
     }
-    if (gx) gx[r * K + k] = v;
+    if (gx) gx[r * K + k] = from_f32<TG>(v);
   }
-  if (gphi) {
-    float* o = gphi + k * kOut;
+  float* o = gphi_part ? gphi_part + ((int64_t)blockIdx.y * K + k) * kOut : gphi;
+  if (o) {
 #pragma unroll
-    for (int j = 0; j < kOut; ++j) o[j] = gp[j];
+    for (int j = 0; j < kOut; ++j) o[(gphi_part ? 0 : k * kOut) + j] = gp[j];
   }
+}
+
+// grad_phi[i] = sum over row chunks c (in order) of gphi_part[c][i], i < K * 24.
+template <int = 0>
+__global__ __launch_bounds__(kThreads) void dynw_gphi_reduce_kernel(const float* __restrict__ part,
+                                                                    float* __restrict__ gphi, int64_t n, int nc) {
+  const int64_t i = (int64_t)blockIdx.x * kThreads + threadIdx.x;
+  if (i >= n) return;
+  float v = 0.f;
+#pragma unroll 4
+  for (int c = 0; c < nc; ++c) v += part[(int64_t)c * n + i];
+  gphi[i] = v;
 }
 
 // ---------------------------------------------------------------------------

@@ -96,15 +96,16 @@ def fused_dynamic_weights_backward(x: torch.Tensor, phi: torch.Tensor, bias: tor
                                    alphas, aux: torch.Tensor, H_pre: torch.Tensor,
                                    grad_H_pre: Optional[torch.Tensor], grad_H_post: Optional[torch.Tensor],
                                    grad_H_res: Optional[torch.Tensor], sinkhorn_iters: int, eps: float):
-    """All gradients of Eq. 14-19 in f32 (replaces the torch math of the
-    reference's _FusedDynamicWeights.backward, src/mhc/ops.py:110-228).
-    Returns (grad_x, grad_phi, grad_bias, grad_alpha[3])."""
+    """All gradients of Eq. 14-19 (replaces the torch math of the reference's
+    _FusedDynamicWeights.backward, src/mhc/ops.py:110-228).  grad_x comes back
+    in x's dtype, as the reference casts it (ops.py:218-228); the parameter
+    gradients are f32.  Returns (grad_x, grad_phi, grad_bias, grad_alpha[3])."""
     R, K = x.shape
     dev = _lib.require_gpu(x, phi, bias, aux, H_pre)
     x = x.contiguous()
     phi = _f32(phi)
     bias = _f32(bias)
-    gx = torch.empty(R, K, device=dev, dtype=torch.float32)
+    gx = torch.empty(R, K, device=dev, dtype=x.dtype)
     gphi = torch.empty(K, 24, device=dev, dtype=torch.float32)
     gbias = torch.empty(24, device=dev, dtype=torch.float32)
     galpha = torch.empty(3, device=dev, dtype=torch.float32)
