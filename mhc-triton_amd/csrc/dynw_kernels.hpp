@@ -314,35 +314,40 @@ __global__ __launch_bounds__(kThreads) void dynw_finalize_kernel(const float* __
 // Follows reference src/mhc/ops.py:138-216 with the Sinkhorn part of
 // _backward.py:30-262 (sgn(0) = 0).
 //
-// Four rows per 256-thread workgroup (R is the batch in the layer path, so
+// RPW rows per 256-thread workgroup (R is the batch in the layer path, so
 // this is a latency problem).  In the layer path the upstream H_pre / H_res
 // gradients arrive as the weight-gradient pass's per-workgroup partials
-// part20[r][k][0:20] (4 H_pre, 16 H_res) over nblk workgroups: wave w sums row
-// w's partials (64 lanes in chunk order, 16-byte loads, then a fixed
-// butterfly).  The standalone op passes them as rows (g_pre [R,4],
-// g_res [R,16]).  Wave 0 then runs the four rows in 16-lane form: lane e of a
-// group owns H_res element e, lanes 0..3 also H_pre[e], lanes 4..7
-// H_post[e - 4].
+// part20[r][k][0:20] (4 H_pre, 16 H_res) over nblk workgroups, which the
+// workgroup sums itself: with RPW = 4, wave w sums row w's partials; with
+// RPW = 1 (the layer path, up to 2048 partials per row at B = 1) all four
+// waves share the row and their sums are added in wave order.  Lanes stride
+// the chunks with 16-byte loads, then a fixed butterfly.  The standalone op
+// passes the gradients as rows (g_pre [R,4], g_res [R,16]).  Wave 0 then runs
+// the rows in 16-lane form: lane e of a group owns H_res element e, lanes 0..3
+// also H_pre[e], lanes 4..7 H_post[e - 4].
 constexpr int kSkSlots = 32;  // Sinkhorn states kept in LDS per lane
 
-template <int = 0>
+template <int RPW>
 __global__ __launch_bounds__(kThreads) void dynw_bwd_rows_kernel(const float* __restrict__ aux, DynParams P,
                                                                  InRow h_pre, InRow g_pre, InRow g_post,
                                                                  InRow g_res, const float* __restrict__ part20,
                                                                  int nblk, float* __restrict__ rowbuf, int64_t R,
                                                                  int64_t K, int iters, float eps) {
+  static_assert(RPW == 1 || RPW == 4, "rows per workgroup");
   __shared__ float slots[kSkSlots * 64];
   __shared__ float red[4][20];
   const int wave = threadIdx.x >> 6;
   const int lane = threadIdx.x & 63;
   if (part20) {
-    const int64_t rw = (int64_t)blockIdx.x * 4 + wave;
+    const int64_t rw = (int64_t)blockIdx.x * RPW + (RPW == 4 ? wave : 0);
+    const int k0 = RPW == 4 ? lane : wave * 64 + lane;
+    const int kstep = RPW == 4 ? 64 : 256;
     f32x4 acc[5];
 #pragma unroll
     for (int q = 0; q < 5; ++q) acc[q] = f32x4{0.f, 0.f, 0.f, 0.f};
     if (rw < R) {
 #pragma unroll 4
-      for (int k = lane; k < nblk; k += 64) {
+      for (int k = k0; k < nblk; k += kstep) {
         const f32x4* p = reinterpret_cast<const f32x4*>(part20 + (rw * nblk + k) * 20);
 #pragma unroll
         for (int q = 0; q < 5; ++q) acc[q] += p[q];
@@ -356,16 +361,24 @@ __global__ __launch_bounds__(kThreads) void dynw_bwd_rows_kernel(const float* __
         if (lane == 0) red[wave][4 * q + c] = v;
       }
     }
+    if (RPW == 1) {
+      __syncthreads();
+      if (threadIdx.x < 20) {
+        const int v = threadIdx.x;
+        red[0][v] = ((red[0][v] + red[1][v]) + red[2][v]) + red[3][v];
+      }
+    }
   }
   __syncthreads();
   if (wave != 0) return;
   const int e = lane & 15;
   const int j = e & 3;
-  const int64_t r_grp = (int64_t)blockIdx.x * 4 + (lane >> 4);
-  const bool live = r_grp < R;
+  const int64_t r_grp = (int64_t)blockIdx.x * RPW + (lane >> 4);
+  const bool live = r_grp < R && (lane >> 4) < RPW;
   const int64_t r = live ? r_grp : R - 1;  // idle groups redo the last row and store nothing
-  const float gpre = part20 ? red[lane >> 4][j] : (g_pre.p ? g_pre.p[r * g_pre.stride + j] : 0.f);
-  const float gres = part20 ? red[lane >> 4][4 + e] : (g_res.p ? g_res.p[r * g_res.stride + e] : 0.f);
+  const int rr = RPW == 4 ? (lane >> 4) : 0;  // this group's row in `red`
+  const float gpre = part20 ? red[rr][j] : (g_pre.p ? g_pre.p[r * g_pre.stride + j] : 0.f);
+  const float gres = part20 ? red[rr][4 + e] : (g_res.p ? g_res.p[r * g_res.stride + e] : 0.f);
   const float gpost = g_post.p ? g_post.p[r * g_post.stride + j] : 0.f;
   const float* a = aux + r * kPart;
   const float inv_rms = a[kOut];
@@ -373,8 +386,9 @@ __global__ __launch_bounds__(kThreads) void dynw_bwd_rows_kernel(const float* __
   const float raw_res = a[8 + e];
   const float raw_pp = a[e & 7];
   // H_res = Sinkhorn(|s_res| + eps): gradient w.r.t. s_res.
-  const float gs_res =
-      sk16_backward<kSkSlots>(inv_rms * ar * raw_res + P.bias_res[e], gres, iters, eps, slots + lane, 64);
+  const float s_res = inv_rms * ar * raw_res + P.bias_res[e];
+  const float gs_res = iters == 20 ? sk16_backward_fixed<20>(s_res, gres, eps)
+                                   : sk16_backward<kSkSlots>(s_res, gres, iters, eps, slots + lane, 64);
   // H_pre = sigmoid / (sum + eps) on lanes 0..3, H_post = 2 sigmoid on lanes 4..7.
   const bool is_pre = (e & 4) == 0;
   const float al_pp = is_pre ? *P.alpha_pre : *P.alpha_post;

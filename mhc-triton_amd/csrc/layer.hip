@@ -138,7 +138,8 @@ __global__ __launch_bounds__(kThreads) void static_weights_bwd_kernel(
   if (threadIdx.x >= 16) return;
   const int e = threadIdx.x;
   const int j = e & 3;
-  gbias[8 + e] = sk16_backward<kSkSlots>(bres[e], tot[8 + e], iters, 1e-8f, slots + e, 16);
+  gbias[8 + e] = iters == 20 ? sk16_backward_fixed<20>(bres[e], tot[8 + e], 1e-8f)
+                             : sk16_backward<kSkSlots>(bres[e], tot[8 + e], iters, 1e-8f, slots + e, 16);
   const bool is_pre = (e & 4) == 0;
   const float sg = sigmoidf(is_pre ? bpre[j] : bpost[j]);
   const float den = sum_row16(sg) + 1e-8f;
@@ -321,7 +322,7 @@ extern "C" int mhc_layer_dynamic_backward(const void* H, int dtype, const void* 
   // kernel also sums grad_bias / grad_alpha.
   DynParams P{H_pre_base, H_post_base, H_res_base, alpha_pre, alpha_post, alpha_res};
   const int64_t K = 4 * D;
-  dynw_bwd_rows_kernel<><<<dim3((unsigned)((B + 3) / 4)), kThreads, 0, st>>>(
+  dynw_bwd_rows_kernel<1><<<dim3((unsigned)B), kThreads, 0, st>>>(
       aux, P, InRow{w, kOut}, InRow{nullptr, 0}, InRow{dH_post, 4}, InRow{nullptr, 0}, part, (int)nblk, rowbuf, B,
       K, iters, eps);
   if ((rc = hip_status(hipGetLastError(), "layer weights backward rows launch"))) return rc;

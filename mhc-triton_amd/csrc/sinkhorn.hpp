@@ -182,6 +182,24 @@ __device__ __forceinline__ float sk16_round_backward(float m, float d, float eps
   return (d - sum_row16(d * mr)) * r;
 }
 
+// sk16_backward for a compile-time iteration count: every forward state stays
+// in a register (one per round per lane) and both sweeps are unrolled, so a
+// round costs only its dependent VALU / DPP chain.
+template <int T>
+__device__ __forceinline__ float sk16_backward_fixed(float mat, float d, float eps) {
+  float st[T > 0 ? T : 1];
+  float m = __builtin_fabsf(mat) + eps;
+#pragma unroll
+  for (int t = 0; t < T; ++t) {
+    st[t] = m;
+    m = sk16_round(m, eps);
+  }
+#pragma unroll
+  for (int t = T - 1; t >= 0; --t) d = sk16_round_backward(st[t], d, eps);
+  const float sg = mat > 0.f ? 1.f : (mat < 0.f ? -1.f : 0.f);
+  return d * sg;
+}
+
 // dM for one matrix in 16-lane form.  The forward states are kept in `slot`
 // (this lane's LDS slots, `stride` floats apart): every state when
 // iters <= NSLOT, otherwise every L-th state with the rest recomputed from the
