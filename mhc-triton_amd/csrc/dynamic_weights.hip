@@ -32,13 +32,14 @@ static DynPlan dyn_plan(int64_t R, int64_t K) {
 
 static size_t align256(size_t v) { return (v + 255) & ~(size_t)255; }
 
-// MFMA plan for bf16 x with many rows: waves of kMfmaTiles 32-row tiles, 4
-// waves per workgroup, and the K steps (16 k each) split into nK chunks so
-// that about 512 workgroups (2 per CU) stream x; at least 16 steps per chunk.
+// MFMA plan for bf16 x with many rows: workgroups of kMfmaRowsWg rows, and the
+// K steps (16 k each) split into nK chunks so that about 2048 workgroups
+// (8 per CU; 4 resident at a time by LDS) stream x; at least 16 steps per
+// chunk.  At R = K = 16384 this runs at 3.2 TB/s: the per-step phi fragment
+// loads (3 KiB per 32 rows x 16 k, shared by the four waves through L1) cost
+// about a quarter of the time, the LDS round trip of x most of the rest.
 constexpr int64_t kMfmaMinRows = 64;
-constexpr int kMfmaTiles = 4;
-constexpr int kMfmaUnroll = 2;
-constexpr int64_t kMfmaWgRows = 4 * 32 * kMfmaTiles;
+constexpr int64_t kMfmaWgRows = kMfmaRowsWg;
 
 struct MfmaPlan {
   int64_t nsteps;  // K / 16
@@ -53,7 +54,7 @@ static MfmaPlan mfma_plan(int64_t R, int64_t K) {
   MfmaPlan p;
   p.nsteps = K / 16;
   const int64_t wg_rows = (R + kMfmaWgRows - 1) / kMfmaWgRows;
-  int64_t nk = (512 + wg_rows - 1) / wg_rows;
+  int64_t nk = (2048 + wg_rows - 1) / wg_rows;
   const int64_t max_nk = p.nsteps / 16 > 0 ? p.nsteps / 16 : 1;
   if (nk > max_nk) nk = max_nk;
   if (nk < 1) nk = 1;
@@ -108,8 +109,7 @@ extern "C" int mhc_dynamic_weights_forward(const void* x, int dtype_x, const flo
     dynw_pack_phi_kernel<><<<dim3((unsigned)((m.nsteps * 64 + kThreads - 1) / kThreads)), kThreads, 0, st>>>(
         phi, packed, m.nsteps);
     if (int rc = hip_status(hipGetLastError(), "dynamic_weights_forward pack launch")) return rc;
-    dynw_mfma_kernel<kMfmaTiles, kMfmaUnroll>
-        <<<dim3((unsigned)((R + kMfmaWgRows - 1) / kMfmaWgRows), (unsigned)m.nK), kThreads, 0, st>>>(
+    dynw_mfma_kernel<><<<dim3((unsigned)((R + kMfmaWgRows - 1) / kMfmaWgRows), (unsigned)m.nK), kThreads, 0, st>>>(
         (const __bf16*)x, packed, part, R, K, m.nK, m.spc);
     if (int rc = hip_status(hipGetLastError(), "dynamic_weights_forward mfma launch")) return rc;
     nK = m.nK;

@@ -138,92 +138,131 @@ __global__ __launch_bounds__(kThreads) void dynw_pack_phi_kernel(const float* __
   packed[(s * 3 + 2) * 64 + lane] = __builtin_bit_cast(u32x4, lo);
 }
 
-// One wave per RT 32-row tiles and one K chunk: each K step loads the three B
-// fragments once and applies them to the RT tiles (RT x 1 KiB of x per 3 KiB
-// of fragments).  Writes the same 25-float partial records as
+// One workgroup per 128-row tile and K chunk (wave w owns rows 32w..32w+31).
+// x is staged through LDS so that global loads are whole 128-byte row
+// segments: per 64-k slab, thread t loads 16 bytes of rows t/8 + 32i
+// (i = 0..3) at k offset 8 (t % 8) -- every 8 lanes read one full line -- two
+// slabs ahead of the one the MFMAs consume (two LDS buffers plus registers):
+// with one slab in flight per workgroup the load path, not the MFMAs, set the
+// pace (3.3 TB/s).  A fragments are then
+// read from LDS rows padded to 144 bytes.  Each 16-k step's three MFMAs start
+// from zero and the step result is added into `acc` with fp32 VALU adds (a
+// long MFMA accumulation chain drifts by ~1e-5 relative over 1024 steps; the
+// round-to-nearest adds do not).  Writes the same 25-float partial records as
 // dynw_partial_kernel: part[r][kc][0:24] and the row's sum of squares [24],
 // which the VALU forms from the A fragments alongside the MFMAs.
-template <int RT, int UNR>
+constexpr int kMfmaRowsWg = 128;
+constexpr int kMfmaSlabK = 64;
+constexpr int kMfmaLdsRow = kMfmaSlabK + 8;  // bf16 per padded LDS row (144 bytes)
+
+template <int = 0>
 __global__ __launch_bounds__(kThreads) void dynw_mfma_kernel(const __bf16* __restrict__ x,
                                                              const u32x4* __restrict__ packed,
                                                              float* __restrict__ part, int64_t R, int64_t K, int nK,
                                                              int64_t steps_per_chunk) {
+  __shared__ __attribute__((aligned(16))) __bf16 tile[2][kMfmaRowsWg * kMfmaLdsRow];
   const int wave = threadIdx.x >> 6;
   const int lane = threadIdx.x & 63;
-  const int64_t row0 = ((int64_t)blockIdx.x * 4 + wave) * (32 * RT);
-  if (row0 >= R) return;  // wave-uniform; no barrier follows
+  const int64_t row0 = (int64_t)blockIdx.x * kMfmaRowsWg;
   const int kc = blockIdx.y;
   const int64_t nsteps = K / 16;
   const int64_t s_beg = (int64_t)kc * steps_per_chunk;
   const int64_t s_end = s_beg + steps_per_chunk < nsteps ? s_beg + steps_per_chunk : nsteps;
-  const u32x4* xp[RT];
-  bool rok[RT];
+  // Global-load role: rows lr + 32 i, 16 bytes at k offset 8 * (t % 8) of the slab.
+  const int lr = threadIdx.x >> 3;
+  const int lk = (threadIdx.x & 7) * 8;
+  const u32x4* gp[4];
+  bool gok[4];
 #pragma unroll
-  for (int t = 0; t < RT; ++t) {
-    const int64_t row = row0 + t * 32 + (lane & 31);
-    rok[t] = row < R;
-    xp[t] = reinterpret_cast<const u32x4*>(x + (rok[t] ? row : row0) * K + (lane >> 5) * 8);
+  for (int i = 0; i < 4; ++i) {
+    const int64_t r = row0 + lr + 32 * i;
+    gok[i] = r < R;
+    gp[i] = reinterpret_cast<const u32x4*>(x + (gok[i] ? r : 0) * K + lk);
   }
-  // Each K step's three MFMAs start from zero and the step's 32x32 result is
-  // added into `acc` with ordinary fp32 adds: a long chain of MFMA
-  // accumulations drifts measurably (1e-5 relative over 1024 steps), the
-  // round-to-nearest VALU adds do not.
-  f32x16 acc[RT], zero;
-  float ss[RT];
+  auto gload = [&](int64_t s0, int64_t s1, u32x4 (&v)[4]) {
+    // 16-k steps s0 .. s1-1 of this slab; k offset lk lies in step s0 + lk / 16.
+    // Out-of-range rows / steps read x[0..7] (always valid) and are zeroed.
+    const bool in = s0 + lk / 16 < s1;
 #pragma unroll
-  for (int i = 0; i < 16; ++i) zero[i] = 0.f;
-#pragma unroll
-  for (int t = 0; t < RT; ++t) {
-    acc[t] = zero;
-    ss[t] = 0.f;
-  }
-  for (int64_t s = s_beg; s < s_end; s += UNR) {
-    u32x4 a[UNR][RT], b[UNR][3];
-#pragma unroll
-    for (int u = 0; u < UNR; ++u) {
-      if (s + u < s_end) {
-#pragma unroll
-        for (int h = 0; h < 3; ++h) b[u][h] = packed[((s + u) * 3 + h) * 64 + lane];
-#pragma unroll
-        for (int t = 0; t < RT; ++t) a[u][t] = rok[t] ? xp[t][(s + u) * 2] : u32x4{0u, 0u, 0u, 0u};
-      }
+    for (int i = 0; i < 4; ++i) {
+      const bool ok = gok[i] && in;
+      const u32x4 t = *(ok ? gp[i] + s0 * 2 : reinterpret_cast<const u32x4*>(x));
+      v[i] = ok ? t : u32x4{0u, 0u, 0u, 0u};
     }
+  };
+  auto lstore = [&](int buf, const u32x4 (&v)[4]) {
 #pragma unroll
-    for (int u = 0; u < UNR; ++u) {
-      if (s + u < s_end) {
+    for (int i = 0; i < 4; ++i)
+      *reinterpret_cast<u32x4*>(&tile[buf][(lr + 32 * i) * kMfmaLdsRow + lk]) = v[i];
+  };
+  f32x16 acc, zero;
 #pragma unroll
-        for (int t = 0; t < RT; ++t) {
-          const bf16x8 av = __builtin_bit_cast(bf16x8, a[u][t]);
-          // smallest part first: the step sum sees the corrections before the bulk
-          f32x16 st = __builtin_amdgcn_mfma_f32_32x32x16_bf16(av, __builtin_bit_cast(bf16x8, b[u][2]), zero, 0, 0, 0);
-          st = __builtin_amdgcn_mfma_f32_32x32x16_bf16(av, __builtin_bit_cast(bf16x8, b[u][1]), st, 0, 0, 0);
-          st = __builtin_amdgcn_mfma_f32_32x32x16_bf16(av, __builtin_bit_cast(bf16x8, b[u][0]), st, 0, 0, 0);
-          acc[t] += st;
+  for (int i = 0; i < 16; ++i) acc[i] = zero[i] = 0.f;
+  float ss = 0.f;
+  const int arow = wave * 32 + (lane & 31);
+  const int akoff = (lane >> 5) * 8;
+  // Two slabs of x are in flight per thread while a third is consumed from
+  // LDS.  The loop is unrolled by two so the register sets va / vb swap roles
+  // without copies (a copy would wait on the load just issued):
+  //   phase 0: slab s in tile[buf], s + 1 in va (issued a phase ago), s + 2 -> vb
+  //   phase 1: slab s + 1 in tile[buf], s + 2 in vb, s + 3 -> va
+  constexpr int kSS = kMfmaSlabK / 16;  // steps per slab
+  auto compute = [&](int64_t s, int bsel) {
 #pragma unroll
-          for (int q = 0; q < 4; ++q) {
-            const float lo_ = __uint_as_float(a[u][t][q] << 16);
-            const float hi_ = __uint_as_float(a[u][t][q] & 0xffff0000u);
-            ss[t] += lo_ * lo_ + hi_ * hi_;
-          }
+    for (int q = 0; q < kSS; ++q) {
+      if (s + q < s_end) {
+        const u32x4 a = *reinterpret_cast<const u32x4*>(&tile[bsel][arow * kMfmaLdsRow + q * 16 + akoff]);
+        const u32x4 b0 = packed[((s + q) * 3 + 0) * 64 + lane];
+        const u32x4 b1 = packed[((s + q) * 3 + 1) * 64 + lane];
+        const u32x4 b2 = packed[((s + q) * 3 + 2) * 64 + lane];
+        const bf16x8 av = __builtin_bit_cast(bf16x8, a);
+        // smallest part first: the step sum sees the corrections before the bulk
+        f32x16 st = __builtin_amdgcn_mfma_f32_32x32x16_bf16(av, __builtin_bit_cast(bf16x8, b2), zero, 0, 0, 0);
+        st = __builtin_amdgcn_mfma_f32_32x32x16_bf16(av, __builtin_bit_cast(bf16x8, b1), st, 0, 0, 0);
+        st = __builtin_amdgcn_mfma_f32_32x32x16_bf16(av, __builtin_bit_cast(bf16x8, b0), st, 0, 0, 0);
+        acc += st;
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+          const float lo_ = __uint_as_float(a[c] << 16);
+          const float hi_ = __uint_as_float(a[c] & 0xffff0000u);
+          ss += lo_ * lo_ + hi_ * hi_;
         }
       }
     }
+  };
+  u32x4 va[4], vb[4];
+  int buf = 0;
+  if (s_beg < s_end) {
+    gload(s_beg, s_end, vb);
+    lstore(0, vb);
+  }
+  if (s_beg + kSS < s_end) gload(s_beg + kSS, s_end, va);
+  __syncthreads();
+  for (int64_t s = s_beg; s < s_end; s += 2 * kSS) {
+    if (s + 2 * kSS < s_end) gload(s + 2 * kSS, s_end, vb);
+    compute(s, buf);
+    if (s + kSS < s_end) lstore(buf ^ 1, va);
+    __syncthreads();
+    buf ^= 1;
+    if (s + kSS >= s_end) break;  // uniform
+    if (s + 3 * kSS < s_end) gload(s + 3 * kSS, s_end, va);
+    compute(s + kSS, buf);
+    if (s + 2 * kSS < s_end) lstore(buf ^ 1, vb);
+    __syncthreads();
+    buf ^= 1;
   }
   const int col = lane & 31;
+  const int64_t wr0 = row0 + wave * 32;
+  if (col < kOut) {
 #pragma unroll
-  for (int t = 0; t < RT; ++t) {
-    const int64_t tr0 = row0 + t * 32;
-    if (col < kOut) {
-#pragma unroll
-      for (int i = 0; i < 16; ++i) {
-        const int64_t r = tr0 + (i >> 2) * 8 + (lane >> 5) * 4 + (i & 3);
-        if (r < R) part[(r * nK + kc) * kPart + col] = acc[t][i];
-      }
+    for (int i = 0; i < 16; ++i) {
+      const int64_t r = wr0 + (i >> 2) * 8 + (lane >> 5) * 4 + (i & 3);
+      if (r < R) part[(r * nK + kc) * kPart + col] = acc[i];
     }
-    const float sst = ss[t] + __shfl_xor(ss[t], 32, 64);  // the two k halves of one row
-    const int64_t row = tr0 + (lane & 31);
-    if (lane < 32 && row < R) part[(row * nK + kc) * kPart + kOut] = sst;
   }
+  const float sst = ss + __shfl_xor(ss, 32, 64);  // the two k halves of one row
+  const int64_t row = wr0 + (lane & 31);
+  if (lane < 32 && row < R) part[(row * nK + kc) * kPart + kOut] = sst;
 }
 
 struct DynParams {
