@@ -112,6 +112,69 @@ template <> struct Io<_Float16> {
   }
 };
 
+// Raw 16-byte vector of each bulk type, and its unpacking to fp32.
+template <typename T> struct RawVec;
+template <> struct RawVec<float> {
+  using type = f32x4;
+  __device__ __forceinline__ static void unpack(const type& v, float* f) {
+    f[0] = v.x; f[1] = v.y; f[2] = v.z; f[3] = v.w;
+  }
+};
+template <> struct RawVec<__bf16> {
+  using type = u32x4;
+  __device__ __forceinline__ static void unpack(const type& r, float* f) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      f[2 * i] = __uint_as_float(r[i] << 16);
+      f[2 * i + 1] = __uint_as_float(r[i] & 0xffff0000u);
+    }
+  }
+};
+template <> struct RawVec<_Float16> {
+  using type = f16x8;
+  __device__ __forceinline__ static void unpack(const type& v, float* f) {
+    const f32x8 w = __builtin_convertvector(v, f32x8);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) f[i] = w[i];
+  }
+};
+
+// W consecutive elements of T held as raw 16-byte vectors until unpacked
+// (W a multiple of the vector width), or as fp32 on the scalar W = 1 path.
+// Kernels issue every load of a tile into fragments first and unpack after:
+// with load and unpack interleaved per row the compiler starts unpacking
+// early rows before the last loads are issued, and fewer bytes are in flight
+// (the closure forward ran 5% slower).
+template <typename T, int W>
+struct Frag {
+  static constexpr int N = Vec<T>::N;
+  static constexpr bool kVec = W >= N;
+  using Raw = typename RawVec<T>::type;
+  Raw r[kVec ? W / N : 1];
+  float s[kVec ? 1 : W];
+
+  template <bool NT = false>
+  __device__ __forceinline__ void load(const T* p) {
+    if constexpr (kVec) {
+#pragma unroll
+      for (int q = 0; q < W / N; ++q) r[q] = vload(reinterpret_cast<const Raw*>(p + q * N), NT);
+    } else {
+#pragma unroll
+      for (int i = 0; i < W; ++i) s[i] = to_f32(p[i]);
+    }
+  }
+
+  __device__ __forceinline__ void unpack(float* f) const {
+    if constexpr (kVec) {
+#pragma unroll
+      for (int q = 0; q < W / N; ++q) RawVec<T>::unpack(r[q], f + q * N);
+    } else {
+#pragma unroll
+      for (int i = 0; i < W; ++i) f[i] = s[i];
+    }
+  }
+};
+
 // Load W consecutive elements when W is a multiple of the 16-byte vector
 // width of T (several 16-byte loads), or W == 1.
 template <typename T, int W, bool NT = false>

@@ -61,7 +61,7 @@ static int launch_bi(const T* H, const float* w, T* bi, int64_t B, int64_t S, in
   return for_batch_chunks(B, [&](int64_t b0, int64_t nb) {
     const Geom g = make_geom<W, kLU>(S, D, b0);
     if (g.ntiles == 0) return (int)MHC_OK;
-    mix_fwd_kernel<T, T, W, kLU, true, false, false, kNtStores><<<dim3(g.ntiles, nb), kThreads, occupancy_lds(4), st>>>(
+    mix_fwd_kernel<T, T, W, kLU, true, false, false, kNtStores><<<dim3(g.ntiles, nb), kThreads, occupancy_lds(3), st>>>(
         H, (const T*)nullptr, WRow{w, kOut}, WRow{nullptr, 0}, WRow{nullptr, 0}, bi, nullptr, g);
     return hip_status(hipGetLastError(), "layer branch_input launch");
   });
@@ -264,7 +264,7 @@ extern "C" int mhc_layer_add_forward(const void* H, int dtype_h, const void* bra
       return for_batch_chunks(B, [&](int64_t b0, int64_t nb) {
         const Geom g = make_geom<W, kLU>(S, D, b0);
         mix_fwd_kernel<TH, TB, W, kLU, false, true, true, kNtStores>
-            <<<dim3(g.ntiles, nb), kThreads, occupancy_lds(3), st>>>(
+            <<<dim3(g.ntiles, nb), kThreads, occupancy_lds(2), st>>>(
             (const TH*)H, (const TB*)branch_output, WRow{nullptr, 0}, WRow{w + 8, kOut}, WRow{w + 4, kOut},
             nullptr, (TH*)H_new, g);
         return hip_status(hipGetLastError(), "layer add forward launch");

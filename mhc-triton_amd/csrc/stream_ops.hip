@@ -42,7 +42,7 @@ static int add_res_fwd(const TH* hr, const TB* bo, const float* post, TH* out, i
   return for_batch_chunks(B, [&](int64_t b0, int64_t nb) {
     const Geom g = make_geom<W, kU>(S, D, b0);
     if (g.ntiles == 0) return (int)MHC_OK;
-    add_residual_fwd_kernel<TH, TB, W, kU, kNtStores><<<dim3(g.ntiles, nb), kThreads, occupancy_lds(3), st>>>(
+    add_residual_fwd_kernel<TH, TB, W, kU, kNtStores><<<dim3(g.ntiles, nb), kThreads, occupancy_lds(2), st>>>(
         hr, bo, WRow{post, 4}, out, g);
     return hip_status(hipGetLastError(), "add_residual_forward launch");
   });
