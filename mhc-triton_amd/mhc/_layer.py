@@ -67,66 +67,214 @@ def _grad_like(g: torch.Tensor, p: torch.Tensor) -> torch.Tensor:
     return g if g.dtype == p.dtype else g.to(p.dtype)
 
 
+def _in_h_dtype(t: Optional[torch.Tensor], H: torch.Tensor) -> Optional[torch.Tensor]:
+    return None if t is None else t.contiguous().to(H.dtype)
+
+
+# ---------------------------------------------------------------------------
+# Launchers of the layer-level entry points.  Each allocates its outputs, calls
+# the C ABI on torch's current stream and returns fresh tensors; the autograd
+# nodes below and the torch.library ops (_library.py) are both built on them.
+# ---------------------------------------------------------------------------
+
+def dynamic_forward(H, phi, H_pre_base, H_post_base, H_res_base, alpha_pre, alpha_post, alpha_res,
+                    iters: int, eps: float):
+    """mhc_layer_dynamic_forward: H -> (branch_input, x [B,4D] f32, w [B,24] f32, aux [B,25] f32)."""
+    B, S, _, D = H.shape
+    dev = _lib.require_gpu(H, phi)
+    H = H.contiguous()
+    params = [_f32(t) for t in (phi, H_pre_base, H_post_base, H_res_base,
+                                alpha_pre.reshape(1), alpha_post.reshape(1), alpha_res.reshape(1))]
+    bi = torch.empty(B, S, D, device=dev, dtype=H.dtype)
+    x = torch.empty(B, 4 * D, device=dev, dtype=torch.float32)
+    w = torch.empty(B, 24, device=dev, dtype=torch.float32)
+    aux = torch.empty(B, 25, device=dev, dtype=torch.float32)
+    lib = _lib.load()
+    code = _lib.dtype_code(H)
+    ws = _ws(lib, B, S, D, code, dev)
+    with _lib.on_device(dev):
+        _lib.check(lib.mhc_layer_dynamic_forward(
+            H.data_ptr(), code, *[p.data_ptr() for p in params], bi.data_ptr(), x.data_ptr(), w.data_ptr(),
+            aux.data_ptr(), B, S, D, int(iters), float(eps), *_wsargs(ws), _lib.stream(dev)),
+            "layer_dynamic_forward")
+    return bi, x, w, aux
+
+
+def dynamic_backward(H, d_bi, dH_new, dH_post, phi, H_pre_base, H_post_base, H_res_base, alpha_pre,
+                     alpha_post, alpha_res, x, w, aux, iters: int, eps: float, need_dH: bool = True):
+    """mhc_layer_dynamic_backward -> (dH or None, grad_phi [4D,24], grad_bias [24], grad_alpha [3]), f32
+    parameter gradients.  dH_new / dH_post are the closure's gradients (None if it was not called)."""
+    B, S, _, D = H.shape
+    dev = _lib.require_gpu(H, phi)
+    H = H.contiguous()
+    d_bi = torch.zeros(B, S, D, device=dev, dtype=H.dtype) if d_bi is None else _in_h_dtype(d_bi, H)
+    dH_new = _in_h_dtype(dH_new, H)
+    dH_post = None if dH_post is None else _f32(dH_post)
+    params = [_f32(t) for t in (phi, H_pre_base, H_post_base, H_res_base,
+                                alpha_pre.reshape(1), alpha_post.reshape(1), alpha_res.reshape(1))]
+    x, w, aux = _f32(x), _f32(w), _f32(aux)
+    dH = torch.empty_like(H) if need_dH else None
+    gphi = torch.empty(4 * D, 24, device=dev, dtype=torch.float32)
+    gbias = torch.empty(24, device=dev, dtype=torch.float32)
+    galpha = torch.empty(3, device=dev, dtype=torch.float32)
+    lib = _lib.load()
+    code = _lib.dtype_code(H)
+    ws = _ws(lib, B, S, D, code, dev)
+    with _lib.on_device(dev):
+        _lib.check(lib.mhc_layer_dynamic_backward(
+            H.data_ptr(), code, d_bi.data_ptr(), _lib.ptr(dH_new), _lib.ptr(dH_post),
+            *[p.data_ptr() for p in params], x.data_ptr(), w.data_ptr(), aux.data_ptr(),
+            _lib.ptr(dH), gphi.data_ptr(), gbias.data_ptr(), galpha.data_ptr(), B, S, D, int(iters), float(eps),
+            *_wsargs(ws), _lib.stream(dev)), "layer_dynamic_backward")
+    return dH, gphi, gbias, galpha
+
+
+def static_forward(H, H_pre_base, H_post_base, H_res_base, iters: int):
+    """mhc_layer_static_forward: H -> (branch_input, w [B,24] f32)."""
+    B, S, _, D = H.shape
+    dev = _lib.require_gpu(H, H_pre_base)
+    H = H.contiguous()
+    params = [_f32(t) for t in (H_pre_base, H_post_base, H_res_base)]
+    bi = torch.empty(B, S, D, device=dev, dtype=H.dtype)
+    w = torch.empty(B, 24, device=dev, dtype=torch.float32)
+    lib = _lib.load()
+    with _lib.on_device(dev):
+        _lib.check(lib.mhc_layer_static_forward(
+            H.data_ptr(), _lib.dtype_code(H), *[p.data_ptr() for p in params], bi.data_ptr(), w.data_ptr(),
+            B, S, D, int(iters), _lib.stream(dev)), "layer_static_forward")
+    return bi, w
+
+
+def static_backward(H, d_bi, dH_new, dH_post, H_pre_base, H_post_base, H_res_base, w, iters: int,
+                    need_dH: bool = True):
+    """mhc_layer_static_backward -> (dH or None, grad_bias [24] f32: pre 0:4, post 4:8, res 8:24)."""
+    B, S, _, D = H.shape
+    dev = _lib.require_gpu(H, w)
+    H = H.contiguous()
+    d_bi = torch.zeros(B, S, D, device=dev, dtype=H.dtype) if d_bi is None else _in_h_dtype(d_bi, H)
+    dH_new = _in_h_dtype(dH_new, H)
+    dH_post = None if dH_post is None else _f32(dH_post)
+    params = [_f32(t) for t in (H_pre_base, H_post_base, H_res_base)]
+    w = _f32(w)
+    dH = torch.empty_like(H) if need_dH else None
+    gbias = torch.empty(24, device=dev, dtype=torch.float32)
+    lib = _lib.load()
+    code = _lib.dtype_code(H)
+    ws = _ws(lib, B, S, D, code, dev)
+    with _lib.on_device(dev):
+        _lib.check(lib.mhc_layer_static_backward(
+            H.data_ptr(), code, d_bi.data_ptr(), _lib.ptr(dH_new), _lib.ptr(dH_post),
+            *[p.data_ptr() for p in params], w.data_ptr(), _lib.ptr(dH), gbias.data_ptr(), B, S, D,
+            int(iters), *_wsargs(ws), _lib.stream(dev)), "layer_static_backward")
+    return dH, gbias
+
+
+def branch_input(H, w):
+    """mhc_layer_branch_input: branch_input = sum_n w[:, n] H[n] with w [B,24] (H_pre in 0:4)."""
+    B, S, _, D = H.shape
+    dev = _lib.require_gpu(H, w)
+    H = H.contiguous()
+    w = _f32(w)
+    bi = torch.empty(B, S, D, device=dev, dtype=H.dtype)
+    lib = _lib.load()
+    with _lib.on_device(dev):
+        _lib.check(lib.mhc_layer_branch_input(H.data_ptr(), _lib.dtype_code(H), w.data_ptr(), bi.data_ptr(),
+                                              B, S, D, _lib.stream(dev)), "layer_branch_input")
+    return bi
+
+
+def mix_backward(H, d_bi, dH_new, w, need_dH: bool = True):
+    """mhc_layer_mix_backward -> (dH or None, dH_pre [B,4] f32, dH_res [B,16] f32)."""
+    B, S, _, D = H.shape
+    dev = _lib.require_gpu(H, w)
+    H = H.contiguous()
+    d_bi = torch.zeros(B, S, D, device=dev, dtype=H.dtype) if d_bi is None else _in_h_dtype(d_bi, H)
+    dH_new = _in_h_dtype(dH_new, H)
+    w = _f32(w)
+    dH = torch.empty_like(H) if need_dH else None
+    dpre = torch.empty(B, 4, device=dev, dtype=torch.float32)
+    dres = torch.empty(B, 16, device=dev, dtype=torch.float32)
+    lib = _lib.load()
+    code = _lib.dtype_code(H)
+    ws = _ws(lib, B, S, D, code, dev)
+    with _lib.on_device(dev):
+        _lib.check(lib.mhc_layer_mix_backward(
+            H.data_ptr(), code, d_bi.data_ptr(), _lib.ptr(dH_new), w.data_ptr(), _lib.ptr(dH),
+            dpre.data_ptr(), dres.data_ptr(), B, S, D, *_wsargs(ws), _lib.stream(dev)), "layer_mix_backward")
+    return dH, dpre, dres
+
+
+def add_forward(H, branch_output, w):
+    """mhc_layer_add_forward: H_new = H_res @ H + H_post * branch_output, in H's dtype."""
+    B, S, _, D = H.shape
+    if tuple(branch_output.shape) != (B, S, D):
+        raise ValueError(f"branch_output must be ({B}, {S}, {D}), got {tuple(branch_output.shape)}")
+    dev = _lib.require_gpu(H, branch_output, w)
+    H = H.contiguous()
+    bo = branch_output.contiguous()
+    w = _f32(w)
+    H_new = torch.empty_like(H)
+    lib = _lib.load()
+    with _lib.on_device(dev):
+        _lib.check(lib.mhc_layer_add_forward(H.data_ptr(), _lib.dtype_code(H), bo.data_ptr(),
+                                             _lib.dtype_code(bo), w.data_ptr(), H_new.data_ptr(), B, S, D,
+                                             _lib.stream(dev)), "layer_add_forward")
+    return H_new
+
+
+def add_backward(dH_new, branch_output, w):
+    """mhc_layer_add_backward -> (d_branch_output in branch_output's dtype, dH_post [B,4] f32)."""
+    B, S, _, D = dH_new.shape
+    dev = _lib.require_gpu(dH_new, branch_output, w)
+    dH_new = dH_new.contiguous()
+    bo = branch_output.contiguous()
+    w = _f32(w)
+    d_bo = torch.empty_like(bo)
+    dH_post = torch.empty(B, 4, device=dev, dtype=torch.float32)
+    lib = _lib.load()
+    code = _lib.dtype_code(dH_new)
+    ws = _ws(lib, B, S, D, code, dev)
+    with _lib.on_device(dev):
+        _lib.check(lib.mhc_layer_add_backward(dH_new.data_ptr(), code, bo.data_ptr(), _lib.dtype_code(bo),
+                                              w.data_ptr(), d_bo.data_ptr(), dH_post.data_ptr(), B, S, D,
+                                              *_wsargs(ws), _lib.stream(dev)), "layer_add_backward")
+    return d_bo, dH_post
+
+
 class _DynamicLayer(torch.autograd.Function):
     """Node A, dynamic fused weights (module.py:119-139 + 177)."""
 
     @staticmethod
     def forward(ctx, H, phi, H_pre_base, H_post_base, H_res_base, alpha_pre, alpha_post, alpha_res,
                 stash: _Stash, iters: int, eps: float):
-        B, S, _, D = H.shape
-        dev = _lib.require_gpu(H, phi)
-        H = H.contiguous()
-        params = [_f32(t) for t in (phi, H_pre_base, H_post_base, H_res_base,
-                                    alpha_pre.reshape(1), alpha_post.reshape(1), alpha_res.reshape(1))]
-        bi = torch.empty(B, S, D, device=dev, dtype=H.dtype)
-        x = torch.empty(B, 4 * D, device=dev, dtype=torch.float32)
-        w = torch.empty(B, 24, device=dev, dtype=torch.float32)
-        aux = torch.empty(B, 25, device=dev, dtype=torch.float32)
-        lib = _lib.load()
-        code = _lib.dtype_code(H)
-        ws = _ws(lib, B, S, D, code, dev)
-        with _lib.on_device(dev):
-            _lib.check(lib.mhc_layer_dynamic_forward(
-                H.data_ptr(), code, *[p.data_ptr() for p in params], bi.data_ptr(), x.data_ptr(), w.data_ptr(),
-                aux.data_ptr(), B, S, D, int(iters), float(eps), *_wsargs(ws), _lib.stream(dev)),
-                "layer_dynamic_forward")
+        params = (phi, H_pre_base, H_post_base, H_res_base, alpha_pre, alpha_post, alpha_res)
+        bi, x, w, aux = dynamic_forward(H, *params, iters, eps)
         ctx.save_for_backward(H, x, w, aux, *params)
         ctx.stash = stash
         ctx.iters = iters
         ctx.eps = eps
-        ctx.param_refs = (phi, H_pre_base, H_post_base, H_res_base, alpha_pre, alpha_post, alpha_res)
         ctx.set_materialize_grads(False)
         return bi, w
 
     @staticmethod
     def backward(ctx, d_bi, d_w):
         H, x, w, aux, *params = ctx.saved_tensors
-        refs = ctx.param_refs
-        B, S, _, D = H.shape
-        dev = H.device
         dH_new, dH_post = ctx.stash.take()
-        if d_bi is None:
-            d_bi = torch.zeros(B, S, D, device=dev, dtype=H.dtype)
-        d_bi = d_bi.contiguous().to(H.dtype)
-        if dH_new is not None:
-            dH_new = dH_new.contiguous().to(H.dtype)
-        need_dH = ctx.needs_input_grad[0]
-        dH = torch.empty_like(H) if need_dH else None
-        gphi = torch.empty(4 * D, 24, device=dev, dtype=torch.float32)
-        gbias = torch.empty(24, device=dev, dtype=torch.float32)
-        galpha = torch.empty(3, device=dev, dtype=torch.float32)
-        lib = _lib.load()
-        code = _lib.dtype_code(H)
-        ws = _ws(lib, B, S, D, code, dev)
-        with _lib.on_device(dev):
-            _lib.check(lib.mhc_layer_dynamic_backward(
-                H.data_ptr(), code, d_bi.data_ptr(), _lib.ptr(dH_new), _lib.ptr(dH_post),
-                *[p.data_ptr() for p in params], x.data_ptr(), w.data_ptr(), aux.data_ptr(), _lib.ptr(dH),
-                gphi.data_ptr(), gbias.data_ptr(), galpha.data_ptr(), B, S, D, int(ctx.iters), float(ctx.eps),
-                *_wsargs(ws), _lib.stream(dev)), "layer_dynamic_backward")
-        return (dH, _grad_like(gphi, refs[0]), _grad_like(gbias[0:4], refs[1]), _grad_like(gbias[4:8], refs[2]),
-                _grad_like(gbias[8:24], refs[3]), _grad_like(galpha[0:1], refs[4]),
-                _grad_like(galpha[1:2], refs[5]), _grad_like(galpha[2:3], refs[6]), None, None, None)
+        dH, gphi, gbias, galpha = dynamic_backward(H, d_bi, dH_new, dH_post, *params, x, w, aux, ctx.iters,
+                                                   ctx.eps, need_dH=ctx.needs_input_grad[0])
+        return (dH, *_dynamic_param_grads(params, gphi, gbias, galpha), None, None, None)
+
+
+def _dynamic_param_grads(params, gphi, gbias, galpha):
+    """The f32 kernel gradients reshaped and cast to each parameter."""
+    return (_grad_like(gphi, params[0]), _grad_like(gbias[0:4], params[1]), _grad_like(gbias[4:8], params[2]),
+            _grad_like(gbias[8:24], params[3]), _grad_like(galpha[0:1], params[4]),
+            _grad_like(galpha[1:2], params[5]), _grad_like(galpha[2:3], params[6]))
+
+
+def _static_param_grads(params, gbias):
+    return (_grad_like(gbias[0:4], params[0]), _grad_like(gbias[4:8], params[1]),
+            _grad_like(gbias[8:24], params[2]))
 
 
 class _StaticLayer(torch.autograd.Function):
@@ -134,48 +282,32 @@ class _StaticLayer(torch.autograd.Function):
 
     @staticmethod
     def forward(ctx, H, H_pre_base, H_post_base, H_res_base, stash: _Stash, iters: int):
-        B, S, _, D = H.shape
-        dev = _lib.require_gpu(H, H_pre_base)
-        H = H.contiguous()
-        params = [_f32(t) for t in (H_pre_base, H_post_base, H_res_base)]
-        bi = torch.empty(B, S, D, device=dev, dtype=H.dtype)
-        w = torch.empty(B, 24, device=dev, dtype=torch.float32)
-        lib = _lib.load()
-        with _lib.on_device(dev):
-            _lib.check(lib.mhc_layer_static_forward(
-                H.data_ptr(), _lib.dtype_code(H), *[p.data_ptr() for p in params], bi.data_ptr(), w.data_ptr(),
-                B, S, D, int(iters), _lib.stream(dev)), "layer_static_forward")
+        params = (H_pre_base, H_post_base, H_res_base)
+        bi, w = static_forward(H, *params, iters)
         ctx.save_for_backward(H, w, *params)
         ctx.stash = stash
         ctx.iters = iters
-        ctx.param_refs = (H_pre_base, H_post_base, H_res_base)
         ctx.set_materialize_grads(False)
         return bi, w
 
     @staticmethod
     def backward(ctx, d_bi, d_w):
         H, w, *params = ctx.saved_tensors
-        refs = ctx.param_refs
-        B, S, _, D = H.shape
-        dev = H.device
         dH_new, dH_post = ctx.stash.take()
-        if d_bi is None:
-            d_bi = torch.zeros(B, S, D, device=dev, dtype=H.dtype)
-        d_bi = d_bi.contiguous().to(H.dtype)
-        if dH_new is not None:
-            dH_new = dH_new.contiguous().to(H.dtype)
-        dH = torch.empty_like(H) if ctx.needs_input_grad[0] else None
-        gbias = torch.empty(24, device=dev, dtype=torch.float32)
-        lib = _lib.load()
-        code = _lib.dtype_code(H)
-        ws = _ws(lib, B, S, D, code, dev)
-        with _lib.on_device(dev):
-            _lib.check(lib.mhc_layer_static_backward(
-                H.data_ptr(), code, d_bi.data_ptr(), _lib.ptr(dH_new), _lib.ptr(dH_post),
-                *[p.data_ptr() for p in params], w.data_ptr(), _lib.ptr(dH), gbias.data_ptr(), B, S, D,
-                int(ctx.iters), *_wsargs(ws), _lib.stream(dev)), "layer_static_backward")
-        return (dH, _grad_like(gbias[0:4], refs[0]), _grad_like(gbias[4:8], refs[1]),
-                _grad_like(gbias[8:24], refs[2]), None, None)
+        dH, gbias = static_backward(H, d_bi, dH_new, dH_post, *params, w, ctx.iters,
+                                    need_dH=ctx.needs_input_grad[0])
+        return (dH, *_static_param_grads(params, gbias), None, None)
+
+
+def _generic_w_grad(dpre, dres, dH_post, d_w, B, dev):
+    gw = torch.zeros(B, 24, device=dev, dtype=torch.float32)
+    gw[:, 0:4] = dpre
+    gw[:, 8:24] = dres
+    if dH_post is not None:
+        gw[:, 4:8] = dH_post
+    if d_w is not None:
+        gw = gw + d_w
+    return gw
 
 
 class _GenericLayer(torch.autograd.Function):
@@ -184,15 +316,8 @@ class _GenericLayer(torch.autograd.Function):
 
     @staticmethod
     def forward(ctx, H, w_in, stash: _Stash):
-        B, S, _, D = H.shape
-        dev = _lib.require_gpu(H, w_in)
-        H = H.contiguous()
         w = _f32(w_in)
-        bi = torch.empty(B, S, D, device=dev, dtype=H.dtype)
-        lib = _lib.load()
-        with _lib.on_device(dev):
-            _lib.check(lib.mhc_layer_branch_input(H.data_ptr(), _lib.dtype_code(H), w.data_ptr(), bi.data_ptr(),
-                                                  B, S, D, _lib.stream(dev)), "layer_branch_input")
+        bi = branch_input(H, w)
         ctx.save_for_backward(H, w)
         ctx.stash = stash
         ctx.w_dtype = w_in.dtype
@@ -202,31 +327,9 @@ class _GenericLayer(torch.autograd.Function):
     @staticmethod
     def backward(ctx, d_bi, d_w):
         H, w = ctx.saved_tensors
-        B, S, _, D = H.shape
-        dev = H.device
         dH_new, dH_post = ctx.stash.take()
-        if d_bi is None:
-            d_bi = torch.zeros(B, S, D, device=dev, dtype=H.dtype)
-        d_bi = d_bi.contiguous().to(H.dtype)
-        if dH_new is not None:
-            dH_new = dH_new.contiguous().to(H.dtype)
-        dH = torch.empty_like(H) if ctx.needs_input_grad[0] else None
-        gw = torch.zeros(B, 24, device=dev, dtype=torch.float32)
-        dpre = torch.empty(B, 4, device=dev, dtype=torch.float32)
-        dres = torch.empty(B, 16, device=dev, dtype=torch.float32)
-        lib = _lib.load()
-        code = _lib.dtype_code(H)
-        ws = _ws(lib, B, S, D, code, dev)
-        with _lib.on_device(dev):
-            _lib.check(lib.mhc_layer_mix_backward(
-                H.data_ptr(), code, d_bi.data_ptr(), _lib.ptr(dH_new), w.data_ptr(), _lib.ptr(dH),
-                dpre.data_ptr(), dres.data_ptr(), B, S, D, *_wsargs(ws), _lib.stream(dev)), "layer_mix_backward")
-        gw[:, 0:4] = dpre
-        gw[:, 8:24] = dres
-        if dH_post is not None:
-            gw[:, 4:8] = dH_post
-        if d_w is not None:
-            gw = gw + d_w
+        dH, dpre, dres = mix_backward(H, d_bi, dH_new, w, need_dH=ctx.needs_input_grad[0])
+        gw = _generic_w_grad(dpre, dres, dH_post, d_w, H.shape[0], H.device)
         return dH, gw.to(ctx.w_dtype), None
 
 
@@ -236,39 +339,17 @@ class _LayerAdd(torch.autograd.Function):
 
     @staticmethod
     def forward(ctx, H, branch_output, w, stash: _Stash):
-        B, S, _, D = H.shape
-        if tuple(branch_output.shape) != (B, S, D):
-            raise ValueError(f"branch_output must be ({B}, {S}, {D}), got {tuple(branch_output.shape)}")
-        dev = _lib.require_gpu(H, branch_output, w)
-        H = H.contiguous()
-        bo = branch_output.contiguous()
-        H_new = torch.empty_like(H)
-        lib = _lib.load()
-        with _lib.on_device(dev):
-            _lib.check(lib.mhc_layer_add_forward(H.data_ptr(), _lib.dtype_code(H), bo.data_ptr(),
-                                                 _lib.dtype_code(bo), w.data_ptr(), H_new.data_ptr(), B, S, D,
-                                                 _lib.stream(dev)), "layer_add_forward")
-        ctx.save_for_backward(bo, w)
+        H_new = add_forward(H, branch_output, w)
+        ctx.save_for_backward(branch_output, w)
         ctx.stash = stash
-        ctx.shape = (B, S, D)
         ctx.h_dtype = H.dtype
         return H_new
 
     @staticmethod
     def backward(ctx, dH_new):
         bo, w = ctx.saved_tensors
-        B, S, D = ctx.shape
-        dev = bo.device
         dH_new = dH_new.contiguous().to(ctx.h_dtype)
-        d_bo = torch.empty_like(bo)
-        dH_post = torch.empty(B, 4, device=dev, dtype=torch.float32)
-        lib = _lib.load()
-        code = _lib.dtype_code(dH_new)
-        ws = _ws(lib, B, S, D, code, dev)
-        with _lib.on_device(dev):
-            _lib.check(lib.mhc_layer_add_backward(dH_new.data_ptr(), code, bo.data_ptr(), _lib.dtype_code(bo),
-                                                  w.data_ptr(), d_bo.data_ptr(), dH_post.data_ptr(), B, S, D,
-                                                  *_wsargs(ws), _lib.stream(dev)), "layer_add_backward")
+        d_bo, dH_post = add_backward(dH_new, bo, w)
         if ctx.needs_input_grad[2]:
             ctx.stash.put(dH_new, dH_post)
         return None, d_bo, None, None

@@ -1,0 +1,449 @@
+"""torch.library registrations of the HIP entry points (namespace ``mhc``).
+
+torch.compile cannot trace through the ctypes calls of the eager launchers, so
+each launcher is also registered as a custom op with a fake implementation
+(output shapes and dtypes only).  Traced code then sees opaque ``torch.ops.mhc.*``
+nodes and compiles the whole graph around them without a graph break.
+
+* The four public ops (reference src/mhc/ops.py:231-323) and the mean-pool
+  carry their backward as ``torch.library.register_autograd`` formulas that call
+  the backward ops.
+* The layer (reference src/mhc/module.py:103-182) uses two autograd nodes, as
+  in eager mode, but passes the closure's gradients to node A functionally:
+  node A returns a view of ``H`` (the *link*) that only the closure consumes;
+  the closure's backward returns ``dH_new`` as the link's gradient and
+  ``dH_post`` inside ``w``'s gradient, and node A writes the complete ``dH``
+  in one pass.  The eager path hands the same two tensors over through a
+  Python side channel (``_layer._Stash``), which traced code cannot express.
+
+Eager calls keep going through the launchers directly: a custom-op dispatch
+costs about 13 us of host time, more than some of the kernels it would wrap.
+"""
+
+from __future__ import annotations
+
+from typing import Optional, Tuple
+
+import torch
+import torch.nn.functional as F
+from torch import Tensor
+
+from . import _backward as _b
+from . import _kernels as _k
+from . import _layer as _l
+
+_F32 = torch.float32
+
+
+def _op(name: str):
+    return torch.library.custom_op(f"mhc::{name}", mutates_args=(), device_types="cuda")
+
+
+def _f32_like(ref: Tensor, *shape) -> Tensor:
+    return ref.new_empty(shape, dtype=_F32)
+
+
+# --------------------------------------------------------------------------
+# Sinkhorn-Knopp (reference _kernels.py:597, _backward.py:503)
+# --------------------------------------------------------------------------
+
+@_op("sinkhorn_forward")
+def sinkhorn_forward(M: Tensor, num_iters: int, eps: float) -> Tensor:
+    return _k.sinkhorn_forward(M, num_iters, eps)
+
+
+@sinkhorn_forward.register_fake
+def _(M, num_iters, eps):
+    return M.new_empty(M.shape)
+
+
+@_op("sinkhorn_backward")
+def sinkhorn_backward(M: Tensor, dP: Tensor, num_iters: int, eps: float) -> Tensor:
+    return _b.sinkhorn_backward(M, dP, num_iters, eps)
+
+
+@sinkhorn_backward.register_fake
+def _(M, dP, num_iters, eps):
+    return M.new_empty(M.shape)
+
+
+def _sinkhorn_setup(ctx, inputs, output):
+    M, num_iters, eps = inputs
+    ctx.save_for_backward(M)
+    ctx.num_iters = num_iters
+    ctx.eps = eps
+
+
+def _sinkhorn_bwd(ctx, dP):
+    M, = ctx.saved_tensors
+    return torch.ops.mhc.sinkhorn_backward(M, dP, ctx.num_iters, ctx.eps), None, None
+
+
+torch.library.register_autograd("mhc::sinkhorn_forward", _sinkhorn_bwd, setup_context=_sinkhorn_setup)
+
+
+# --------------------------------------------------------------------------
+# Stream mix (reference _kernels.py:617, _backward.py:578)
+# --------------------------------------------------------------------------
+
+@_op("stream_mix_forward")
+def stream_mix_forward(H: Tensor, H_pre: Tensor, H_res: Tensor) -> Tuple[Tensor, Tensor]:
+    return _k.stream_mix_forward(H, H_pre, H_res)
+
+
+@stream_mix_forward.register_fake
+def _(H, H_pre, H_res):
+    B, S, _, D = H.shape
+    return H.new_empty(B, S, D), H.new_empty(H.shape)
+
+
+@_op("stream_mix_backward")
+def stream_mix_backward(d_branch_input: Tensor, dH_residual: Tensor, H: Tensor, H_pre: Tensor,
+                        H_res: Tensor) -> Tuple[Tensor, Tensor, Tensor]:
+    return _b.stream_mix_backward(d_branch_input, dH_residual, H, H_pre, H_res)
+
+
+@stream_mix_backward.register_fake
+def _(d_branch_input, dH_residual, H, H_pre, H_res):
+    B = H.shape[0]
+    return H.new_empty(H.shape), H_pre.new_empty(B, 4), H_res.new_empty(B, 4, 4)
+
+
+def _mix_setup(ctx, inputs, output):
+    ctx.save_for_backward(*inputs)
+
+
+def _mix_bwd(ctx, d_bi, d_res):
+    H, H_pre, H_res = ctx.saved_tensors
+    if d_bi is None:
+        d_bi = H.new_zeros(H.shape[0], H.shape[1], H.shape[3])
+    if d_res is None:
+        d_res = torch.zeros_like(H)
+    return torch.ops.mhc.stream_mix_backward(d_bi, d_res, H, H_pre, H_res)
+
+
+torch.library.register_autograd("mhc::stream_mix_forward", _mix_bwd, setup_context=_mix_setup)
+
+
+# --------------------------------------------------------------------------
+# Add residual (reference _kernels.py:655, _backward.py:533)
+# --------------------------------------------------------------------------
+
+@_op("add_residual_forward")
+def add_residual_forward(H_residual: Tensor, branch_output: Tensor, H_post: Tensor) -> Tensor:
+    return _k.add_residual_forward(H_residual, branch_output, H_post)
+
+
+@add_residual_forward.register_fake
+def _(H_residual, branch_output, H_post):
+    return H_residual.new_empty(H_residual.shape)
+
+
+@_op("add_residual_backward")
+def add_residual_backward(dH_new: Tensor, branch_output: Tensor, H_post: Tensor) -> Tuple[Tensor, Tensor]:
+    """(d_branch_output, dH_post); dH_residual is dH_new itself and is not an output."""
+    _, d_bo, dpost = _b.add_residual_backward(dH_new, branch_output, H_post)
+    return d_bo, dpost
+
+
+@add_residual_backward.register_fake
+def _(dH_new, branch_output, H_post):
+    return branch_output.new_empty(branch_output.shape), H_post.new_empty(dH_new.shape[0], 4)
+
+
+def _add_setup(ctx, inputs, output):
+    H_residual, bo, H_post = inputs
+    ctx.save_for_backward(bo, H_post)
+
+
+def _add_bwd(ctx, dH_new):
+    bo, H_post = ctx.saved_tensors
+    d_bo, dpost = torch.ops.mhc.add_residual_backward(dH_new, bo, H_post)
+    return dH_new, d_bo, dpost
+
+
+torch.library.register_autograd("mhc::add_residual_forward", _add_bwd, setup_context=_add_setup)
+
+
+# --------------------------------------------------------------------------
+# Dynamic weights (reference _kernels.py:690, ops.py:72-228)
+# --------------------------------------------------------------------------
+
+@_op("dynamic_weights_forward")
+def dynamic_weights_forward(x: Tensor, phi: Tensor, bias: Tensor, alpha_pre: Tensor, alpha_post: Tensor,
+                            alpha_res: Tensor, sinkhorn_iters: int,
+                            eps: float) -> Tuple[Tensor, Tensor, Tensor, Tensor]:
+    """(H_pre [R,4], H_post [R,4], H_res [R,4,4], aux [R,25]), all f32."""
+    return _k.fused_dynamic_weights_forward(x, phi, bias, alpha_pre, alpha_post, alpha_res, sinkhorn_iters,
+                                            eps, return_aux=True)
+
+
+@dynamic_weights_forward.register_fake
+def _(x, phi, bias, alpha_pre, alpha_post, alpha_res, sinkhorn_iters, eps):
+    R = x.shape[0]
+    return _f32_like(x, R, 4), _f32_like(x, R, 4), _f32_like(x, R, 4, 4), _f32_like(x, R, 25)
+
+
+@_op("dynamic_weights_backward")
+def dynamic_weights_backward(x: Tensor, phi: Tensor, bias: Tensor, alpha_pre: Tensor, alpha_post: Tensor,
+                             alpha_res: Tensor, aux: Tensor, H_pre: Tensor, grad_H_pre: Optional[Tensor],
+                             grad_H_post: Optional[Tensor], grad_H_res: Optional[Tensor], sinkhorn_iters: int,
+                             eps: float) -> Tuple[Tensor, Tensor, Tensor, Tensor]:
+    """(grad_x in x's dtype, grad_phi [K,24], grad_bias [24], grad_alpha [3]), parameter grads f32."""
+    alphas = [_k._alpha_tensor(a, x.device) for a in (alpha_pre, alpha_post, alpha_res)]
+    return _b.fused_dynamic_weights_backward(
+        x, phi, bias, alphas, aux, H_pre, grad_H_pre, grad_H_post,
+        None if grad_H_res is None else grad_H_res.reshape(-1, 16), sinkhorn_iters, eps)
+
+
+@dynamic_weights_backward.register_fake
+def _(x, phi, bias, alpha_pre, alpha_post, alpha_res, aux, H_pre, grad_H_pre, grad_H_post, grad_H_res,
+      sinkhorn_iters, eps):
+    R, K = x.shape
+    return x.new_empty(R, K), _f32_like(x, K, 24), _f32_like(x, 24), _f32_like(x, 3)
+
+
+def _dynw_setup(ctx, inputs, output):
+    x, phi, bias, a_pre, a_post, a_res, iters, eps = inputs
+    H_pre, _, _, aux = output
+    ctx.save_for_backward(x, phi, bias, a_pre, a_post, a_res, H_pre, aux)
+    ctx.iters = iters
+    ctx.eps = eps
+    ctx.mark_non_differentiable(aux)
+    ctx.set_materialize_grads(False)
+
+
+def _dynw_bwd(ctx, g_pre, g_post, g_res, g_aux):
+    x, phi, bias, a_pre, a_post, a_res, H_pre, aux = ctx.saved_tensors
+    gx, gphi, gbias, galpha = torch.ops.mhc.dynamic_weights_backward(
+        x, phi, bias, a_pre, a_post, a_res, aux, H_pre, g_pre, g_post, g_res, ctx.iters, ctx.eps)
+    return (gx, gphi.to(phi.dtype), gbias.to(bias.dtype),
+            galpha[0:1].reshape(a_pre.shape).to(a_pre.dtype), galpha[1:2].reshape(a_post.shape).to(a_post.dtype),
+            galpha[2:3].reshape(a_res.shape).to(a_res.dtype), None, None)
+
+
+torch.library.register_autograd("mhc::dynamic_weights_forward", _dynw_bwd, setup_context=_dynw_setup)
+
+
+# --------------------------------------------------------------------------
+# Mean-pool (reference module.py:123)
+# --------------------------------------------------------------------------
+
+@_op("mean_pool")
+def mean_pool(H: Tensor) -> Tensor:
+    """x [B, 4*dim] f32 = mean of H over the sequence, stream-major."""
+    return _k.mean_pool(H)
+
+
+@mean_pool.register_fake
+def _(H):
+    B, _, n, D = H.shape
+    return _f32_like(H, B, n * D)
+
+
+def _pool_setup(ctx, inputs, output):
+    H, = inputs
+    ctx.shape = H.shape
+    ctx.dtype = H.dtype
+
+
+def _pool_bwd(ctx, gx):
+    B, S, n, D = ctx.shape
+    return (gx / S).to(ctx.dtype).reshape(B, 1, n, D).expand(B, S, n, D)
+
+
+torch.library.register_autograd("mhc::mean_pool", _pool_bwd, setup_context=_pool_setup)
+
+
+# --------------------------------------------------------------------------
+# Layer-level entry points (include/mhc_abi.h mhc_layer_*)
+# --------------------------------------------------------------------------
+
+@_op("layer_dynamic_forward")
+def layer_dynamic_forward(H: Tensor, phi: Tensor, H_pre_base: Tensor, H_post_base: Tensor, H_res_base: Tensor,
+                          alpha_pre: Tensor, alpha_post: Tensor, alpha_res: Tensor, iters: int,
+                          eps: float) -> Tuple[Tensor, Tensor, Tensor, Tensor]:
+    """(branch_input, x [B,4D] f32, w [B,24] f32, aux [B,25] f32)."""
+    return _l.dynamic_forward(H, phi, H_pre_base, H_post_base, H_res_base, alpha_pre, alpha_post, alpha_res,
+                              iters, eps)
+
+
+@layer_dynamic_forward.register_fake
+def _(H, phi, H_pre_base, H_post_base, H_res_base, alpha_pre, alpha_post, alpha_res, iters, eps):
+    B, S, _, D = H.shape
+    return H.new_empty(B, S, D), _f32_like(H, B, 4 * D), _f32_like(H, B, 24), _f32_like(H, B, 25)
+
+
+@_op("layer_dynamic_backward")
+def layer_dynamic_backward(H: Tensor, d_bi: Optional[Tensor], dH_new: Optional[Tensor], dH_post: Optional[Tensor],
+                           phi: Tensor, H_pre_base: Tensor, H_post_base: Tensor, H_res_base: Tensor,
+                           alpha_pre: Tensor, alpha_post: Tensor, alpha_res: Tensor, x: Tensor, w: Tensor,
+                           aux: Tensor, iters: int, eps: float) -> Tuple[Tensor, Tensor, Tensor, Tensor]:
+    """(dH, grad_phi [4D,24], grad_bias [24], grad_alpha [3]), parameter grads f32."""
+    return _l.dynamic_backward(H, d_bi, dH_new, dH_post, phi, H_pre_base, H_post_base, H_res_base, alpha_pre,
+                               alpha_post, alpha_res, x, w, aux, iters, eps)
+
+
+@layer_dynamic_backward.register_fake
+def _(H, d_bi, dH_new, dH_post, phi, H_pre_base, H_post_base, H_res_base, alpha_pre, alpha_post, alpha_res,
+      x, w, aux, iters, eps):
+    D = H.shape[3]
+    return H.new_empty(H.shape), _f32_like(H, 4 * D, 24), _f32_like(H, 24), _f32_like(H, 3)
+
+
+@_op("layer_static_forward")
+def layer_static_forward(H: Tensor, H_pre_base: Tensor, H_post_base: Tensor, H_res_base: Tensor,
+                         iters: int) -> Tuple[Tensor, Tensor]:
+    """(branch_input, w [B,24] f32)."""
+    return _l.static_forward(H, H_pre_base, H_post_base, H_res_base, iters)
+
+
+@layer_static_forward.register_fake
+def _(H, H_pre_base, H_post_base, H_res_base, iters):
+    B, S, _, D = H.shape
+    return H.new_empty(B, S, D), _f32_like(H, B, 24)
+
+
+@_op("layer_static_backward")
+def layer_static_backward(H: Tensor, d_bi: Optional[Tensor], dH_new: Optional[Tensor], dH_post: Optional[Tensor],
+                          H_pre_base: Tensor, H_post_base: Tensor, H_res_base: Tensor, w: Tensor,
+                          iters: int) -> Tuple[Tensor, Tensor]:
+    """(dH, grad_bias [24] f32)."""
+    return _l.static_backward(H, d_bi, dH_new, dH_post, H_pre_base, H_post_base, H_res_base, w, iters)
+
+
+@layer_static_backward.register_fake
+def _(H, d_bi, dH_new, dH_post, H_pre_base, H_post_base, H_res_base, w, iters):
+    return H.new_empty(H.shape), _f32_like(H, 24)
+
+
+@_op("layer_branch_input")
+def layer_branch_input(H: Tensor, w: Tensor) -> Tensor:
+    return _l.branch_input(H, w)
+
+
+@layer_branch_input.register_fake
+def _(H, w):
+    B, S, _, D = H.shape
+    return H.new_empty(B, S, D)
+
+
+@_op("layer_mix_backward")
+def layer_mix_backward(H: Tensor, d_bi: Optional[Tensor], dH_new: Optional[Tensor],
+                       w: Tensor) -> Tuple[Tensor, Tensor, Tensor]:
+    """(dH, dH_pre [B,4] f32, dH_res [B,16] f32)."""
+    return _l.mix_backward(H, d_bi, dH_new, w)
+
+
+@layer_mix_backward.register_fake
+def _(H, d_bi, dH_new, w):
+    B = H.shape[0]
+    return H.new_empty(H.shape), _f32_like(H, B, 4), _f32_like(H, B, 16)
+
+
+@_op("layer_add_forward")
+def layer_add_forward(H: Tensor, branch_output: Tensor, w: Tensor) -> Tensor:
+    return _l.add_forward(H, branch_output, w)
+
+
+@layer_add_forward.register_fake
+def _(H, branch_output, w):
+    return H.new_empty(H.shape)
+
+
+@_op("layer_add_backward")
+def layer_add_backward(dH_new: Tensor, branch_output: Tensor, w: Tensor) -> Tuple[Tensor, Tensor]:
+    """(d_branch_output, dH_post [B,4] f32)."""
+    return _l.add_backward(dH_new, branch_output, w)
+
+
+@layer_add_backward.register_fake
+def _(dH_new, branch_output, w):
+    return branch_output.new_empty(branch_output.shape), _f32_like(dH_new, dH_new.shape[0], 4)
+
+
+def _link_grads(d_w: Optional[Tensor]) -> Optional[Tensor]:
+    """dH_post, as the closure stores it in w's gradient (columns 4:8)."""
+    return None if d_w is None else d_w[:, 4:8].contiguous()
+
+
+class DynamicLayer(torch.autograd.Function):
+    """Node A, dynamic fused weights: H -> (branch_input, w, link)."""
+
+    @staticmethod
+    def forward(ctx, H, phi, H_pre_base, H_post_base, H_res_base, alpha_pre, alpha_post, alpha_res,
+                iters: int, eps: float):
+        params = (phi, H_pre_base, H_post_base, H_res_base, alpha_pre, alpha_post, alpha_res)
+        bi, x, w, aux = torch.ops.mhc.layer_dynamic_forward(H, *params, iters, eps)
+        ctx.save_for_backward(H, x, w, aux, *params)
+        ctx.iters = iters
+        ctx.eps = eps
+        ctx.set_materialize_grads(False)
+        return bi, w, H.view_as(H)
+
+    @staticmethod
+    def backward(ctx, d_bi, d_w, d_link):
+        H, x, w, aux, *params = ctx.saved_tensors
+        dH, gphi, gbias, galpha = torch.ops.mhc.layer_dynamic_backward(
+            H, d_bi, d_link, _link_grads(d_w), *params, x, w, aux, ctx.iters, ctx.eps)
+        return (dH, *_l._dynamic_param_grads(params, gphi, gbias, galpha), None, None)
+
+
+class StaticLayer(torch.autograd.Function):
+    """Node A, static weights: H -> (branch_input, w, link)."""
+
+    @staticmethod
+    def forward(ctx, H, H_pre_base, H_post_base, H_res_base, iters: int):
+        params = (H_pre_base, H_post_base, H_res_base)
+        bi, w = torch.ops.mhc.layer_static_forward(H, *params, iters)
+        ctx.save_for_backward(H, w, *params)
+        ctx.iters = iters
+        ctx.set_materialize_grads(False)
+        return bi, w, H.view_as(H)
+
+    @staticmethod
+    def backward(ctx, d_bi, d_w, d_link):
+        H, w, *params = ctx.saved_tensors
+        dH, gbias = torch.ops.mhc.layer_static_backward(H, d_bi, d_link, _link_grads(d_w), *params, w, ctx.iters)
+        return (dH, *_l._static_param_grads(params, gbias), None)
+
+
+class GenericLayer(torch.autograd.Function):
+    """Node A for weights produced by torch ops (the unfused dynamic path): (H, w) -> (branch_input, w, link)."""
+
+    @staticmethod
+    def forward(ctx, H, w_in):
+        w = w_in.float()
+        bi = torch.ops.mhc.layer_branch_input(H, w)
+        ctx.save_for_backward(H, w)
+        ctx.w_dtype = w_in.dtype
+        ctx.set_materialize_grads(False)
+        return bi, w.clone() if w is w_in else w, H.view_as(H)
+
+    @staticmethod
+    def backward(ctx, d_bi, d_w, d_link):
+        H, w = ctx.saved_tensors
+        dH, dpre, dres = torch.ops.mhc.layer_mix_backward(H, d_bi, d_link, w)
+        gw = torch.cat([dpre, torch.zeros_like(dpre), dres], dim=1)
+        if d_w is not None:
+            gw = gw + d_w  # includes the closure's dH_post in columns 4:8
+        return dH, gw.to(ctx.w_dtype)
+
+
+class LayerAdd(torch.autograd.Function):
+    """Node B, the closure: (link, branch_output, w) -> H_new.  Its backward returns
+    dH_new as the link's gradient and dH_post in columns 4:8 of w's gradient, for
+    node A to consume (neither is the true gradient of those inputs)."""
+
+    @staticmethod
+    def forward(ctx, link, branch_output, w):
+        ctx.save_for_backward(branch_output, w)
+        ctx.h_dtype = link.dtype
+        return torch.ops.mhc.layer_add_forward(link, branch_output, w)
+
+    @staticmethod
+    def backward(ctx, dH_new):
+        bo, w = ctx.saved_tensors
+        dH_new = dH_new.to(ctx.h_dtype)
+        d_bo, dH_post = torch.ops.mhc.layer_add_backward(dH_new, bo, w)
+        return dH_new, d_bo, F.pad(dH_post, (4, 16))

@@ -13,7 +13,7 @@ from typing import Callable, Tuple
 import torch
 import torch.nn as nn
 
-from . import _layer
+from . import _layer, _library
 from ._kernels import mean_pool
 from .ops import sinkhorn_knopp
 
@@ -95,13 +95,14 @@ class HyperConnection(nn.Module):
         if H.dim() != 4 or H.shape[2] != self.num_streams or H.shape[3] != self.dim:
             raise ValueError(f"H must be (batch, seq, {self.num_streams}, {self.dim}), got {tuple(H.shape)}")
 
-    def _unfused_weights(self, H: torch.Tensor) -> torch.Tensor:
+    def _unfused_weights(self, H: torch.Tensor, traced: bool = False) -> torch.Tensor:
         """Packed weights [B,24] of the unfused dynamic path (reference
         src/mhc/module.py:141-163): RMS-normalised mean, three Linears, sigmoid
         (no x2 on H_post), normalisation with 1e-8 and Sinkhorn with eps 1e-8."""
         B = H.shape[0]
         n = self.num_streams
-        x = _MeanPool.apply(H).to(self.W_pre.weight.dtype)
+        pooled = torch.ops.mhc.mean_pool(H) if traced else _MeanPool.apply(H)
+        x = pooled.to(self.W_pre.weight.dtype)
         rms = torch.sqrt((x * x).mean(dim=-1, keepdim=True) + self.eps)
         x = x / rms
         delta_post = self.W_post(x) * self.scale_post
@@ -110,12 +111,18 @@ class HyperConnection(nn.Module):
         H_post = torch.sigmoid(self.H_post_base + delta_post)
         H_pre = torch.sigmoid(self.H_pre_base + delta_pre)
         H_pre = H_pre / (H_pre.sum(dim=-1, keepdim=True) + 1e-8)
-        H_res = sinkhorn_knopp((self.H_res_base + delta_res).contiguous(), self.sinkhorn_iters)
+        M = (self.H_res_base + delta_res).contiguous()
+        if traced:
+            H_res = torch.ops.mhc.sinkhorn_forward(M, self.sinkhorn_iters, 1e-8)
+        else:
+            H_res = sinkhorn_knopp(M, self.sinkhorn_iters)
         return torch.cat([H_pre, H_post, H_res.reshape(B, n * n)], dim=1)
 
     def forward(self, H: torch.Tensor) -> Tuple[torch.Tensor, Callable[[torch.Tensor], torch.Tensor]]:
         """H (batch, seq, 4, dim) -> (branch_input (batch, seq, dim), add_residual)."""
         self._check_input(H)
+        if torch.compiler.is_compiling():
+            return self._forward_traced(H)
         stash = _layer._Stash()
         if not self.dynamic:
             bi, w = _layer._StaticLayer.apply(H, self.H_pre_base, self.H_post_base, self.H_res_base, stash,
@@ -129,6 +136,24 @@ class HyperConnection(nn.Module):
 
         def add_residual(branch_output: torch.Tensor) -> torch.Tensor:
             return _layer._LayerAdd.apply(H, branch_output, w, stash)
+
+        return bi, add_residual
+
+    def _forward_traced(self, H: torch.Tensor):
+        """The same two nodes as ``forward``, on the torch.library ops, with the closure's
+        gradients passed to node A through a link output instead of a side channel."""
+        if not self.dynamic:
+            bi, w, link = _library.StaticLayer.apply(H, self.H_pre_base, self.H_post_base, self.H_res_base,
+                                                     self.sinkhorn_iters)
+        elif self.use_fused_weights:
+            bi, w, link = _library.DynamicLayer.apply(H, self.phi, self.H_pre_base, self.H_post_base,
+                                                      self.H_res_base, self.alpha_pre, self.alpha_post,
+                                                      self.alpha_res, self.sinkhorn_iters, self.eps)
+        else:
+            bi, w, link = _library.GenericLayer.apply(H, self._unfused_weights(H, traced=True))
+
+        def add_residual(branch_output: torch.Tensor) -> torch.Tensor:
+            return _library.LayerAdd.apply(link, branch_output, w)
 
         return bi, add_residual
 

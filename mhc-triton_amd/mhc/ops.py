@@ -12,6 +12,7 @@ import torch
 
 from . import _backward as _bwd
 from . import _kernels as _k
+from . import _library  # noqa: F401  (registers torch.ops.mhc.*)
 
 
 class _SinkhornKnopp(torch.autograd.Function):
@@ -99,16 +100,22 @@ class _FusedDynamicWeights(torch.autograd.Function):
 
 def sinkhorn_knopp(M: torch.Tensor, num_iters: int = 20, eps: float = 1e-8) -> torch.Tensor:
     """Project (batch, 4, 4) matrices to doubly stochastic via Sinkhorn-Knopp."""
+    if torch.compiler.is_compiling():
+        return torch.ops.mhc.sinkhorn_forward(M, num_iters, eps)
     return _SinkhornKnopp.apply(M, num_iters, eps)
 
 
 def fused_stream_mix(H: torch.Tensor, H_pre: torch.Tensor, H_res: torch.Tensor) -> Tuple[torch.Tensor, torch.Tensor]:
     """branch_input (batch, seq, dim) and H_residual (batch, seq, 4, dim) of H (batch, seq, 4, dim)."""
+    if torch.compiler.is_compiling():
+        return torch.ops.mhc.stream_mix_forward(H, H_pre, H_res)
     return _FusedStreamMix.apply(H, H_pre, H_res)
 
 
 def fused_add_residual(H_residual: torch.Tensor, branch_output: torch.Tensor, H_post: torch.Tensor) -> torch.Tensor:
     """H_new[n] = H_residual[n] + H_post[n] * branch_output."""
+    if torch.compiler.is_compiling():
+        return torch.ops.mhc.add_residual_forward(H_residual, branch_output, H_post)
     return _FusedAddResidual.apply(H_residual, branch_output, H_post)
 
 
@@ -123,4 +130,8 @@ def fused_dynamic_weights(
     eps: float = 1e-6,
 ) -> Tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
     """(H_pre [batch,4], H_post [batch,4], H_res [batch,4,4]) from x [batch, 4*dim] (Eq. 14-19)."""
+    if torch.compiler.is_compiling():
+        alphas = [a if isinstance(a, torch.Tensor) else torch.tensor([float(a)], device=x.device)
+                  for a in (alpha_pre, alpha_post, alpha_res)]
+        return torch.ops.mhc.dynamic_weights_forward(x, phi, bias, *alphas, sinkhorn_iters, eps)[:3]
     return _FusedDynamicWeights.apply(x, phi, bias, alpha_pre, alpha_post, alpha_res, sinkhorn_iters, eps)

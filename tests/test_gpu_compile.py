@@ -1,0 +1,197 @@
+"""torch.compile over the HIP path, and torch.library.opcheck of every registered op.
+
+Compiled (``fullgraph=True``: any graph break fails the test) and eager runs of
+the same step launch the same kernels in the same order, so outputs and every
+gradient must agree bit for bit.  The compiled layer hands the closure's
+gradients to node A through a link output instead of the eager side channel;
+this is what the equality checks.  ``aot_eager`` runs the traced graph with
+torch's own kernels around the ``torch.ops.mhc`` nodes.
+"""
+
+import pytest
+import torch
+
+import mhc
+
+pytestmark = pytest.mark.gpu
+
+DEV = "cuda"
+
+
+def _compile(fn, dynamic=False):
+    torch._dynamo.reset()
+    return torch.compile(fn, backend="aot_eager", fullgraph=True, dynamic=dynamic)
+
+
+def _layer_case(dynamic, fused, dtype, B=2, S=64, D=256, seed=0):
+    g = torch.Generator().manual_seed(seed)
+    hc = mhc.HyperConnection(D, dynamic=dynamic, use_fused_weights=fused, layer_idx=1)
+    with torch.no_grad():
+        if dynamic and fused:
+            hc.phi.copy_(torch.randn(hc.phi.shape, generator=g) * 0.02)
+        if dynamic and not fused:
+            for lin in (hc.W_pre, hc.W_post, hc.W_res):
+                lin.weight.copy_(torch.randn(lin.weight.shape, generator=g) * 0.02)
+        hc.H_res_base.add_(torch.randn((4, 4), generator=g) * 0.5)
+    H = torch.randn((B, S, 4, D), generator=g).to(dtype)
+    W = torch.randn((D, D), generator=g) / D ** 0.5
+    gHn = torch.randn((B, S, 4, D), generator=g).to(dtype)
+    gbi = torch.randn((B, S, D), generator=g).to(dtype)
+    return hc.to(DEV), H.to(DEV), W.to(DEV), gHn.to(DEV), gbi.to(DEV)
+
+
+def _run(step, hc, H, W, gHn, gbi, calls):
+    hc.zero_grad(set_to_none=True)
+    Hl = H.clone().requires_grad_(True)
+    Wl = W.clone().requires_grad_(True)
+    outs = step(Hl, Wl)
+    grads = [gbi] + [gHn * (k + 1) for k in range(calls)]
+    torch.autograd.backward(list(outs), grads)
+    res = {"out%d" % i: o.detach() for i, o in enumerate(outs)}
+    res["H"] = Hl.grad
+    res["W"] = Wl.grad
+    for n, p in hc.named_parameters():
+        res[n] = p.grad
+    return res
+
+
+def _assert_identical(a, b):
+    assert a.keys() == b.keys()
+    for k in a:
+        if a[k] is None or b[k] is None:
+            assert a[k] is None and b[k] is None, k
+            continue
+        assert a[k].dtype == b[k].dtype and a[k].shape == b[k].shape, k
+        assert torch.equal(a[k], b[k]), (k, float((a[k].float() - b[k].float()).abs().max()))
+
+
+@pytest.mark.parametrize("dtype,calls", [(torch.bfloat16, 1), (torch.bfloat16, 0), (torch.bfloat16, 2),
+                                         (torch.float32, 1)])
+@pytest.mark.parametrize("dynamic,fused", [(True, True), (False, True), (True, False)])
+def test_compiled_layer_step_matches_eager_bitwise(dynamic, fused, dtype, calls):
+    hc, H, W, gHn, gbi = _layer_case(dynamic, fused, dtype)
+
+    def step(Hl, Wl):
+        bi, add = hc(Hl)
+        outs = [bi]
+        for k in range(calls):
+            bo = torch.tanh(bi.float() @ Wl * (k + 1)).to(bi.dtype)  # the caller's layer
+            outs.append(add(bo))
+        return outs
+
+    eager = _run(step, hc, H, W, gHn, gbi, calls)
+    compiled = _run(_compile(step), hc, H, W, gHn, gbi, calls)
+    _assert_identical(eager, compiled)
+    assert eager["H"] is not None and torch.isfinite(eager["H"].float()).all()
+
+
+def _step_of(hc):
+    def step(Hl, Wl):
+        bi, add = hc(Hl)
+        return [bi, add(torch.tanh(bi.float() @ Wl).to(bi.dtype))]
+    return step
+
+
+def test_compiled_layer_with_dynamic_shapes():
+    """One compiled graph serves three sequence lengths (symbolic shapes through the fake kernels)."""
+    from torch._dynamo.utils import counters
+
+    hc, H, W, gHn, gbi = _layer_case(True, True, torch.bfloat16, S=96)
+    step = _step_of(hc)
+    step_c = _compile(step, dynamic=True)
+    counters.clear()
+    for S in (64, 96, 33):
+        case = (H[:, :S].contiguous(), W, gHn[:, :S].contiguous(), gbi[:, :S].contiguous())
+        _assert_identical(_run(step, hc, *case, 1), _run(step_c, hc, *case, 1))
+    assert counters["stats"]["unique_graphs"] == 1
+
+
+def test_compiled_public_ops_match_eager_bitwise():
+    g = torch.Generator().manual_seed(1)
+    B, S, D = 2, 32, 128
+    H = torch.randn((B, S, 4, D), generator=g).bfloat16().to(DEV)
+    x = torch.randn((B, 4 * D), generator=g).to(DEV)
+    phi = (torch.randn((4 * D, 24), generator=g) * 0.05).to(DEV)
+    bias = torch.randn(24, generator=g).to(DEV)
+    alphas = [torch.tensor([0.3], device=DEV), torch.tensor([0.2], device=DEV), torch.tensor([0.1], device=DEV)]
+    M = torch.exp(torch.randn((64, 4, 4), generator=g)).to(DEV)
+    bo = torch.randn((B, S, D), generator=g).bfloat16().to(DEV)
+
+    def fn(H, x, phi, bias, a0, a1, a2, M, bo):
+        pre, post, res = mhc.fused_dynamic_weights(x, phi, bias, a0, a1, a2)
+        bi, hres = mhc.fused_stream_mix(H, pre, res)
+        Hn = mhc.fused_add_residual(hres, bo * bi, post)
+        P = mhc.sinkhorn_knopp(M, 20)
+        return Hn.float().square().mean() + P.square().sum() + bi.float().mean()
+
+    def run(f):
+        leaves = [t.clone().requires_grad_(True) for t in (H, x, phi, bias, *alphas, M, bo)]
+        loss = f(*leaves)
+        loss.backward()
+        return {"loss": loss.detach(), **{"g%d" % i: t.grad for i, t in enumerate(leaves)}}
+
+    _assert_identical(run(fn), run(_compile(fn)))
+
+
+_CASES = []
+
+
+def _opcheck_cases():
+    if _CASES:
+        return _CASES
+    g = torch.Generator().manual_seed(2)
+    B, S, D, R, K = 2, 16, 64, 3, 256
+    r = lambda *s, dt=torch.float32: torch.randn(s, generator=g).to(dt).to(DEV)  # noqa: E731
+    H, bi, bo = r(B, S, 4, D, dt=torch.bfloat16), r(B, S, D, dt=torch.bfloat16), r(B, S, D, dt=torch.bfloat16)
+    pre = torch.softmax(r(B, 4), -1)
+    post = torch.sigmoid(r(B, 4)) * 2
+    M = torch.exp(r(5, 4, 4))
+    res = mhc.sinkhorn_knopp(M[:B].clone(), 20)
+    a = [torch.tensor([0.1], device=DEV) for _ in range(3)]
+    x, phi, bias = r(R, K), r(K, 24) * 0.02, r(24)
+    Hp, Hpo, Hr, aux = torch.ops.mhc.dynamic_weights_forward(x, phi, bias, *a, 20, 1e-6)
+    base = [r(4), r(4), r(4, 4)]
+    phiL = r(4 * D, 24) * 0.02
+    biL, xL, wL, auxL = torch.ops.mhc.layer_dynamic_forward(H, phiL, *base, *a, 20, 1e-6)
+    _, wS = torch.ops.mhc.layer_static_forward(H, *base, 20)
+    dpost = r(B, 4)
+    rg = lambda t: t.clone().requires_grad_(True)  # noqa: E731
+    _CASES.extend([
+        ("sinkhorn_forward", (rg(M), 20, 1e-8)),
+        ("sinkhorn_backward", (M, r(5, 4, 4), 20, 1e-8)),
+        ("stream_mix_forward", (rg(H.float()), rg(pre), rg(res))),
+        ("stream_mix_backward", (bi, H, H, pre, res)),
+        ("add_residual_forward", (rg(H.float()), rg(bo.float()), rg(post))),
+        ("add_residual_backward", (H, bo, post)),
+        ("dynamic_weights_forward", (rg(x), rg(phi), rg(bias), *[rg(t) for t in a], 20, 1e-6)),
+        ("dynamic_weights_backward", (x, phi, bias, *a, aux, Hp, r(R, 4), None, r(R, 4, 4), 20, 1e-6)),
+        ("mean_pool", (rg(H.float()),)),
+        ("layer_dynamic_forward", (H, phiL, *base, *a, 20, 1e-6)),
+        ("layer_dynamic_backward", (H, bi, H, dpost, phiL, *base, *a, xL, wL, auxL, 20, 1e-6)),
+        ("layer_dynamic_backward", (H, bi, None, None, phiL, *base, *a, xL, wL, auxL, 20, 1e-6)),
+        ("layer_static_forward", (H, *base, 20)),
+        ("layer_static_backward", (H, bi, H, dpost, *base, wS, 20)),
+        ("layer_branch_input", (H, wL)),
+        ("layer_mix_backward", (H, bi, H, wL)),
+        ("layer_add_forward", (H, bo, wL)),
+        ("layer_add_backward", (H, bo, wL)),
+    ])
+    return _CASES
+
+
+N_CASES = 18
+
+
+def test_opcheck_covers_every_registered_op():
+    cases = _opcheck_cases()
+    assert len(cases) == N_CASES
+    assert {n for n, _ in cases} == {n for n in dir(torch.ops.mhc) if not n.startswith("_") and n != "name"}
+
+
+@pytest.mark.parametrize("idx", range(N_CASES))
+def test_opcheck(idx):
+    """Schema (no mutation, no aliasing), fake kernel against the real one (shapes,
+    dtypes, strides), autograd registration and AOT dispatch with dynamic shapes."""
+    name, args = _opcheck_cases()[idx]
+    print(f"opcheck mhc::{name}", flush=True)
+    torch.library.opcheck(getattr(torch.ops.mhc, name).default, args)
