@@ -2,6 +2,7 @@
 """mHC layer forward+backward throughput on one MI355X.
 
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload config3]
+    python bench.py --ops        # the low-level ops one by one (one JSON line)
 
 One "step" is the HyperConnection layer's forward and backward over one
 synthetic batch, exactly as a transformer block uses it:
@@ -78,6 +79,9 @@ def _parse():
     ap.add_argument("--workload", default="config3", choices=sorted(WORKLOADS))
     ap.add_argument("--cpu-seconds", type=float, default=12.0,
                     help="target CPU time of the cpu_baseline sample (0 disables it)")
+    ap.add_argument("--ops", action="store_true",
+                    help="time the low-level ops one by one (config-2 Sinkhorn, the stream ops and "
+                         "expand / collapse at config-3 size, dynamic weights) and exit")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="only run 3 plain device copies of 512 MiB (the known-size kernel that scales "
                          "rocprofv3 FETCH_SIZE / WRITE_SIZE readings into bytes) and exit")
@@ -98,6 +102,87 @@ def _calibrate_copy() -> int:
     print(json.dumps({"calibration": "device copy", "bytes_read": COPY_BYTES, "bytes_written": COPY_BYTES,
                       "launches": 3}), flush=True)
     return 0
+
+
+def _ops_leg(n: int = 20, warm: int = 3) -> dict:
+    """Each low-level op alone, timed with HIP events on torch's current stream
+    (the stream the kernels run on): mean time per call and the fraction of
+    8 TB/s its algorithmic bytes reach.  Inputs are resident before timing;
+    gradient calls use torch.autograd.grad, so nothing accumulates between calls."""
+    import torch
+
+    import mhc
+    from mhc import _backward as KB
+    from mhc import _kernels as K
+
+    dev = "cuda"
+    g = torch.Generator(device=dev)
+    g.manual_seed(0)
+
+    def timed(fn, calls=n):
+        for _ in range(warm):
+            fn()
+        torch.cuda.synchronize()
+        a = torch.cuda.Event(enable_timing=True)
+        b = torch.cuda.Event(enable_timing=True)
+        a.record()
+        for _ in range(calls):
+            fn()
+        b.record()
+        torch.cuda.synchronize()
+        return a.elapsed_time(b) / calls * 1e3  # us
+
+    out = {}
+
+    def rec(name, us, nbytes):
+        out[name] = {"us": round(us, 1), "hbm_frac": round(nbytes / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4)}
+
+    # config 2: Sinkhorn over 2^20 fp32 matrices (fwd reads M, writes P; bwd reads M, dP, writes dM)
+    M = torch.exp(torch.randn((1 << 20, 4, 4), generator=g, device=dev))
+    dP = torch.randn((1 << 20, 4, 4), generator=g, device=dev)
+    rec("sinkhorn_fwd config2", timed(lambda: K.sinkhorn_forward(M, 20, 1e-8)), 2 * M.numel() * 4)
+    rec("sinkhorn_bwd config2", timed(lambda: KB.sinkhorn_backward(M, dP, 20, 1e-8)), 3 * M.numel() * 4)
+    del M, dP
+    # the stream ops at config-3 size, bf16
+    B, S, D = 4, 4096, 4096
+    e, T = 2, B * S
+    H = torch.randn((B, S, 4, D), generator=g, device=dev).bfloat16()
+    pre = torch.softmax(torch.randn((B, 4), generator=g, device=dev), -1)
+    res = K.sinkhorn_forward(torch.randn((B, 4, 4), generator=g, device=dev), 20, 1e-8)
+    post = torch.rand((B, 4), generator=g, device=dev) * 2
+    bo = torch.randn((B, S, D), generator=g, device=dev).bfloat16()
+    rec("stream_mix_fwd config3", timed(lambda: K.stream_mix_forward(H, pre, res)), 9 * D * e * T)
+    bi, hr = K.stream_mix_forward(H, pre, res)
+    rec("add_residual_fwd config3", timed(lambda: K.add_residual_forward(hr, bo, post)), 9 * D * e * T)
+    dhn = torch.randn((B, S, 4, D), generator=g, device=dev).bfloat16()
+    rec("add_residual_bwd config3", timed(lambda: KB.add_residual_backward(dhn, bo, post)), 6 * D * e * T)
+    rec("stream_mix_bwd config3", timed(lambda: KB.stream_mix_backward(bi, dhn, H, pre, res)), 13 * D * e * T)
+    rec("mean_pool config3", timed(lambda: K.mean_pool(H)), 4 * D * e * T)
+    rec("stream_expand config3", timed(lambda: K.stream_expand(bo)), 5 * D * e * T)
+    rec("stream_collapse config3", timed(lambda: K.stream_collapse(H, 0.25)), 5 * D * e * T)
+    del hr, dhn, bi
+    # fused dynamic weights: R = B rows (the module's use) and R = tokens rows (bf16, MFMA path)
+    phi = torch.randn((4 * D, 24), generator=g, device=dev) * 0.02
+    bias = torch.randn(24, generator=g, device=dev)
+    al = [torch.tensor([0.1], device=dev) for _ in range(3)]
+    x4 = torch.randn((4, 4 * D), generator=g, device=dev)
+    rec("dynamic_weights_fwd R=4 K=16384 f32", timed(lambda: K.fused_dynamic_weights_forward(x4, phi, bias, *al)),
+        4 * 4 * D * 4)
+    xt = torch.randn((T, 4 * D), generator=g, device=dev).bfloat16()
+    rec("dynamic_weights_fwd R=16384 K=16384 bf16",
+        timed(lambda: K.fused_dynamic_weights_forward(xt, phi, bias, *al), 5), T * 4 * D * e)
+    xl = xt.clone().requires_grad_(True)
+    phl = phi.clone().requires_grad_(True)
+    gs = [torch.randn((T, 4), generator=g, device=dev), torch.randn((T, 4), generator=g, device=dev),
+          torch.randn((T, 4, 4), generator=g, device=dev)]
+
+    def fwd_bwd():
+        o = mhc.fused_dynamic_weights(xl, phl, bias, *al)
+        torch.autograd.grad(o, [xl, phl], gs)
+
+    # x read by the forward, x read and grad_x written by the backward
+    rec("dynamic_weights_fwd+bwd R=16384 K=16384 bf16", timed(fwd_bwd, 5), 3 * T * 4 * D * e)
+    return out
 
 
 def _build_inputs(cfg, dev):
@@ -258,6 +343,10 @@ def main() -> int:
     from mhc import _lib
 
     _lib.load()  # fails loudly when the HIP library is not built
+    if args.ops:
+        print(json.dumps({"ops": _ops_leg(), "unit": "us per call", "peak_GBps": HBM_PEAK_GBS,
+                          "device": torch.cuda.get_device_name(0)}), flush=True)
+        return 0
 
     cfg = WORKLOADS[args.workload]
     B, S, D = cfg["B"], cfg["S"], cfg["D"]

@@ -259,6 +259,26 @@ int mhc_layer_static_backward(const void* H, int dtype, const void* d_branch_inp
                               float* grad_bias, int64_t B, int64_t S, int64_t D, int iters,
                               void* workspace, size_t workspace_bytes, mhc_stream_t stream);
 
+/* ------------------------------------------------------------------------
+ * The two ends of a hyper-connection stack.  No counterpart in the
+ * reference, which takes the hyper-hidden state (batch, seq, 4, dim) as
+ * given (README.md:38-39) and leaves building it from the embeddings, and
+ * reducing it at the model output, to the caller.  Each is the other's
+ * backward with the same scale (they are adjoint), so two entry points
+ * cover both passes.
+ * Accumulation is f32; x, y and H may have different dtypes.
+ * ------------------------------------------------------------------------ */
+
+/* H[b,s,n,:] = scale * x[b,s,:] for n = 0..3.  x [B,S,D] (dtype_x),
+ * H [B,S,4,D] (dtype_h).  Backward of stream_collapse. */
+int mhc_stream_expand(const void* x, int dtype_x, void* H, int dtype_h, int64_t B, int64_t S,
+                      int64_t D, float scale, mhc_stream_t stream);
+
+/* y[b,s,:] = scale * sum_n H[b,s,n,:] (scale 1 = sum, 1/4 = mean).  H [B,S,4,D]
+ * (dtype_h), y [B,S,D] (dtype_y).  Backward of stream_expand. */
+int mhc_stream_collapse(const void* H, int dtype_h, void* y, int dtype_y, int64_t B, int64_t S,
+                        int64_t D, float scale, mhc_stream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

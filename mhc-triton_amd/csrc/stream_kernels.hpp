@@ -363,6 +363,62 @@ __global__ __launch_bounds__(kThreads) void mix_bwd_kernel(const T* __restrict__
   }
 }
 
+// ---------------------------------------------------------------------------
+// The two ends of a hyper-connection stack (no counterpart in the reference,
+// whose callers build them from torch ops):
+//   expand:   H[s,n,:] = scale * x[s,:]           n = 0..3   (model input)
+//   collapse: y[s,:]   = scale * sum_n H[s,n,:]              (model output)
+// Each is the other's adjoint with the same scale, so the pair also serves as
+// each other's backward.  An item is W consecutive elements of one token row;
+// W is the wider 16-byte vector of the two dtypes (or 1 on the ragged path).
+// ---------------------------------------------------------------------------
+template <typename TX, typename TH, int W, int NT = 0>
+__global__ __launch_bounds__(kThreads) void expand_kernel(const TX* __restrict__ x, TH* __restrict__ H,
+                                                          float scale, Geom g) {
+  const int64_t b = g.b0 + blockIdx.y;
+  const int64_t D = g.D;
+  for (uint32_t tile = blockIdx.x; tile < g.ntiles; tile += gridDim.x) {
+    const uint32_t i = tile * kThreads + threadIdx.x;
+    if (i >= g.items) continue;
+    const uint32_t s = i / g.nch;
+    const int64_t cw = (int64_t)(i - s * g.nch) * W;
+    float v[W];
+    ld<TX, W, (NT & 1) != 0>(x + b * g.S * D + (int64_t)s * D + cw, v);
+#pragma unroll
+    for (int e = 0; e < W; ++e) v[e] *= scale;
+    TH* out = H + b * g.S * 4 * D + (int64_t)s * 4 * D + cw;
+#pragma unroll
+    for (int n = 0; n < 4; ++n) st<TH, W, (NT & 2) != 0>(out + n * D, v);
+  }
+}
+
+template <typename TH, typename TY, int W, int NT = 0>
+__global__ __launch_bounds__(kThreads) void collapse_kernel(const TH* __restrict__ H, TY* __restrict__ y,
+                                                            float scale, Geom g) {
+  const int64_t b = g.b0 + blockIdx.y;
+  const int64_t D = g.D;
+  for (uint32_t tile = blockIdx.x; tile < g.ntiles; tile += gridDim.x) {
+    const uint32_t i = tile * kThreads + threadIdx.x;
+    const bool ok = i < g.items;
+    const uint32_t s = ok ? i / g.nch : 0;
+    const int64_t cw = ok ? (int64_t)(i - s * g.nch) * W : 0;
+    const int64_t hoff = b * g.S * 4 * D + (int64_t)s * 4 * D + cw;
+    Frag<TH, W> hf[4];
+    if (ok) {
+#pragma unroll
+      for (int n = 0; n < 4; ++n) hf[n].template load<(NT & 1) != 0>(H + hoff + n * D);
+    }
+    loads_issued();
+    if (!ok) continue;
+    float h[4][W], r[W];
+#pragma unroll
+    for (int n = 0; n < 4; ++n) hf[n].unpack(h[n]);
+#pragma unroll
+    for (int e = 0; e < W; ++e) r[e] = (((h[0][e] + h[1][e]) + h[2][e]) + h[3][e]) * scale;
+    st<TY, W, (NT & 2) != 0>(y + b * g.S * D + (int64_t)s * D + cw, r);
+  }
+}
+
 // Final reduction of [B][nblk][NV] partials into up to two outputs:
 // out0[b*SPLIT + k] for k < SPLIT, out1[b*(NV-SPLIT) + k-SPLIT] otherwise.
 template <int NV, int SPLIT>

@@ -207,3 +207,59 @@ extern "C" int mhc_add_residual_backward(const void* dH_new, int dtype_h, const 
   return add_residual_backward_any(dH_new, dtype_h, branch_output, dtype_bo, WRow{H_post, 4}, d_branch_output,
                                    dH_post, B, S, D, (float*)workspace, (hipStream_t)stream);
 }
+
+namespace mhc {
+
+template <typename TX, typename TH, int W>
+static int expand_launch(const TX* x, TH* H, float scale, int64_t B, int64_t S, int64_t D, hipStream_t st) {
+  return for_batch_chunks(B, [&](int64_t b0, int64_t nb) {
+    const Geom g = make_geom<W, 1>(S, D, b0);
+    expand_kernel<TX, TH, W, kNtStores><<<dim3(g.ntiles, nb), kThreads, occupancy_lds(2), st>>>(x, H, scale, g);
+    return hip_status(hipGetLastError(), "stream_expand launch");
+  });
+}
+
+template <typename TH, typename TY, int W>
+static int collapse_launch(const TH* H, TY* y, float scale, int64_t B, int64_t S, int64_t D, hipStream_t st) {
+  return for_batch_chunks(B, [&](int64_t b0, int64_t nb) {
+    const Geom g = make_geom<W, 1>(S, D, b0);
+    collapse_kernel<TH, TY, W, kNtStores><<<dim3(g.ntiles, nb), kThreads, occupancy_lds(3), st>>>(H, y, scale, g);
+    return hip_status(hipGetLastError(), "stream_collapse launch");
+  });
+}
+
+}  // namespace mhc
+
+extern "C" int mhc_stream_expand(const void* x, int dtype_x, void* H, int dtype_h, int64_t B, int64_t S, int64_t D,
+                                 float scale, mhc_stream_t stream) {
+  if (int rc = check_bsd("stream_expand", B, S, D)) return rc;
+  if (B * S * D == 0) return MHC_OK;
+  if (!x || !H) {
+    set_error("stream_expand: null pointer");
+    return MHC_ERR_ARG;
+  }
+  hipStream_t st = (hipStream_t)stream;
+  // TH: the stream tensor's dtype, TB: x's dtype.
+  return MHC_DISPATCH_DTYPE2(dtype_h, dtype_x, [&] {
+    constexpr int WV = wide_w<TH, TB>();
+    if (vec_ok(D, WV, {x, H})) return expand_launch<TB, TH, WV>((const TB*)x, (TH*)H, scale, B, S, D, st);
+    return expand_launch<TB, TH, 1>((const TB*)x, (TH*)H, scale, B, S, D, st);
+  });
+}
+
+extern "C" int mhc_stream_collapse(const void* H, int dtype_h, void* y, int dtype_y, int64_t B, int64_t S,
+                                   int64_t D, float scale, mhc_stream_t stream) {
+  if (int rc = check_bsd("stream_collapse", B, S, D)) return rc;
+  if (B * S * D == 0) return MHC_OK;
+  if (!H || !y) {
+    set_error("stream_collapse: null pointer");
+    return MHC_ERR_ARG;
+  }
+  hipStream_t st = (hipStream_t)stream;
+  // TH: the stream tensor's dtype, TB: y's dtype.
+  return MHC_DISPATCH_DTYPE2(dtype_h, dtype_y, [&] {
+    constexpr int WV = wide_w<TH, TB>();
+    if (vec_ok(D, WV, {H, y})) return collapse_launch<TH, TB, WV>((const TH*)H, (TB*)y, scale, B, S, D, st);
+    return collapse_launch<TH, TB, 1>((const TH*)H, (TB*)y, scale, B, S, D, st);
+  });
+}

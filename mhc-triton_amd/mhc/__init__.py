@@ -7,6 +7,7 @@ every op running on hand-written HIP kernels behind the C ABI of
 PyTorch and run anywhere.
 """
 
+from . import streams  # stream expand / collapse (not in __all__, which is the reference's)
 from .module import HyperConnection
 from .ops import (
     sinkhorn_knopp,

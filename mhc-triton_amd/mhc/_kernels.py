@@ -164,3 +164,36 @@ def mean_pool(H: torch.Tensor) -> torch.Tensor:
         _lib.check(lib.mhc_mean_pool(H.data_ptr(), code, x.data_ptr(), B, S, D, _lib.ptr(ws),
                                      0 if ws is None else ws.numel(), _lib.stream(dev)), "mean_pool")
     return x
+
+
+def stream_expand(x: torch.Tensor, scale: float = 1.0, dtype: torch.dtype = None) -> torch.Tensor:
+    """H[b,s,n,:] = scale * x[b,s,:] for the 4 streams, H in ``dtype`` (default x's).
+    The backward of ``stream_collapse``.  No reference launcher: the reference
+    takes the (batch, seq, 4, dim) state as given (README.md:38-39)."""
+    if x.dim() != 3:
+        raise ShapeError(f"x must be (batch, seq, dim), got {tuple(x.shape)}")
+    B, S, D = x.shape
+    dev = _lib.require_gpu(x)
+    x = x.contiguous()
+    H = torch.empty(B, S, 4, D, device=dev, dtype=dtype or x.dtype)
+    lib = _lib.load()
+    with _lib.on_device(dev):
+        _lib.check(lib.mhc_stream_expand(x.data_ptr(), _lib.dtype_code(x), H.data_ptr(), _lib.dtype_code(H),
+                                         B, S, D, float(scale), _lib.stream(dev)), "stream_expand")
+    return H
+
+
+def stream_collapse(H: torch.Tensor, scale: float = 1.0, dtype: torch.dtype = None) -> torch.Tensor:
+    """y[b,s,:] = scale * sum_n H[b,s,n,:], y in ``dtype`` (default H's); scale 1/4
+    is the stream mean.  The backward of ``stream_expand``."""
+    if H.dim() != 4 or H.shape[2] != 4:
+        raise ShapeError(f"H must be (batch, seq, 4, dim), got {tuple(H.shape)}")
+    B, S, _, D = H.shape
+    dev = _lib.require_gpu(H)
+    H = H.contiguous()
+    y = torch.empty(B, S, D, device=dev, dtype=dtype or H.dtype)
+    lib = _lib.load()
+    with _lib.on_device(dev):
+        _lib.check(lib.mhc_stream_collapse(H.data_ptr(), _lib.dtype_code(H), y.data_ptr(), _lib.dtype_code(y),
+                                           B, S, D, float(scale), _lib.stream(dev)), "stream_collapse")
+    return y

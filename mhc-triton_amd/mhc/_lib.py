@@ -45,6 +45,8 @@ _SIGNATURES = {
     "mhc_dynamic_weights_backward": (
         _I, [_P, _I, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _I64, _I64, _I, _F, _P, _SZ, _P]),
     "mhc_layer_workspace_bytes": (_SZ, [_I64, _I64, _I64, _I]),
+    "mhc_stream_expand": (_I, [_P, _I, _P, _I, _I64, _I64, _I64, _F, _P]),
+    "mhc_stream_collapse": (_I, [_P, _I, _P, _I, _I64, _I64, _I64, _F, _P]),
     "mhc_mean_pool_workspace_bytes": (_SZ, [_I64, _I64, _I64, _I]),
     "mhc_mean_pool": (_I, [_P, _I, _P, _I64, _I64, _I64, _P, _SZ, _P]),
     "mhc_layer_dynamic_forward": (

@@ -447,3 +447,47 @@ class LayerAdd(torch.autograd.Function):
         dH_new = dH_new.to(ctx.h_dtype)
         d_bo, dH_post = torch.ops.mhc.layer_add_backward(dH_new, bo, w)
         return dH_new, d_bo, F.pad(dH_post, (4, 16))
+
+
+# --------------------------------------------------------------------------
+# Stream expand / collapse (mhc.streams; no reference counterpart)
+# --------------------------------------------------------------------------
+
+@_op("stream_expand")
+def stream_expand(x: Tensor, scale: float, dtype: Optional[torch.dtype] = None) -> Tensor:
+    return _k.stream_expand(x, scale, dtype)
+
+
+@stream_expand.register_fake
+def _(x, scale, dtype=None):
+    B, S, D = x.shape
+    return x.new_empty(B, S, 4, D, dtype=dtype or x.dtype)
+
+
+@_op("stream_collapse")
+def stream_collapse(H: Tensor, scale: float, dtype: Optional[torch.dtype] = None) -> Tensor:
+    return _k.stream_collapse(H, scale, dtype)
+
+
+@stream_collapse.register_fake
+def _(H, scale, dtype=None):
+    B, S, _, D = H.shape
+    return H.new_empty(B, S, D, dtype=dtype or H.dtype)
+
+
+def _ends_setup(ctx, inputs, output):
+    t, scale, _ = inputs
+    ctx.scale = scale
+    ctx.in_dtype = t.dtype
+
+
+def _expand_bwd(ctx, dH):
+    return torch.ops.mhc.stream_collapse(dH, ctx.scale, ctx.in_dtype), None, None
+
+
+def _collapse_bwd(ctx, dy):
+    return torch.ops.mhc.stream_expand(dy, ctx.scale, ctx.in_dtype), None, None
+
+
+torch.library.register_autograd("mhc::stream_expand", _expand_bwd, setup_context=_ends_setup)
+torch.library.register_autograd("mhc::stream_collapse", _collapse_bwd, setup_context=_ends_setup)

@@ -174,6 +174,31 @@ def add_residual_backward(dH_new, bo, H_post, dt=F64):
 
 
 # ---------------------------------------------------------------------------
+# Stream expand / collapse at the ends of a stack.  No reference function: the
+# reference takes the (batch, seq, 4, dim) hyper-hidden state as given
+# (README.md:38-39).  The two are adjoint, so each backward is the other.
+# ---------------------------------------------------------------------------
+
+def stream_expand(x, scale=1.0, n=4, dt=F64):
+    """H[b,s,k,:] = scale * x[b,s,:] for k < n."""
+    x = _a(x, dt)
+    return np.repeat((dt(scale) * x)[:, :, None, :], n, axis=2)
+
+
+def stream_collapse(H, scale=1.0, dt=F64):
+    """y[b,s,:] = scale * sum_k H[b,s,k,:]."""
+    return dt(scale) * _a(H, dt).sum(axis=2)
+
+
+def stream_expand_backward(dH, scale=1.0, dt=F64):
+    return stream_collapse(dH, scale, dt)
+
+
+def stream_collapse_backward(dy, scale=1.0, n=4, dt=F64):
+    return stream_expand(dy, scale, n, dt)
+
+
+# ---------------------------------------------------------------------------
 # Mean-pool (module.py:123) and static / unfused weights (module.py:108-117,141-163)
 # ---------------------------------------------------------------------------
 

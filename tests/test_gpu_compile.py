@@ -133,6 +133,41 @@ def test_compiled_public_ops_match_eager_bitwise():
     _assert_identical(run(fn), run(_compile(fn)))
 
 
+def test_compiled_model_ends_match_eager_bitwise():
+    """expand -> two HyperConnection layers -> collapse, compiled as one graph."""
+    from mhc.streams import collapse_streams, expand_streams
+
+    g = torch.Generator().manual_seed(4)
+    B, S, D = 2, 48, 128
+    hcs = [mhc.HyperConnection(D, layer_idx=i).to(DEV) for i in range(2)]
+    with torch.no_grad():
+        for hc in hcs:
+            hc.phi.copy_((torch.randn(hc.phi.shape, generator=g) * 0.02).to(DEV))
+    x = torch.randn((B, S, D), generator=g).bfloat16().to(DEV)
+    W = (torch.randn((D, D), generator=g) / D ** 0.5).to(DEV)
+    gy = torch.randn((B, S, D), generator=g).bfloat16().to(DEV)
+
+    def model(xl, Wl):
+        H = expand_streams(xl)
+        for hc in hcs:
+            bi, add = hc(H)
+            H = add(torch.tanh(bi.float() @ Wl).to(bi.dtype))
+        return collapse_streams(H)
+
+    def run(f):
+        for hc in hcs:
+            hc.zero_grad(set_to_none=True)
+        xl, Wl = x.clone().requires_grad_(True), W.clone().requires_grad_(True)
+        y = f(xl, Wl)
+        y.backward(gy)
+        out = {"y": y.detach(), "x": xl.grad, "W": Wl.grad}
+        for i, hc in enumerate(hcs):
+            out.update({f"{i}.{n}": p.grad for n, p in hc.named_parameters()})
+        return out
+
+    _assert_identical(run(model), run(_compile(model)))
+
+
 _CASES = []
 
 
@@ -175,11 +210,13 @@ def _opcheck_cases():
         ("layer_mix_backward", (H, bi, H, wL)),
         ("layer_add_forward", (H, bo, wL)),
         ("layer_add_backward", (H, bo, wL)),
+        ("stream_expand", (rg(bo.float()), 0.5, torch.bfloat16)),
+        ("stream_collapse", (rg(H.float()), 0.25, None)),
     ])
     return _CASES
 
 
-N_CASES = 18
+N_CASES = 20
 
 
 def test_opcheck_covers_every_registered_op():

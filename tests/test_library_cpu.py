@@ -19,7 +19,7 @@ OPS = {
     "add_residual_forward", "add_residual_backward", "dynamic_weights_forward", "dynamic_weights_backward",
     "mean_pool", "layer_dynamic_forward", "layer_dynamic_backward", "layer_static_forward",
     "layer_static_backward", "layer_branch_input", "layer_mix_backward", "layer_add_forward",
-    "layer_add_backward",
+    "layer_add_backward", "stream_expand", "stream_collapse",
 }
 BF = torch.bfloat16
 F32 = torch.float32
@@ -76,6 +76,10 @@ def test_fake_kernels_give_the_launchers_output_shapes_and_dtypes():
         assert sig([ops.layer_add_forward(H, bo, e(B, 24))]) == [((B, S, 4, D), BF, "cuda")]
         assert sig(ops.layer_add_backward(H, bo, e(B, 24))) == [((B, S, D), torch.float16, "cuda"),
                                                                 ((B, 4), F32, "cuda")]
+        assert sig([ops.stream_expand(bo, 1.0)]) == [((B, S, 4, D), torch.float16, "cuda")]
+        assert sig([ops.stream_expand(bo, 1.0, BF)]) == [((B, S, 4, D), BF, "cuda")]
+        assert sig([ops.stream_collapse(H, 0.25)]) == [((B, S, D), BF, "cuda")]
+        assert sig([ops.stream_collapse(H, 0.25, F32)]) == [((B, S, D), F32, "cuda")]
 
 
 @pytest.mark.parametrize("dynamic,fused", [(True, True), (False, True), (True, False)])
@@ -114,6 +118,6 @@ def test_public_ops_trace_to_registered_ops():
         assert "torch.compiler.is_compiling()" in src and "torch.ops.mhc." in src, fn.__name__
     assert "self._forward_traced(H)" in inspect.getsource(module.HyperConnection.forward)
     for op in ("sinkhorn_forward", "stream_mix_forward", "add_residual_forward", "dynamic_weights_forward",
-               "mean_pool"):
+               "mean_pool", "stream_expand", "stream_collapse"):
         assert torch._C._dispatch_has_kernel_for_dispatch_key(f"mhc::{op}", "Autograd"), op
     assert _library.LayerAdd is not None

@@ -262,6 +262,28 @@ def test_add_residual_identity_and_backward_adjoint():
     assert abs((dHn * O.add_residual(np.zeros_like(H), bo, Y)).sum() - (dpost * Y).sum()) < 1e-10
 
 
+def test_stream_expand_collapse_closed_forms_adjoint_and_autograd():
+    B, S, D = 2, 5, 7
+    x = RNG.standard_normal((B, S, D))
+    Y = RNG.standard_normal((B, S, 4, D))
+    for scale in (1.0, 0.25, -1.5):
+        H = O.stream_expand(x, scale)
+        assert H.shape == (B, S, 4, D)
+        for k in range(4):
+            assert np.array_equal(H[:, :, k, :], scale * x)
+        assert np.allclose(O.stream_collapse(H, scale), 4 * scale * scale * x, rtol=1e-14, atol=0)
+        # adjoint pair: <expand(x), Y> = <x, collapse(Y)>
+        assert abs((O.stream_expand(x, scale) * Y).sum() - (x * O.stream_collapse(Y, scale)).sum()) < 1e-10
+        # torch autograd of independent torch expressions
+        xt = torch.tensor(x, requires_grad=True)
+        Ht = torch.tensor(Y, requires_grad=True)
+        (xt.unsqueeze(2).expand(B, S, 4, D) * scale * torch.tensor(Y)).sum().backward()
+        (torch.einsum("bsnd->bsd", Ht) * scale * torch.tensor(x)).sum().backward()
+        assert np.allclose(O.stream_expand_backward(Y, scale), xt.grad.numpy(), rtol=1e-13, atol=1e-13)
+        assert np.allclose(O.stream_collapse_backward(x, scale), Ht.grad.numpy(), rtol=1e-13, atol=1e-13)
+    assert np.allclose(O.stream_collapse(Y, 0.25), Y.mean(axis=2), rtol=1e-13, atol=1e-15)
+
+
 # --------------------------------------------------------------------------- whole layer
 
 def _layer_params(dynamic, fused, D, rng, zero_phi=False):
