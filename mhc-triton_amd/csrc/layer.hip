@@ -148,11 +148,11 @@ __global__ __launch_bounds__(kThreads) void static_weights_bwd_kernel(
   else if (e < 8) gbias[4 + j] = tot[4 + j] * sg * (1.f - sg);
 }
 
-// Pass B (REDUCE only), pass C (WRITE_DH + HAS_GX) and the static pass BC
-// (REDUCE + WRITE_DH) share mix_bwd_kernel.
-template <typename T, int W, bool HAS_DHN, bool REDUCE, bool WRITE_DH, bool HAS_GX>
-static int launch_mix_bwd(const T* dbi, const T* dhn, const T* H, const float* gx, const float* w, T* dH,
-                          float* part, int64_t B, int64_t S, int64_t D, uint32_t* nblk_out, hipStream_t st) {
+// Pass B (REDUCE only), the static pass BC (REDUCE + WRITE_DH) and the
+// generic mix backward share mix_bwd_kernel.
+template <typename T, int W, bool HAS_DHN, bool REDUCE, bool WRITE_DH>
+static int launch_mix_bwd(const T* dbi, const T* dhn, const T* H, const float* w, T* dH, float* part, int64_t B,
+                          int64_t S, int64_t D, uint32_t* nblk_out, hipStream_t st) {
   // Pass B writes nothing bulk: two items per lane and full occupancy.  The
   // passes that write dH take one item per lane and capped occupancy.
   constexpr int U = WRITE_DH ? kLU : kLRU;
@@ -161,33 +161,63 @@ static int launch_mix_bwd(const T* dbi, const T* dhn, const T* H, const float* g
   const uint32_t nblk = REDUCE ? reduce_blocks(g0.ntiles, B) : g0.ntiles;
   if (nblk_out) *nblk_out = nblk;
   if (nblk == 0) return MHC_OK;
-  const float inv_S = S > 0 ? 1.f / (float)S : 0.f;
   return for_batch_chunks(B, [&](int64_t b0, int64_t nb) {
     const Geom g = make_geom<W, U>(S, D, b0);
-    mix_bwd_kernel<T, W, U, HAS_DHN, REDUCE, WRITE_DH, HAS_GX, kNtStores><<<dim3(nblk, nb), kThreads, lds, st>>>(
-        dbi, dhn, H, gx, inv_S, WRow{w, kOut}, WRow{w + 8, kOut}, dH, part, g);
+    mix_bwd_kernel<T, W, U, HAS_DHN, REDUCE, WRITE_DH, kNtStores><<<dim3(nblk, nb), kThreads, lds, st>>>(
+        dbi, dhn, H, WRow{w, kOut}, WRow{w + 8, kOut}, dH, part, g);
     return hip_status(hipGetLastError(), "layer mix backward launch");
   });
 }
 
-template <typename T, bool REDUCE, bool WRITE_DH, bool HAS_GX>
-static int mix_bwd_dispatch(const void* dbi, const void* dhn, const void* H, const float* gx, const float* w,
-                            void* dH, float* part, int64_t B, int64_t S, int64_t D, uint32_t* nblk,
-                            hipStream_t st) {
+template <typename T, bool REDUCE, bool WRITE_DH>
+static int mix_bwd_dispatch(const void* dbi, const void* dhn, const void* H, const float* w, void* dH, float* part,
+                            int64_t B, int64_t S, int64_t D, uint32_t* nblk, hipStream_t st) {
   constexpr int WV = Vec<T>::N;
-  const bool vec = vec_ok(D, WV, {dbi, dhn, H, dH}) && (!HAS_GX || aligned16(gx));
+  const bool vec = vec_ok(D, WV, {dbi, dhn, H, dH});
   if (dhn) {
     if (vec)
-      return launch_mix_bwd<T, WV, true, REDUCE, WRITE_DH, HAS_GX>((const T*)dbi, (const T*)dhn, (const T*)H, gx, w,
-                                                                   (T*)dH, part, B, S, D, nblk, st);
-    return launch_mix_bwd<T, 1, true, REDUCE, WRITE_DH, HAS_GX>((const T*)dbi, (const T*)dhn, (const T*)H, gx, w,
-                                                                (T*)dH, part, B, S, D, nblk, st);
+      return launch_mix_bwd<T, WV, true, REDUCE, WRITE_DH>((const T*)dbi, (const T*)dhn, (const T*)H, w, (T*)dH,
+                                                           part, B, S, D, nblk, st);
+    return launch_mix_bwd<T, 1, true, REDUCE, WRITE_DH>((const T*)dbi, (const T*)dhn, (const T*)H, w, (T*)dH, part,
+                                                        B, S, D, nblk, st);
   }
   if (vec)
-    return launch_mix_bwd<T, WV, false, REDUCE, WRITE_DH, HAS_GX>((const T*)dbi, nullptr, (const T*)H, gx, w, (T*)dH,
-                                                                  part, B, S, D, nblk, st);
-  return launch_mix_bwd<T, 1, false, REDUCE, WRITE_DH, HAS_GX>((const T*)dbi, nullptr, (const T*)H, gx, w, (T*)dH,
-                                                               part, B, S, D, nblk, st);
+    return launch_mix_bwd<T, WV, false, REDUCE, WRITE_DH>((const T*)dbi, nullptr, (const T*)H, w, (T*)dH, part, B,
+                                                          S, D, nblk, st);
+  return launch_mix_bwd<T, 1, false, REDUCE, WRITE_DH>((const T*)dbi, nullptr, (const T*)H, w, (T*)dH, part, B, S,
+                                                       D, nblk, st);
+}
+
+// Pass C of the dynamic backward: two tokens per workgroup (grad_x loaded
+// once for both), 2 workgroups per CU; both measured best at config-3 size.
+constexpr int kDhTokens = 2;
+
+template <typename T, int W, bool HAS_DHN>
+static int launch_dh(const T* dbi, const T* dhn, const float* gx, const float* w, T* dH, int64_t B, int64_t S,
+                     int64_t D, hipStream_t st) {
+  const uint32_t ncb = (uint32_t)((D / W + kThreads - 1) / kThreads);
+  const int64_t groups = (S + kDhTokens - 1) / kDhTokens;
+  if (ncb == 0 || groups == 0) return MHC_OK;
+  const float inv_S = 1.f / (float)S;
+  return for_batch_chunks(B, [&](int64_t b0, int64_t nb) {
+    dh_kernel<T, W, kDhTokens, HAS_DHN, kNtStores>
+        <<<dim3((unsigned)(groups * ncb), (unsigned)nb), kThreads, occupancy_lds(2), st>>>(
+            dbi, dhn, gx, inv_S, WRow{w, kOut}, WRow{w + 8, kOut}, dH, S, D, ncb, b0);
+    return hip_status(hipGetLastError(), "layer dH launch");
+  });
+}
+
+template <typename T>
+static int dh_dispatch(const void* dbi, const void* dhn, const float* gx, const float* w, void* dH, int64_t B,
+                       int64_t S, int64_t D, hipStream_t st) {
+  constexpr int WV = Vec<T>::N;
+  const bool vec = vec_ok(D, WV, {dbi, dhn, dH}) && aligned16(gx);
+  if (dhn) {
+    if (vec) return launch_dh<T, WV, true>((const T*)dbi, (const T*)dhn, gx, w, (T*)dH, B, S, D, st);
+    return launch_dh<T, 1, true>((const T*)dbi, (const T*)dhn, gx, w, (T*)dH, B, S, D, st);
+  }
+  if (vec) return launch_dh<T, WV, false>((const T*)dbi, nullptr, gx, w, (T*)dH, B, S, D, st);
+  return launch_dh<T, 1, false>((const T*)dbi, nullptr, gx, w, (T*)dH, B, S, D, st);
 }
 
 }  // namespace mhc
@@ -314,7 +344,7 @@ extern "C" int mhc_layer_dynamic_backward(const void* H, int dtype, const void* 
   // Pass B: dH_pre, dH_res.
   uint32_t nblk = 0;
   int rc = MHC_DISPATCH_DTYPE(dtype, [&] {
-    return mix_bwd_dispatch<T, true, false, false>(d_branch_input, dH_new, H, nullptr, w, nullptr, part, B, S, D,
+    return mix_bwd_dispatch<T, true, false>(d_branch_input, dH_new, H, w, nullptr, part, B, S, D,
                                                    &nblk, st);
   });
   if (rc) return rc;
@@ -332,10 +362,7 @@ extern "C" int mhc_layer_dynamic_backward(const void* H, int dtype, const void* 
   if ((rc = hip_status(hipGetLastError(), "layer weights backward wide launch"))) return rc;
   if (!dH || S * D == 0) return MHC_OK;
   // Pass C: dH.
-  return MHC_DISPATCH_DTYPE(dtype, [&] {
-    return mix_bwd_dispatch<T, false, true, true>(d_branch_input, dH_new, nullptr, gx, w, dH, nullptr, B, S, D,
-                                                  nullptr, st);
-  });
+  return MHC_DISPATCH_DTYPE(dtype, [&] { return dh_dispatch<T>(d_branch_input, dH_new, gx, w, dH, B, S, D, st); });
 }
 
 extern "C" int mhc_layer_static_backward(const void* H, int dtype, const void* d_branch_input, const void* dH_new,
@@ -359,9 +386,9 @@ extern "C" int mhc_layer_static_backward(const void* H, int dtype, const void* d
   uint32_t nblk = 0;
   int rc = MHC_DISPATCH_DTYPE(dtype, [&] {
     if (dH)
-      return mix_bwd_dispatch<T, true, true, false>(d_branch_input, dH_new, H, nullptr, w, dH, part, B, S, D, &nblk,
+      return mix_bwd_dispatch<T, true, true>(d_branch_input, dH_new, H, w, dH, part, B, S, D, &nblk,
                                                     st);
-    return mix_bwd_dispatch<T, true, false, false>(d_branch_input, dH_new, H, nullptr, w, nullptr, part, B, S, D,
+    return mix_bwd_dispatch<T, true, false>(d_branch_input, dH_new, H, w, nullptr, part, B, S, D,
                                                    &nblk, st);
   });
   if (rc) return rc;
@@ -399,9 +426,9 @@ extern "C" int mhc_layer_mix_backward(const void* H, int dtype, const void* d_br
   uint32_t nblk = 0;
   int rc = MHC_DISPATCH_DTYPE(dtype, [&] {
     if (dH)
-      return mix_bwd_dispatch<T, true, true, false>(d_branch_input, dH_new, H, nullptr, w, dH, part, B, S, D, &nblk,
+      return mix_bwd_dispatch<T, true, true>(d_branch_input, dH_new, H, w, dH, part, B, S, D, &nblk,
                                                     st);
-    return mix_bwd_dispatch<T, true, false, false>(d_branch_input, dH_new, H, nullptr, w, nullptr, part, B, S, D,
+    return mix_bwd_dispatch<T, true, false>(d_branch_input, dH_new, H, w, nullptr, part, B, S, D,
                                                    &nblk, st);
   });
   if (rc) return rc;

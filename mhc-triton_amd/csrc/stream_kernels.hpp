@@ -264,13 +264,12 @@ __global__ __launch_bounds__(kThreads) void add_residual_bwd_kernel(const T* __r
 //   REDUCE:   part[0:4]  = sum dbi * H[s,n,:]          -> dH_pre
 //             part[4:20] = sum dhn[s,n,:] * H[s,m,:]   -> dH_res (n-major)
 // HAS_DHN = false treats dhn as zero (H_new / H_residual got no gradient).
-// HAS_GX adds the mean-pool backward term grad_x[b, m*D + d] / S.
+// (The dynamic layer's dH, which also adds grad_x / S, is dh_kernel.)
 // ---------------------------------------------------------------------------
-template <typename T, int W, int U, bool HAS_DHN, bool REDUCE, bool WRITE_DH, bool HAS_GX, int NT = 0>
+template <typename T, int W, int U, bool HAS_DHN, bool REDUCE, bool WRITE_DH, int NT = 0>
 __global__ __launch_bounds__(kThreads) void mix_bwd_kernel(const T* __restrict__ dbi, const T* __restrict__ dhn,
-                                                           const T* __restrict__ H, const float* __restrict__ gx,
-                                                           float inv_S, WRow pre, WRow res, T* __restrict__ dH,
-                                                           float* __restrict__ part, Geom g) {
+                                                           const T* __restrict__ H, WRow pre, WRow res,
+                                                           T* __restrict__ dH, float* __restrict__ part, Geom g) {
   __shared__ float lds[4 * 20];
   const int64_t b = g.b0 + blockIdx.y;
   float wp[4], wr[16];
@@ -286,7 +285,6 @@ __global__ __launch_bounds__(kThreads) void mix_bwd_kernel(const T* __restrict__
     float db[U][W];
     float dn[U][4][W];
     float h[U][4][W];
-    float gv[U][4][W];
     int64_t off[U];  // offset of (s, n=0, c*W) in the [S,4,D] plane
     int64_t cw[U];
     int64_t s_[U];
@@ -309,10 +307,6 @@ __global__ __launch_bounds__(kThreads) void mix_bwd_kernel(const T* __restrict__
         if constexpr (REDUCE) {
 #pragma unroll
           for (int n = 0; n < 4; ++n) ld<T, W, (NT & 1) != 0>(H + off[u] + n * D, h[u][n]);
-        }
-        if constexpr (HAS_GX) {
-#pragma unroll
-          for (int n = 0; n < 4; ++n) ld<float, W>(gx + b * 4 * D + n * D + cw[u], gv[u][n]);
         }
       }
     }
@@ -345,7 +339,6 @@ __global__ __launch_bounds__(kThreads) void mix_bwd_kernel(const T* __restrict__
 #pragma unroll
               for (int n = 0; n < 4; ++n) v = __builtin_fmaf(wr[4 * n + m], dn[u][n][e], v);
             }
-            if constexpr (HAS_GX) v = __builtin_fmaf(gv[u][m][e], inv_S, v);
             r[e] = v;
           }
           st<T, W, (NT & 2) != 0>(dH + off[u] + m * D, r);
@@ -359,6 +352,70 @@ __global__ __launch_bounds__(kThreads) void mix_bwd_kernel(const T* __restrict__
       float* pp = part + (b * gridDim.x + blockIdx.x) * 20;
 #pragma unroll
       for (int k = 0; k < 20; ++k) pp[k] = acc[k];
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// dH of the dynamic layer (pass C):
+//   dH[s,m,:] = pre[m] d_bi[s,:] + sum_n res[n,m] dHn[s,n,:] + grad_x[m,:] / S
+// grad_x (f32, [4][D] per batch) is the same for every token, so a workgroup
+// walks TT consecutive tokens of one 256*W-column block and loads its grad_x
+// slice once: per token a lane then issues 5 loads instead of 13 (at config-3
+// size 212 -> 200 us).  Same arithmetic, in the same order, as the WRITE_DH
+// path of mix_bwd_kernel, so the results are bit-identical.
+// Grid: x = token group * ncb + column block (ncb blocks of 256 items), y =
+// batch within the launch.
+// ---------------------------------------------------------------------------
+template <typename T, int W, int TT, bool HAS_DHN, int NT = 0>
+__global__ __launch_bounds__(kThreads) void dh_kernel(const T* __restrict__ dbi, const T* __restrict__ dhn,
+                                                      const float* __restrict__ gx, float inv_S, WRow pre,
+                                                      WRow res, T* __restrict__ dH, int64_t S, int64_t D,
+                                                      uint32_t ncb, int64_t b0) {
+  const int64_t b = b0 + blockIdx.y;
+  const uint32_t cblk = blockIdx.x % ncb;
+  const int64_t s0 = (int64_t)(blockIdx.x / ncb) * TT;
+  const int64_t c = (int64_t)cblk * kThreads + threadIdx.x;
+  if (c >= D / W) return;
+  const int64_t cw = c * W;
+  float wp[4], wr[16];
+  load_w4(pre, b, wp);
+  if constexpr (HAS_DHN) load_w16(res, b, wr);
+  float gv[4][W];
+#pragma unroll
+  for (int m = 0; m < 4; ++m) ld<float, W>(gx + b * 4 * D + m * D + cw, gv[m]);
+#pragma unroll
+  for (int t = 0; t < TT; ++t) {
+    const int64_t s = s0 + t;
+    if (s >= S) break;
+    const int64_t off = b * S * 4 * D + s * 4 * D + cw;
+    Frag<T, W> bf;
+    Frag<T, W> nf[4];
+    bf.template load<(NT & 1) != 0>(dbi + b * S * D + s * D + cw);
+    if constexpr (HAS_DHN) {
+#pragma unroll
+      for (int n = 0; n < 4; ++n) nf[n].template load<(NT & 1) != 0>(dhn + off + n * D);
+    }
+    loads_issued();
+    float db[W], dn[4][W];
+    bf.unpack(db);
+    if constexpr (HAS_DHN) {
+#pragma unroll
+      for (int n = 0; n < 4; ++n) nf[n].unpack(dn[n]);
+    }
+#pragma unroll
+    for (int m = 0; m < 4; ++m) {
+      float r[W];
+#pragma unroll
+      for (int e = 0; e < W; ++e) {
+        float v = wp[m] * db[e];
+        if constexpr (HAS_DHN) {
+#pragma unroll
+          for (int n = 0; n < 4; ++n) v = __builtin_fmaf(wr[4 * n + m], dn[n][e], v);
+        }
+        r[e] = __builtin_fmaf(gv[m][e], inv_S, v);
+      }
+      st<T, W, (NT & 2) != 0>(dH + off + m * D, r);
     }
   }
 }

@@ -27,8 +27,8 @@ static int stream_mix_bwd(const T* dbi, const T* dhr, const T* H, const float* p
   const uint32_t nblk = reduce_blocks(g0.ntiles, B);
   int rc = for_batch_chunks(B, [&](int64_t b0, int64_t nb) {
     const Geom g = make_geom<W, kU>(S, D, b0);
-    mix_bwd_kernel<T, W, kU, true, true, true, false, kNtStores><<<dim3(nblk, nb), kThreads, occupancy_lds(3), st>>>(
-        dbi, dhr, H, nullptr, 0.f, WRow{pre, 4}, WRow{res, 16}, dH, part, g);
+    mix_bwd_kernel<T, W, kU, true, true, true, kNtStores><<<dim3(nblk, nb), kThreads, occupancy_lds(3), st>>>(
+        dbi, dhr, H, WRow{pre, 4}, WRow{res, 16}, dH, part, g);
     return hip_status(hipGetLastError(), "stream_mix_backward launch");
   });
   if (rc) return rc;
