@@ -231,7 +231,9 @@ static int launch_meanpool(const T* H, float* x, const float* phi, float* projpa
   const bool phi_vec = phi ? aligned16(phi) : false;
   for (int64_t b0 = 0; b0 < B; b0 += kMaxGridY) {
     const int64_t nb = (B - b0) < kMaxGridY ? (B - b0) : kMaxGridY;
-    colsum_kernel<T, W, kPoolUN><<<dim3((unsigned)p.ncc, (unsigned)p.nS, (unsigned)nb), kThreads, 0, st>>>(
+    // Plain loads: in the layer, branch_input reads H next and finds part of it
+    // in the 256 MB memory-side cache.
+    colsum_kernel<T, W, kPoolUN, false><<<dim3((unsigned)p.ncc, (unsigned)p.nS, (unsigned)nb), kThreads, 0, st>>>(
         H, colpart, S, K, p.SC, p.nS, b0);
     if (int rc = hip_status(hipGetLastError(), "mean_pool column-sum launch")) return rc;
     colsum_reduce_kernel<PROJ><<<dim3((unsigned)p.nrc, (unsigned)nb), kThreads, 0, st>>>(
@@ -243,7 +245,7 @@ static int launch_meanpool(const T* H, float* x, const float* phi, float* projpa
 
 static bool pool_vec(int dtype, int64_t K, const void* H) {
   const int W = dtype == MHC_DTYPE_F32 ? 4 : 8;
-  return K % W == 0 && aligned16(H);
+  return K % W == 0 && aligned16(H) && span_ok(kPoolUN * K, 4);
 }
 
 PoolPlan mean_pool_plan(int dtype, int64_t B, int64_t S, int64_t D, const void* H) {

@@ -549,32 +549,39 @@ __global__ __launch_bounds__(kThreads) void dynw_gphi_reduce_kernel(const float*
 //   projection partials of its 256 columns (x . phi[c,:] and x^2), so the
 //   dynamic-weight projection needs no extra pass over x.
 // ---------------------------------------------------------------------------
-template <typename T, int W, int UN>
+// Loads go through a buffer span rebased at each group of UN rows (the host
+// keeps UN rows of K under 2^31 bytes), with the streaming (nt) policy when
+// NT is set.
+template <typename T, int W, int UN, bool NT = true, bool BUF = (W > 1)>
 __global__ __launch_bounds__(kThreads) void colsum_kernel(const T* __restrict__ H, float* __restrict__ colpart,
                                                           int64_t S, int64_t K, int64_t SC, int nS, int64_t b0) {
   const int64_t b = b0 + blockIdx.z;
   const int sc = blockIdx.y;
-  const int64_t col = (int64_t)blockIdx.x * (kThreads * W) + (int64_t)threadIdx.x * W;
+  const int64_t cblk = (int64_t)blockIdx.x * (kThreads * W);
+  const int64_t col = cblk + (int64_t)threadIdx.x * W;
   if (col >= K) return;
   const int64_t sbeg = (int64_t)sc * SC;
   const int64_t send = sbeg + SC < S ? sbeg + SC : S;
   float acc[W];
 #pragma unroll
   for (int e = 0; e < W; ++e) acc[e] = 0.f;
-  const T* p = H + b * S * K + col;
+  const T* base = H + b * S * K + cblk;
+  const uint32_t lane_e = (uint32_t)threadIdx.x * W;
   int64_t s = sbeg;
   for (; s + (UN - 1) < send; s += UN) {
+    const Span<T, BUF> sp(base + s * K, (int64_t)UN * K);
     float v[UN][W];
 #pragma unroll
-    for (int u = 0; u < UN; ++u) ld<T, W>(p + (s + u) * K, v[u]);
+    for (int u = 0; u < UN; ++u) ld<T, W, NT>(sp, (uint32_t)(u * K) + lane_e, v[u]);
 #pragma unroll
     for (int u = 0; u < UN; ++u)
 #pragma unroll
       for (int e = 0; e < W; ++e) acc[e] += v[u][e];
   }
   for (; s < send; ++s) {
+    const Span<T, BUF> sp(base + s * K, K);
     float v[W];
-    ld<T, W>(p + s * K, v);
+    ld<T, W, NT>(sp, lane_e, v);
 #pragma unroll
     for (int e = 0; e < W; ++e) acc[e] += v[e];
   }

@@ -61,7 +61,7 @@ static int launch_bi(const T* H, const float* w, T* bi, int64_t B, int64_t S, in
   return for_batch_chunks(B, [&](int64_t b0, int64_t nb) {
     const Geom g = make_geom<W, kLU>(S, D, b0);
     if (g.ntiles == 0) return (int)MHC_OK;
-    mix_fwd_kernel<T, T, W, kLU, true, false, false, kNtStores><<<dim3(g.ntiles, nb), kThreads, occupancy_lds(3), st>>>(
+    mix_fwd_kernel<T, T, W, kLU, true, false, false, kNt><<<dim3(g.ntiles, nb), kThreads, occupancy_lds(3), st>>>(
         H, (const T*)nullptr, WRow{w, kOut}, WRow{nullptr, 0}, WRow{nullptr, 0}, bi, nullptr, g);
     return hip_status(hipGetLastError(), "layer branch_input launch");
   });
@@ -163,7 +163,9 @@ static int launch_mix_bwd(const T* dbi, const T* dhn, const T* H, const float* w
   if (nblk == 0) return MHC_OK;
   return for_batch_chunks(B, [&](int64_t b0, int64_t nb) {
     const Geom g = make_geom<W, U>(S, D, b0);
-    mix_bwd_kernel<T, W, U, HAS_DHN, REDUCE, WRITE_DH, kNtStores><<<dim3(nblk, nb), kThreads, lds, st>>>(
+    // Pass B (REDUCE only): nt on the H loads alone; d_bi and dH_new are read again by pass C.
+    constexpr int NT = WRITE_DH ? kNt : 4;
+    mix_bwd_kernel<T, W, U, HAS_DHN, REDUCE, WRITE_DH, NT><<<dim3(nblk, nb), kThreads, lds, st>>>(
         dbi, dhn, H, WRow{w, kOut}, WRow{w + 8, kOut}, dH, part, g);
     return hip_status(hipGetLastError(), "layer mix backward launch");
   });
@@ -200,7 +202,7 @@ static int launch_dh(const T* dbi, const T* dhn, const float* gx, const float* w
   if (ncb == 0 || groups == 0) return MHC_OK;
   const float inv_S = 1.f / (float)S;
   return for_batch_chunks(B, [&](int64_t b0, int64_t nb) {
-    dh_kernel<T, W, kDhTokens, HAS_DHN, kNtStores>
+    dh_kernel<T, W, kDhTokens, HAS_DHN, kNt>
         <<<dim3((unsigned)(groups * ncb), (unsigned)nb), kThreads, occupancy_lds(2), st>>>(
             dbi, dhn, gx, inv_S, WRow{w, kOut}, WRow{w + 8, kOut}, dH, S, D, ncb, b0);
     return hip_status(hipGetLastError(), "layer dH launch");
@@ -293,7 +295,7 @@ extern "C" int mhc_layer_add_forward(const void* H, int dtype_h, const void* bra
       constexpr int W = decltype(wtag)::value;
       return for_batch_chunks(B, [&](int64_t b0, int64_t nb) {
         const Geom g = make_geom<W, kLU>(S, D, b0);
-        mix_fwd_kernel<TH, TB, W, kLU, false, true, true, kNtStores>
+        mix_fwd_kernel<TH, TB, W, kLU, false, true, true, kNt>
             <<<dim3(g.ntiles, nb), kThreads, occupancy_lds(2), st>>>(
             (const TH*)H, (const TB*)branch_output, WRow{nullptr, 0}, WRow{w + 8, kOut}, WRow{w + 4, kOut},
             nullptr, (TH*)H_new, g);

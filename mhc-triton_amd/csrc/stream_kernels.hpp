@@ -24,8 +24,10 @@ namespace mhc {
 // closure forward, 5 loads per lane, runs at 73% of 8 TB/s with 8 workgroups
 // per CU and at 75-77% with 2-3; the closure backward at 69% and 74%).  The kernels use almost no LDS, so the cap is set
 // by reserving dynamic LDS at launch: at most `wg_per_cu` workgroups fit on a
-// CU.  Streamed outputs are written with non-temporal stores (NT = 2), which
-// lifts every write-heavy kernel by 3-6%.
+// CU.  Streamed tensors are read and written with the streaming (nt) cache
+// policy (NT bit 0: loads, bit 1: stores).  Through buffer spans (Span) nt
+// loads and stores lift the closure forward from 76% to 79-81% of 8 TB/s; on
+// 64-bit global addressing only the nt stores helped (3-6%).
 // ---------------------------------------------------------------------------
 constexpr size_t kLdsPerCu = 160 * 1024;
 
@@ -33,14 +35,14 @@ inline size_t occupancy_lds(int wg_per_cu) {
   return wg_per_cu <= 0 ? 0 : (kLdsPerCu / (size_t)wg_per_cu - 1024) & ~(size_t)255;
 }
 
-constexpr int kNtStores = 2;
+constexpr int kNt = 3;
 
-// Load order inside a tile.  The forward kernels (RAW_FIRST) load every
-// vector of the tile into raw fragments, keep the compiler from starting to
-// unpack before the last load is issued (scheduling barrier), then unpack:
-// +2-5% (the closure forward 74% -> 77% of 8 TB/s).  The backward kernels,
-// which carry 9-13 loads per item, unpack each vector as it is loaded
-// (ld<>): held back that way they lose 2-5%.
+// Load order inside a tile.  The forward kernels load every vector of the
+// tile into raw fragments, keep the compiler from starting to unpack before
+// the last load is issued (scheduling barrier), then unpack: +2-5% (the
+// closure forward 74% -> 77% of 8 TB/s).  The backward kernels, which carry
+// 9-13 loads per item, unpack each vector as it is loaded (ld<>): held back
+// that way they lose 2-5%.
 __device__ __forceinline__ void loads_issued() { __builtin_amdgcn_sched_barrier(0); }
 
 // Per-batch fp32 weight rows: element n of batch b is p[b * stride + n].
@@ -87,7 +89,7 @@ __device__ __forceinline__ void load_w16(WRow w, int64_t b, float (&v)[16]) {
 // Used for fused_stream_mix (BI + RES), the layer's branch_input pass (BI)
 // and the layer closure (RES + ADD_BO, H_residual never stored).
 // ---------------------------------------------------------------------------
-template <typename T, typename TB, int W, int U, bool BI, bool RES, bool ADD_BO, int NT = 0, bool RAW_FIRST = true>
+template <typename T, typename TB, int W, int U, bool BI, bool RES, bool ADD_BO, int NT = 0, bool BUF = (W > 1)>
 __global__ __launch_bounds__(kThreads) void mix_fwd_kernel(const T* __restrict__ H, const TB* __restrict__ bo,
                                                            WRow pre, WRow res, WRow post, T* __restrict__ bi,
                                                            T* __restrict__ out, Geom g) {
@@ -97,28 +99,35 @@ __global__ __launch_bounds__(kThreads) void mix_fwd_kernel(const T* __restrict__
   if constexpr (RES) load_w16(res, b, wr);
   if constexpr (ADD_BO) load_w4(post, b, wq);
   const int64_t D = g.D;
-  const T* Hb = H + b * g.S * 4 * D;
   for (uint32_t tile = blockIdx.x; tile < g.ntiles; tile += gridDim.x) {
+    // Spans start at the tile's first token.
+    const int64_t s_lo = (int64_t)(tile * (kThreads * U)) / g.nch;
+    const int64_t t0 = b * g.S + s_lo;
+    const int64_t rest = g.S - s_lo;
+    const Span<T, BUF> hs(H + t0 * 4 * D, rest * 4 * D);
     Frag<T, W> hf[U][4];
     Frag<TB, W> bf[U];
-    int64_t s_[U], cw[U];
+    uint32_t e4[U], e1[U];  // element offsets in the [.,4,D] and [.,D] spans
     bool ok[U];
 #pragma unroll
     for (int u = 0; u < U; ++u) {
       const uint32_t i = tile * (kThreads * U) + u * kThreads + threadIdx.x;
       ok[u] = i < g.items;
-      const uint32_t s = ok[u] ? i / g.nch : 0;
+      const uint32_t s = ok[u] ? i / g.nch : (uint32_t)s_lo;
       const uint32_t c = ok[u] ? i - s * g.nch : 0;
-      s_[u] = s;
-      cw[u] = (int64_t)c * W;
+      const uint32_t ds = s - (uint32_t)s_lo;
+      e4[u] = ds * 4 * (uint32_t)D + c * W;
+      e1[u] = ds * (uint32_t)D + c * W;
       if (ok[u]) {
-        const T* hp = Hb + s_[u] * 4 * D + cw[u];
 #pragma unroll
-        for (int n = 0; n < 4; ++n) hf[u][n].template load<(NT & 1) != 0>(hp + n * D);
-        if constexpr (ADD_BO) bf[u].template load<(NT & 1) != 0>(bo + b * g.S * D + s_[u] * D + cw[u]);
+        for (int n = 0; n < 4; ++n) hf[u][n].template load<(NT & 1) != 0>(hs, e4[u] + n * (uint32_t)D);
+        if constexpr (ADD_BO) {
+          const Span<TB, BUF> bs(bo + t0 * D, rest * D);
+          bf[u].template load<(NT & 1) != 0>(bs, e1[u]);
+        }
       }
     }
-    if constexpr (RAW_FIRST) loads_issued();
+    loads_issued();
 #pragma unroll
     for (int u = 0; u < U; ++u) {
       if (!ok[u]) continue;
@@ -131,10 +140,11 @@ __global__ __launch_bounds__(kThreads) void mix_fwd_kernel(const T* __restrict__
 #pragma unroll
         for (int e = 0; e < W; ++e)
           r[e] = wp[0] * h[0][e] + wp[1] * h[1][e] + wp[2] * h[2][e] + wp[3] * h[3][e];
-        st<T, W, (NT & 2) != 0>(bi + b * g.S * D + s_[u] * D + cw[u], r);
+        const Span<T, BUF> bis(bi + t0 * D, rest * D);
+        st<T, W, (NT & 2) != 0>(bis, e1[u], r);
       }
       if constexpr (RES) {
-        T* op = out + b * g.S * 4 * D + s_[u] * 4 * D + cw[u];
+        const Span<T, BUF> os(out + t0 * 4 * D, rest * 4 * D);
 #pragma unroll
         for (int n = 0; n < 4; ++n) {
           float r[W];
@@ -145,7 +155,7 @@ __global__ __launch_bounds__(kThreads) void mix_fwd_kernel(const T* __restrict__
             if constexpr (ADD_BO) v += wq[n] * bv[e];
             r[e] = v;
           }
-          st<T, W, (NT & 2) != 0>(op + n * D, r);
+          st<T, W, (NT & 2) != 0>(os, e4[u] + n * (uint32_t)D, r);
         }
       }
     }
@@ -156,7 +166,7 @@ __global__ __launch_bounds__(kThreads) void mix_fwd_kernel(const T* __restrict__
 // Add residual forward from a materialised H_residual (fused_add_residual):
 //   out[s,n,:] = hr[s,n,:] + post[n] bo[s,:]
 // ---------------------------------------------------------------------------
-template <typename T, typename TB, int W, int U, int NT = 0, bool RAW_FIRST = true>
+template <typename T, typename TB, int W, int U, int NT = 0, bool BUF = (W > 1)>
 __global__ __launch_bounds__(kThreads) void add_residual_fwd_kernel(const T* __restrict__ hr,
                                                                     const TB* __restrict__ bo, WRow post,
                                                                     T* __restrict__ out, Geom g) {
@@ -165,24 +175,31 @@ __global__ __launch_bounds__(kThreads) void add_residual_fwd_kernel(const T* __r
   load_w4(post, b, wq);
   const int64_t D = g.D;
   for (uint32_t tile = blockIdx.x; tile < g.ntiles; tile += gridDim.x) {
+    const int64_t s_lo = (int64_t)(tile * (kThreads * U)) / g.nch;
+    const int64_t t0 = b * g.S + s_lo;
+    const int64_t rest = g.S - s_lo;
+    const Span<T, BUF> hs(hr + t0 * 4 * D, rest * 4 * D);
+    const Span<TB, BUF> bs(bo + t0 * D, rest * D);
     Frag<T, W> hf[U][4];
     Frag<TB, W> bf[U];
-    int64_t hoff[U];
+    uint32_t e4[U];
     bool ok[U];
 #pragma unroll
     for (int u = 0; u < U; ++u) {
       const uint32_t i = tile * (kThreads * U) + u * kThreads + threadIdx.x;
       ok[u] = i < g.items;
-      const uint32_t s = ok[u] ? i / g.nch : 0;
+      const uint32_t s = ok[u] ? i / g.nch : (uint32_t)s_lo;
       const uint32_t c = ok[u] ? i - s * g.nch : 0;
-      hoff[u] = b * g.S * 4 * D + (int64_t)s * 4 * D + (int64_t)c * W;
+      const uint32_t ds = s - (uint32_t)s_lo;
+      e4[u] = ds * 4 * (uint32_t)D + c * W;
       if (ok[u]) {
 #pragma unroll
-        for (int n = 0; n < 4; ++n) hf[u][n].template load<(NT & 1) != 0>(hr + hoff[u] + n * D);
-        bf[u].template load<(NT & 1) != 0>(bo + b * g.S * D + (int64_t)s * D + (int64_t)c * W);
+        for (int n = 0; n < 4; ++n) hf[u][n].template load<(NT & 1) != 0>(hs, e4[u] + n * (uint32_t)D);
+        bf[u].template load<(NT & 1) != 0>(bs, ds * (uint32_t)D + c * W);
       }
     }
-    if constexpr (RAW_FIRST) loads_issued();
+    loads_issued();
+    const Span<T, BUF> os(out + t0 * 4 * D, rest * 4 * D);
 #pragma unroll
     for (int u = 0; u < U; ++u) {
       if (!ok[u]) continue;
@@ -195,7 +212,7 @@ __global__ __launch_bounds__(kThreads) void add_residual_fwd_kernel(const T* __r
         float r[W];
 #pragma unroll
         for (int e = 0; e < W; ++e) r[e] = h[n][e] + wq[n] * bv[e];
-        st<T, W, (NT & 2) != 0>(out + hoff[u] + n * D, r);
+        st<T, W, (NT & 2) != 0>(os, e4[u] + n * (uint32_t)D, r);
       }
     }
   }
@@ -206,7 +223,7 @@ __global__ __launch_bounds__(kThreads) void add_residual_fwd_kernel(const T* __r
 //   d_bo[s,:] = sum_n post[n] dHn[s,n,:]              (written, dtype TB)
 //   part[k]   = sum dHn[s,k,:] * bo[s,:]   k < 4      (reduced -> dH_post)
 // ---------------------------------------------------------------------------
-template <typename T, typename TB, int W, int U, int NT = 0>
+template <typename T, typename TB, int W, int U, int NT = 0, bool BUF = (W > 1)>
 __global__ __launch_bounds__(kThreads) void add_residual_bwd_kernel(const T* __restrict__ dhn,
                                                                     const TB* __restrict__ bo, WRow post,
                                                                     TB* __restrict__ dbo, float* __restrict__ part,
@@ -218,22 +235,29 @@ __global__ __launch_bounds__(kThreads) void add_residual_bwd_kernel(const T* __r
   const int64_t D = g.D;
   float acc[4] = {0.f, 0.f, 0.f, 0.f};
   for (uint32_t tile = blockIdx.x; tile < g.ntiles; tile += gridDim.x) {
+    const int64_t s_lo = (int64_t)(tile * (kThreads * U)) / g.nch;
+    const int64_t t0 = b * g.S + s_lo;
+    const int64_t rest = g.S - s_lo;
+    const Span<T, BUF> hs(dhn + t0 * 4 * D, rest * 4 * D);
+    const Span<TB, BUF> bs(bo + t0 * D, rest * D);
+    const Span<TB, BUF> ds_(dbo + t0 * D, rest * D);
     float h[U][4][W];
     float bv[U][W];
-    int64_t boff[U];
+    uint32_t e1[U];
     bool ok[U];
 #pragma unroll
     for (int u = 0; u < U; ++u) {
       const uint32_t i = tile * (kThreads * U) + u * kThreads + threadIdx.x;
       ok[u] = i < g.items;
-      const uint32_t s = ok[u] ? i / g.nch : 0;
+      const uint32_t s = ok[u] ? i / g.nch : (uint32_t)s_lo;
       const uint32_t c = ok[u] ? i - s * g.nch : 0;
-      boff[u] = b * g.S * D + (int64_t)s * D + (int64_t)c * W;
+      const uint32_t dt = s - (uint32_t)s_lo;
+      e1[u] = dt * (uint32_t)D + c * W;
       if (ok[u]) {
-        const T* hp = dhn + b * g.S * 4 * D + (int64_t)s * 4 * D + (int64_t)c * W;
+        const uint32_t e4 = dt * 4 * (uint32_t)D + c * W;
 #pragma unroll
-        for (int n = 0; n < 4; ++n) ld<T, W, (NT & 1) != 0>(hp + n * D, h[u][n]);
-        ld<TB, W, (NT & 1) != 0>(bo + boff[u], bv[u]);
+        for (int n = 0; n < 4; ++n) ld<T, W, (NT & 1) != 0>(hs, e4 + n * (uint32_t)D, h[u][n]);
+        ld<TB, W, (NT & 1) != 0>(bs, e1[u], bv[u]);
       }
     }
 #pragma unroll
@@ -246,7 +270,7 @@ __global__ __launch_bounds__(kThreads) void add_residual_bwd_kernel(const T* __r
 #pragma unroll
         for (int n = 0; n < 4; ++n) acc[n] += h[u][n][e] * bv[u][e];
       }
-      st<TB, W, (NT & 2) != 0>(dbo + boff[u], r);
+      st<TB, W, (NT & 2) != 0>(ds_, e1[u], r);
     }
   }
   block_sum<4>(acc, lds);
@@ -265,8 +289,11 @@ __global__ __launch_bounds__(kThreads) void add_residual_bwd_kernel(const T* __r
 //             part[4:20] = sum dhn[s,n,:] * H[s,m,:]   -> dH_res (n-major)
 // HAS_DHN = false treats dhn as zero (H_new / H_residual got no gradient).
 // (The dynamic layer's dH, which also adds grad_x / S, is dh_kernel.)
+// NT bit 2 puts the nt policy on the H loads alone: the dynamic layer's pass B
+// reads H for the last time but d_bi and dH_new again in pass C, which then
+// finds part of them in the 256 MB memory-side cache.
 // ---------------------------------------------------------------------------
-template <typename T, int W, int U, bool HAS_DHN, bool REDUCE, bool WRITE_DH, int NT = 0>
+template <typename T, int W, int U, bool HAS_DHN, bool REDUCE, bool WRITE_DH, int NT = 0, bool BUF = (W > 1)>
 __global__ __launch_bounds__(kThreads) void mix_bwd_kernel(const T* __restrict__ dbi, const T* __restrict__ dhn,
                                                            const T* __restrict__ H, WRow pre, WRow res,
                                                            T* __restrict__ dH, float* __restrict__ part, Geom g) {
@@ -282,34 +309,38 @@ __global__ __launch_bounds__(kThreads) void mix_bwd_kernel(const T* __restrict__
 #pragma unroll
   for (int k = 0; k < 20; ++k) acc[k] = 0.f;
   for (uint32_t tile = blockIdx.x; tile < g.ntiles; tile += gridDim.x) {
+    const int64_t s_lo = (int64_t)(tile * (kThreads * U)) / g.nch;
+    const int64_t t0 = b * g.S + s_lo;
+    const int64_t rest = g.S - s_lo;
+    const Span<T, BUF> dbs(dbi + t0 * D, rest * D);
+    const Span<T, BUF> dns(dhn + t0 * 4 * D, rest * 4 * D);
+    const Span<T, BUF> hs(H + t0 * 4 * D, rest * 4 * D);
     float db[U][W];
     float dn[U][4][W];
     float h[U][4][W];
-    int64_t off[U];  // offset of (s, n=0, c*W) in the [S,4,D] plane
-    int64_t cw[U];
-    int64_t s_[U];
+    uint32_t e4[U];  // element offset of (s, n=0, c*W) in the [.,4,D] spans
     bool ok[U];
 #pragma unroll
     for (int u = 0; u < U; ++u) {
       const uint32_t i = tile * (kThreads * U) + u * kThreads + threadIdx.x;
       ok[u] = i < g.items;
-      const uint32_t s = ok[u] ? i / g.nch : 0;
+      const uint32_t s = ok[u] ? i / g.nch : (uint32_t)s_lo;
       const uint32_t c = ok[u] ? i - s * g.nch : 0;
-      s_[u] = s;
-      cw[u] = (int64_t)c * W;
-      off[u] = b * g.S * 4 * D + (int64_t)s * 4 * D + cw[u];
+      const uint32_t dt = s - (uint32_t)s_lo;
+      e4[u] = dt * 4 * (uint32_t)D + c * W;
       if (ok[u]) {
-        ld<T, W, (NT & 1) != 0>(dbi + b * g.S * D + (int64_t)s * D + cw[u], db[u]);
+        ld<T, W, (NT & 1) != 0>(dbs, dt * (uint32_t)D + c * W, db[u]);
         if constexpr (HAS_DHN) {
 #pragma unroll
-          for (int n = 0; n < 4; ++n) ld<T, W, (NT & 1) != 0>(dhn + off[u] + n * D, dn[u][n]);
+          for (int n = 0; n < 4; ++n) ld<T, W, (NT & 1) != 0>(dns, e4[u] + n * (uint32_t)D, dn[u][n]);
         }
         if constexpr (REDUCE) {
 #pragma unroll
-          for (int n = 0; n < 4; ++n) ld<T, W, (NT & 1) != 0>(H + off[u] + n * D, h[u][n]);
+          for (int n = 0; n < 4; ++n) ld<T, W, (NT & 5) != 0>(hs, e4[u] + n * (uint32_t)D, h[u][n]);
         }
       }
     }
+    const Span<T, BUF> dHs(dH + t0 * 4 * D, rest * 4 * D);
 #pragma unroll
     for (int u = 0; u < U; ++u) {
       if (!ok[u]) continue;
@@ -341,7 +372,7 @@ __global__ __launch_bounds__(kThreads) void mix_bwd_kernel(const T* __restrict__
             }
             r[e] = v;
           }
-          st<T, W, (NT & 2) != 0>(dH + off[u] + m * D, r);
+          st<T, W, (NT & 2) != 0>(dHs, e4[u] + m * (uint32_t)D, r);
         }
       }
     }
@@ -367,7 +398,7 @@ __global__ __launch_bounds__(kThreads) void mix_bwd_kernel(const T* __restrict__
 // Grid: x = token group * ncb + column block (ncb blocks of 256 items), y =
 // batch within the launch.
 // ---------------------------------------------------------------------------
-template <typename T, int W, int TT, bool HAS_DHN, int NT = 0>
+template <typename T, int W, int TT, bool HAS_DHN, int NT = 0, bool BUF = (W > 1)>
 __global__ __launch_bounds__(kThreads) void dh_kernel(const T* __restrict__ dbi, const T* __restrict__ dhn,
                                                       const float* __restrict__ gx, float inv_S, WRow pre,
                                                       WRow res, T* __restrict__ dH, int64_t S, int64_t D,
@@ -378,6 +409,11 @@ __global__ __launch_bounds__(kThreads) void dh_kernel(const T* __restrict__ dbi,
   const int64_t c = (int64_t)cblk * kThreads + threadIdx.x;
   if (c >= D / W) return;
   const int64_t cw = c * W;
+  const int64_t t0 = b * S + s0;
+  const int64_t rest = S - s0;
+  const Span<T, BUF> dbs(dbi + t0 * D, rest * D);
+  const Span<T, BUF> dns(dhn + t0 * 4 * D, rest * 4 * D);
+  const Span<T, BUF> dHs(dH + t0 * 4 * D, rest * 4 * D);
   float wp[4], wr[16];
   load_w4(pre, b, wp);
   if constexpr (HAS_DHN) load_w16(res, b, wr);
@@ -388,13 +424,13 @@ __global__ __launch_bounds__(kThreads) void dh_kernel(const T* __restrict__ dbi,
   for (int t = 0; t < TT; ++t) {
     const int64_t s = s0 + t;
     if (s >= S) break;
-    const int64_t off = b * S * 4 * D + s * 4 * D + cw;
+    const uint32_t e4 = (uint32_t)t * 4 * (uint32_t)D + (uint32_t)cw;
     Frag<T, W> bf;
     Frag<T, W> nf[4];
-    bf.template load<(NT & 1) != 0>(dbi + b * S * D + s * D + cw);
+    bf.template load<(NT & 1) != 0>(dbs, (uint32_t)t * (uint32_t)D + (uint32_t)cw);
     if constexpr (HAS_DHN) {
 #pragma unroll
-      for (int n = 0; n < 4; ++n) nf[n].template load<(NT & 1) != 0>(dhn + off + n * D);
+      for (int n = 0; n < 4; ++n) nf[n].template load<(NT & 1) != 0>(dns, e4 + n * (uint32_t)D);
     }
     loads_issued();
     float db[W], dn[4][W];
@@ -415,7 +451,7 @@ __global__ __launch_bounds__(kThreads) void dh_kernel(const T* __restrict__ dbi,
         }
         r[e] = __builtin_fmaf(gv[m][e], inv_S, v);
       }
-      st<T, W, (NT & 2) != 0>(dH + off + m * D, r);
+      st<T, W, (NT & 2) != 0>(dHs, e4 + m * (uint32_t)D, r);
     }
   }
 }
@@ -429,41 +465,50 @@ __global__ __launch_bounds__(kThreads) void dh_kernel(const T* __restrict__ dbi,
 // each other's backward.  An item is W consecutive elements of one token row;
 // W is the wider 16-byte vector of the two dtypes (or 1 on the ragged path).
 // ---------------------------------------------------------------------------
-template <typename TX, typename TH, int W, int NT = 0>
+template <typename TX, typename TH, int W, int NT = 0, bool BUF = (W > 1)>
 __global__ __launch_bounds__(kThreads) void expand_kernel(const TX* __restrict__ x, TH* __restrict__ H,
                                                           float scale, Geom g) {
   const int64_t b = g.b0 + blockIdx.y;
   const int64_t D = g.D;
   for (uint32_t tile = blockIdx.x; tile < g.ntiles; tile += gridDim.x) {
+    const int64_t s_lo = (int64_t)(tile * kThreads) / g.nch;
+    const int64_t t0 = b * g.S + s_lo;
+    const int64_t rest = g.S - s_lo;
     const uint32_t i = tile * kThreads + threadIdx.x;
     if (i >= g.items) continue;
     const uint32_t s = i / g.nch;
-    const int64_t cw = (int64_t)(i - s * g.nch) * W;
+    const uint32_t cw = (i - s * g.nch) * W;
+    const uint32_t dt = s - (uint32_t)s_lo;
+    const Span<TX, BUF> xs(x + t0 * D, rest * D);
+    const Span<TH, BUF> hs(H + t0 * 4 * D, rest * 4 * D);
     float v[W];
-    ld<TX, W, (NT & 1) != 0>(x + b * g.S * D + (int64_t)s * D + cw, v);
+    ld<TX, W, (NT & 1) != 0>(xs, dt * (uint32_t)D + cw, v);
 #pragma unroll
     for (int e = 0; e < W; ++e) v[e] *= scale;
-    TH* out = H + b * g.S * 4 * D + (int64_t)s * 4 * D + cw;
 #pragma unroll
-    for (int n = 0; n < 4; ++n) st<TH, W, (NT & 2) != 0>(out + n * D, v);
+    for (int n = 0; n < 4; ++n) st<TH, W, (NT & 2) != 0>(hs, dt * 4 * (uint32_t)D + cw + n * (uint32_t)D, v);
   }
 }
 
-template <typename TH, typename TY, int W, int NT = 0>
+template <typename TH, typename TY, int W, int NT = 0, bool BUF = (W > 1)>
 __global__ __launch_bounds__(kThreads) void collapse_kernel(const TH* __restrict__ H, TY* __restrict__ y,
                                                             float scale, Geom g) {
   const int64_t b = g.b0 + blockIdx.y;
   const int64_t D = g.D;
   for (uint32_t tile = blockIdx.x; tile < g.ntiles; tile += gridDim.x) {
+    const int64_t s_lo = (int64_t)(tile * kThreads) / g.nch;
+    const int64_t t0 = b * g.S + s_lo;
+    const int64_t rest = g.S - s_lo;
     const uint32_t i = tile * kThreads + threadIdx.x;
     const bool ok = i < g.items;
-    const uint32_t s = ok ? i / g.nch : 0;
-    const int64_t cw = ok ? (int64_t)(i - s * g.nch) * W : 0;
-    const int64_t hoff = b * g.S * 4 * D + (int64_t)s * 4 * D + cw;
+    const uint32_t s = ok ? i / g.nch : (uint32_t)s_lo;
+    const uint32_t cw = ok ? (i - s * g.nch) * W : 0;
+    const uint32_t dt = s - (uint32_t)s_lo;
+    const Span<TH, BUF> hs(H + t0 * 4 * D, rest * 4 * D);
     Frag<TH, W> hf[4];
     if (ok) {
 #pragma unroll
-      for (int n = 0; n < 4; ++n) hf[n].template load<(NT & 1) != 0>(H + hoff + n * D);
+      for (int n = 0; n < 4; ++n) hf[n].template load<(NT & 1) != 0>(hs, dt * 4 * (uint32_t)D + cw + n * (uint32_t)D);
     }
     loads_issued();
     if (!ok) continue;
@@ -472,7 +517,8 @@ __global__ __launch_bounds__(kThreads) void collapse_kernel(const TH* __restrict
     for (int n = 0; n < 4; ++n) hf[n].unpack(h[n]);
 #pragma unroll
     for (int e = 0; e < W; ++e) r[e] = (((h[0][e] + h[1][e]) + h[2][e]) + h[3][e]) * scale;
-    st<TY, W, (NT & 2) != 0>(y + b * g.S * D + (int64_t)s * D + cw, r);
+    const Span<TY, BUF> ys(y + t0 * D, rest * D);
+    st<TY, W, (NT & 2) != 0>(ys, dt * (uint32_t)D + cw, r);
   }
 }
 
@@ -507,9 +553,13 @@ __global__ __launch_bounds__(kThreads) void reduce_split_kernel(const float* __r
 // ---------------------------------------------------------------------------
 
 // True when every pointer is 16-byte aligned and D splits into whole 16-byte
-// vectors of every dtype involved.
+// vectors of every dtype involved.  The vector path addresses through
+// per-workgroup buffer spans (Span): a tile of up to 2 * 256 items touches at
+// most 2 + 4096 / nch tokens (dh_kernel: 2), i.e. under (16384 + 8 D) elements
+// of a [., 4, D] tensor, which must stay below 2^31 bytes for fp32.
 inline bool vec_ok(int64_t D, int W, std::initializer_list<const void*> ptrs) {
   if (D % W != 0) return false;
+  if (!span_ok(16384 + 8 * D, 4)) return false;
   for (const void* p : ptrs)
     if (p && !aligned16(p)) return false;
   return true;

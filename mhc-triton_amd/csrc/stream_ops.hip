@@ -13,7 +13,7 @@ static int stream_mix_fwd(const T* H, const float* pre, const float* res, T* bi,
   return for_batch_chunks(B, [&](int64_t b0, int64_t nb) {
     const Geom g = make_geom<W, kU>(S, D, b0);
     if (g.ntiles == 0) return (int)MHC_OK;
-    mix_fwd_kernel<T, T, W, kU, true, true, false, kNtStores><<<dim3(g.ntiles, nb), kThreads, occupancy_lds(2), st>>>(
+    mix_fwd_kernel<T, T, W, kU, true, true, false, kNt><<<dim3(g.ntiles, nb), kThreads, occupancy_lds(2), st>>>(
         H, (const T*)nullptr, WRow{pre, 4}, WRow{res, 16}, WRow{nullptr, 0}, bi, out, g);
     return hip_status(hipGetLastError(), "stream_mix_forward launch");
   });
@@ -27,7 +27,7 @@ static int stream_mix_bwd(const T* dbi, const T* dhr, const T* H, const float* p
   const uint32_t nblk = reduce_blocks(g0.ntiles, B);
   int rc = for_batch_chunks(B, [&](int64_t b0, int64_t nb) {
     const Geom g = make_geom<W, kU>(S, D, b0);
-    mix_bwd_kernel<T, W, kU, true, true, true, kNtStores><<<dim3(nblk, nb), kThreads, occupancy_lds(3), st>>>(
+    mix_bwd_kernel<T, W, kU, true, true, true, kNt><<<dim3(nblk, nb), kThreads, occupancy_lds(3), st>>>(
         dbi, dhr, H, WRow{pre, 4}, WRow{res, 16}, dH, part, g);
     return hip_status(hipGetLastError(), "stream_mix_backward launch");
   });
@@ -42,7 +42,7 @@ static int add_res_fwd(const TH* hr, const TB* bo, const float* post, TH* out, i
   return for_batch_chunks(B, [&](int64_t b0, int64_t nb) {
     const Geom g = make_geom<W, kU>(S, D, b0);
     if (g.ntiles == 0) return (int)MHC_OK;
-    add_residual_fwd_kernel<TH, TB, W, kU, kNtStores><<<dim3(g.ntiles, nb), kThreads, occupancy_lds(2), st>>>(
+    add_residual_fwd_kernel<TH, TB, W, kU, kNt><<<dim3(g.ntiles, nb), kThreads, occupancy_lds(4), st>>>(
         hr, bo, WRow{post, 4}, out, g);
     return hip_status(hipGetLastError(), "add_residual_forward launch");
   });
@@ -55,7 +55,7 @@ static int add_res_bwd(const TH* dhn, const TB* bo, WRow post, TB* dbo, float* d
   const uint32_t nblk = reduce_blocks(g0.ntiles, B);
   int rc = for_batch_chunks(B, [&](int64_t b0, int64_t nb) {
     const Geom g = make_geom<W, kU>(S, D, b0);
-    add_residual_bwd_kernel<TH, TB, W, kU, kNtStores><<<dim3(nblk, nb), kThreads, occupancy_lds(2), st>>>(
+    add_residual_bwd_kernel<TH, TB, W, kU, kNt><<<dim3(nblk, nb), kThreads, occupancy_lds(2), st>>>(
         dhn, bo, post, dbo, part, g);
     return hip_status(hipGetLastError(), "add_residual_backward launch");
   });
@@ -214,7 +214,8 @@ template <typename TX, typename TH, int W>
 static int expand_launch(const TX* x, TH* H, float scale, int64_t B, int64_t S, int64_t D, hipStream_t st) {
   return for_batch_chunks(B, [&](int64_t b0, int64_t nb) {
     const Geom g = make_geom<W, 1>(S, D, b0);
-    expand_kernel<TX, TH, W, kNtStores><<<dim3(g.ntiles, nb), kThreads, occupancy_lds(2), st>>>(x, H, scale, g);
+    // nt stores only: with nt on its one load this write-dominated kernel runs 10% slower.
+    expand_kernel<TX, TH, W, 2><<<dim3(g.ntiles, nb), kThreads, occupancy_lds(2), st>>>(x, H, scale, g);
     return hip_status(hipGetLastError(), "stream_expand launch");
   });
 }
@@ -223,7 +224,7 @@ template <typename TH, typename TY, int W>
 static int collapse_launch(const TH* H, TY* y, float scale, int64_t B, int64_t S, int64_t D, hipStream_t st) {
   return for_batch_chunks(B, [&](int64_t b0, int64_t nb) {
     const Geom g = make_geom<W, 1>(S, D, b0);
-    collapse_kernel<TH, TY, W, kNtStores><<<dim3(g.ntiles, nb), kThreads, occupancy_lds(3), st>>>(H, y, scale, g);
+    collapse_kernel<TH, TY, W, kNt><<<dim3(g.ntiles, nb), kThreads, occupancy_lds(4), st>>>(H, y, scale, g);
     return hip_status(hipGetLastError(), "stream_collapse launch");
   });
 }
