@@ -231,10 +231,12 @@ static int launch_meanpool(const T* H, float* x, const float* phi, float* projpa
   const bool phi_vec = phi ? aligned16(phi) : false;
   for (int64_t b0 = 0; b0 < B; b0 += kMaxGridY) {
     const int64_t nb = (B - b0) < kMaxGridY ? (B - b0) : kMaxGridY;
-    // Plain loads: in the layer, branch_input reads H next and finds part of it
-    // in the 256 MB memory-side cache.
-    colsum_kernel<T, W, kPoolUN, false><<<dim3((unsigned)p.ncc, (unsigned)p.nS, (unsigned)nb), kThreads, 0, st>>>(
-        H, colpart, S, K, p.SC, p.nS, b0);
+    // The first half of each S chunk with nt loads, the second half plain: in
+    // the layer, branch_input reads H next and finds the chunk tails in the
+    // memory-side cache (colsum + branch_input: -4 us at config-3 size, -6 us
+    // at config 4, against all plain).
+    colsum_kernel<T, W, kPoolUN><<<dim3((unsigned)p.ncc, (unsigned)p.nS, (unsigned)nb), kThreads, 0, st>>>(
+        H, colpart, S, K, p.SC, p.nS, p.SC / 2, b0);
     if (int rc = hip_status(hipGetLastError(), "mean_pool column-sum launch")) return rc;
     colsum_reduce_kernel<PROJ><<<dim3((unsigned)p.nrc, (unsigned)nb), kThreads, 0, st>>>(
         colpart, x, phi, projpart, K, p.nS, inv_S, b0, phi_vec);

@@ -550,25 +550,14 @@ __global__ __launch_bounds__(kThreads) void dynw_gphi_reduce_kernel(const float*
 //   dynamic-weight projection needs no extra pass over x.
 // ---------------------------------------------------------------------------
 // Loads go through a buffer span rebased at each group of UN rows (the host
-// keeps UN rows of K under 2^31 bytes), with the streaming (nt) policy when
-// NT is set.
-template <typename T, int W, int UN, bool NT = true, bool BUF = (W > 1)>
-__global__ __launch_bounds__(kThreads) void colsum_kernel(const T* __restrict__ H, float* __restrict__ colpart,
-                                                          int64_t S, int64_t K, int64_t SC, int nS, int64_t b0) {
-  const int64_t b = b0 + blockIdx.z;
-  const int sc = blockIdx.y;
-  const int64_t cblk = (int64_t)blockIdx.x * (kThreads * W);
-  const int64_t col = cblk + (int64_t)threadIdx.x * W;
-  if (col >= K) return;
-  const int64_t sbeg = (int64_t)sc * SC;
-  const int64_t send = sbeg + SC < S ? sbeg + SC : S;
-  float acc[W];
-#pragma unroll
-  for (int e = 0; e < W; ++e) acc[e] = 0.f;
-  const T* base = H + b * S * K + cblk;
-  const uint32_t lane_e = (uint32_t)threadIdx.x * W;
-  int64_t s = sbeg;
-  for (; s + (UN - 1) < send; s += UN) {
+// keeps UN rows of K under 2^31 bytes).  The first nt_rows rows of each S
+// chunk are read with the streaming (nt) policy, the rest plain: what
+// branch_input reads next and can find in the 256 MB memory-side cache is the
+// tail of every chunk, and nt on the rest speeds this read up.
+template <bool NT, typename T, int W, int UN, bool BUF>
+__device__ __forceinline__ void colsum_rows(const T* base, int64_t K, uint32_t lane_e, int64_t& s, int64_t end,
+                                            float* acc) {
+  for (; s + (UN - 1) < end; s += UN) {
     const Span<T, BUF> sp(base + s * K, (int64_t)UN * K);
     float v[UN][W];
 #pragma unroll
@@ -578,13 +567,35 @@ __global__ __launch_bounds__(kThreads) void colsum_kernel(const T* __restrict__ 
 #pragma unroll
       for (int e = 0; e < W; ++e) acc[e] += v[u][e];
   }
-  for (; s < send; ++s) {
+  for (; s < end; ++s) {
     const Span<T, BUF> sp(base + s * K, K);
     float v[W];
     ld<T, W, NT>(sp, lane_e, v);
 #pragma unroll
     for (int e = 0; e < W; ++e) acc[e] += v[e];
   }
+}
+
+template <typename T, int W, int UN, bool BUF = (W > 1)>
+__global__ __launch_bounds__(kThreads) void colsum_kernel(const T* __restrict__ H, float* __restrict__ colpart,
+                                                          int64_t S, int64_t K, int64_t SC, int nS, int64_t nt_rows,
+                                                          int64_t b0) {
+  const int64_t b = b0 + blockIdx.z;
+  const int sc = blockIdx.y;
+  const int64_t cblk = (int64_t)blockIdx.x * (kThreads * W);
+  const int64_t col = cblk + (int64_t)threadIdx.x * W;
+  if (col >= K) return;
+  const int64_t sbeg = (int64_t)sc * SC;
+  const int64_t send = sbeg + SC < S ? sbeg + SC : S;
+  const int64_t smid = sbeg + nt_rows < send ? sbeg + nt_rows : send;
+  float acc[W];
+#pragma unroll
+  for (int e = 0; e < W; ++e) acc[e] = 0.f;
+  const T* base = H + b * S * K + cblk;
+  const uint32_t lane_e = (uint32_t)threadIdx.x * W;
+  int64_t s = sbeg;
+  colsum_rows<true, T, W, UN, BUF>(base, K, lane_e, s, smid, acc);
+  colsum_rows<false, T, W, UN, BUF>(base, K, lane_e, s, send, acc);
   st<float, W>(colpart + ((b * nS + sc) * K + col), acc);
 }
 
