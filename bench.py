@@ -3,6 +3,7 @@
 
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload config3]
     python bench.py --ops        # the low-level ops one by one (one JSON line)
+    python bench.py --readme     # the reference's own benchmark table, same workloads
 
 One "step" is the HyperConnection layer's forward and backward over one
 synthetic batch, exactly as a transformer block uses it:
@@ -82,6 +83,10 @@ def _parse():
     ap.add_argument("--ops", action="store_true",
                     help="time the low-level ops one by one (config-2 Sinkhorn, the stream ops and "
                          "expand / collapse at config-3 size, dynamic weights) and exit")
+    ap.add_argument("--readme", action="store_true",
+                    help="run the reference's published benchmark table (README.md:183-202, made by "
+                         "benchmarks/benchmark.py) on this build: same workloads, same timing method, "
+                         "beside the published H100 numbers, and exit")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="only run 3 plain device copies of 512 MiB (the known-size kernel that scales "
                          "rocprofv3 FETCH_SIZE / WRITE_SIZE readings into bytes) and exit")
@@ -182,6 +187,138 @@ def _ops_leg(n: int = 20, warm: int = 3) -> dict:
 
     # x read by the forward, x read and grad_x written by the backward
     rec("dynamic_weights_fwd+bwd R=16384 K=16384 bf16", timed(fwd_bwd, 5), 3 * T * 4 * D * e)
+    return out
+
+
+# The reference's published table (README.md:183-202): NVIDIA H100 80GB HBM3, batch=16, seq=2048,
+# dim=4096, fp16, made by benchmarks/benchmark.py.  Times in ms, memory in MB.
+README_PUBLISHED = {
+    "sinkhorn_20iter": {"pytorch_ms": 0.74, "triton_ms": 0.47},
+    "stream_mix": {"pytorch_ms": 8.53, "triton_ms": 1.00},
+    "add_residual": {"pytorch_ms": 2.57, "triton_ms": 0.89},
+    "dynamic_weights": {"pytorch_ms": 0.90, "triton_ms": 0.11},
+    "full_forward_backward": {"pytorch_ms": 85.00, "triton_ms": 13.66},
+    "peak_memory_sinkhorn_backward": {"pytorch_mb": 120.0, "triton_mb": 68.0},
+    "peak_memory_full_forward_backward": {"pytorch_mb": 8003.6, "triton_mb": 6162.8},
+}
+
+
+def _readme_leg(batch: int = 16, seq: int = 2048, dim: int = 4096) -> dict:
+    """The reference's benchmark table on this build, one op at a time, the way
+    benchmarks/benchmark.py measures it: 10 warm-up calls, then the mean wall time of 100
+    calls between two device synchronisations (time.perf_counter), on fp16 inputs drawn
+    as the script draws them (:53-138, :141-180).  The same workloads also run through
+    the package's pure-PyTorch baselines (the reference's `*_torch` path) on this GPU, and
+    peak memory is measured as the script does (:184-200)."""
+    import torch
+
+    import mhc
+
+    dev = "cuda"
+    torch.manual_seed(0)
+
+    def wall_ms(fn, warmup=10, repeats=100):
+        for _ in range(warmup):
+            fn()
+        torch.cuda.synchronize()
+        t = time.perf_counter()
+        for _ in range(repeats):
+            fn()
+        torch.cuda.synchronize()
+        return (time.perf_counter() - t) / repeats * 1e3
+
+    def peak_mb(fn, warmup=3):
+        for _ in range(warmup):
+            fn()
+        torch.cuda.synchronize()
+        torch.cuda.empty_cache()
+        torch.cuda.reset_peak_memory_stats()
+        fn()
+        torch.cuda.synchronize()
+        return torch.cuda.max_memory_allocated() / (1024 * 1024)
+
+    out = {}
+
+    def rec(name, ours, torch_path, unit="ms"):
+        pub = README_PUBLISHED[name]
+        key = "triton_" + unit
+        out[name] = {f"ours_{unit}": round(ours, 4), f"torch_baseline_mi355x_{unit}": round(torch_path, 4),
+                     f"published_h100_triton_{unit}": pub[key],
+                     f"published_h100_pytorch_{unit}": pub["pytorch_" + unit],
+                     "published_triton_over_ours": round(pub[key] / ours, 2)}
+
+    half = torch.float16
+
+    # Each workload lives in its own function, as in the script, so that nothing from
+    # another one is allocated while it is measured.
+    def sinkhorn():  # (:53-64), batch*seq matrices
+        M = torch.randn(batch * seq, 4, 4, device=dev, dtype=half)
+        rec("sinkhorn_20iter", wall_ms(lambda: mhc.sinkhorn_knopp(M, num_iters=20)),
+            wall_ms(lambda: mhc.sinkhorn_knopp_torch(M, num_iters=20)))
+
+    def stream_mix():  # (:67-83)
+        H = torch.randn(batch, seq, 4, dim, device=dev, dtype=half)
+        H_pre = torch.softmax(torch.randn(batch, 4, device=dev, dtype=half), dim=-1)
+        H_res = mhc.sinkhorn_knopp(torch.randn(batch, 4, 4, device=dev, dtype=half), num_iters=20)
+        rec("stream_mix", wall_ms(lambda: mhc.fused_stream_mix(H, H_pre, H_res)),
+            wall_ms(lambda: mhc.fused_stream_mix_torch(H, H_pre, H_res)))
+
+    def add_residual():  # (:86-106)
+        H_residual = torch.randn(batch, seq, 4, dim, device=dev, dtype=half)
+        bo = torch.randn(batch, seq, dim, device=dev, dtype=half)
+        H_post = torch.softmax(torch.randn(batch, 4, device=dev, dtype=half), dim=-1)
+        rec("add_residual", wall_ms(lambda: mhc.fused_add_residual(H_residual, bo, H_post)),
+            wall_ms(lambda: mhc.fused_add_residual_torch(H_residual, bo, H_post)))
+
+    def dynamic_weights():  # (:109-138), x [batch, 4*dim] fp32
+        x = torch.randn(batch, 4 * dim, device=dev)
+        phi = torch.randn(4 * dim, 24, device=dev) * 0.01
+        bias = torch.randn(24, device=dev)
+        al = [torch.tensor(0.1, device=dev) for _ in range(3)]
+        rec("dynamic_weights", wall_ms(lambda: mhc.fused_dynamic_weights(x, phi, bias, *al)),
+            wall_ms(lambda: mhc.fused_dynamic_weights_torch(x, phi, bias, *al)))
+
+    def full_layer(measure):  # (:141-180 and :226-260), fp16 module
+        hc = mhc.HyperConnection(dim=dim, num_streams=4, dynamic=True).to(dev).half()
+        hc_t = mhc.HyperConnectionTorch(dim=dim, num_streams=4, dynamic=True).to(dev).half()
+        hc_t.load_state_dict(hc.state_dict())
+        H = torch.randn(batch, seq, 4, dim, device=dev, dtype=half, requires_grad=True)
+
+        def fwd_bwd(module):
+            def run():
+                H_in = H.detach().requires_grad_(True)
+                bi, add_residual = module(H_in)
+                H_new = add_residual(bi * 0.5)
+                H_new.sum().backward()
+                return H_in.grad
+            return run
+
+        if measure == "time":
+            rec("full_forward_backward", wall_ms(fwd_bwd(hc)), wall_ms(fwd_bwd(hc_t), warmup=2, repeats=10))
+        else:
+            ours = peak_mb(fwd_bwd(hc))
+            rec("peak_memory_full_forward_backward", ours, peak_mb(fwd_bwd(hc_t)), unit="mb")
+
+    def sinkhorn_memory():  # (:203-223)
+        M = torch.randn(batch * seq, 4, 4, device=dev, dtype=half, requires_grad=True)
+
+        def sk_bwd(fn):
+            def run():
+                M_in = M.detach().requires_grad_(True)
+                fn(M_in, num_iters=20).sum().backward()
+                return M_in.grad
+            return run
+
+        ours = peak_mb(sk_bwd(mhc.sinkhorn_knopp))
+        rec("peak_memory_sinkhorn_backward", ours, peak_mb(sk_bwd(mhc.sinkhorn_knopp_torch)), unit="mb")
+
+    # Memory first, ours before the PyTorch path: the latter's matmuls leave a BLAS workspace
+    # allocated through the caching allocator that later peaks would include.
+    for leg in (sinkhorn_memory, lambda: full_layer("memory"), sinkhorn, stream_mix, add_residual,
+                dynamic_weights, lambda: full_layer("time")):
+        leg()
+        torch.cuda.synchronize()
+        torch.cuda.empty_cache()
     return out
 
 
@@ -345,6 +482,14 @@ def main() -> int:
     _lib.load()  # fails loudly when the HIP library is not built
     if args.ops:
         print(json.dumps({"ops": _ops_leg(), "unit": "us per call", "peak_GBps": HBM_PEAK_GBS,
+                          "device": torch.cuda.get_device_name(0)}), flush=True)
+        return 0
+    if args.readme:
+        print(json.dumps({"readme_table": _readme_leg(),
+                          "config": {"batch": 16, "seq": 2048, "dim": 4096, "dtype": "fp16"},
+                          "method": "benchmarks/benchmark.py: mean wall time of 100 calls after 10 "
+                                    "warm-up (PyTorch full fwd+bwd: 10 after 2), device-synchronised",
+                          "published_hardware": "NVIDIA H100 80GB HBM3 (README.md:185)",
                           "device": torch.cuda.get_device_name(0)}), flush=True)
         return 0
 
