@@ -520,6 +520,194 @@ __global__ __launch_bounds__(kThreads) void dynw_bwd_wide_kernel(const TX* __res
   }
 }
 
+// The wide pass for many bf16 rows (the standalone op at R = tokens), both
+// products on MFMA (v_mfma_f32_32x32x16_bf16; fragment layout above):
+//   grad_x [R, K]  = G [R, 24] phi^T [24, K] + coef [R] x      (bf16 out)
+//   grad_phi [K, 24] = x^T [K, R] G [R, 24]                      (f32, per chunk)
+// with G = grad_raw = rowbuf[r][0:24] and coef = rowbuf[r][24].  A workgroup
+// owns 128 columns (wave w: the 32-column block at 32 w) and a chunk of RC
+// rows, walked in blocks of 32 NB rows.  Per block the x tile (bf16) and the G
+// rows (25 floats each) are staged in LDS with 16-byte loads, the next block's
+// loads being in flight meanwhile; then, per 32-row sub-block,
+//   grad_x: A = G rows from LDS, B = phi^T (registers for the whole kernel);
+//           G and phi are split into bf16 hi + lo and three products summed
+//           (relative error ~2^-16); the epilogue adds coef * x in the MFMA
+//           output layout, writes bf16 to an LDS tile, and the tile leaves as
+//           coalesced 16-byte stores (direct 2-byte stores from the MFMA
+//           layout made the whole call 10% slower);
+//   grad_phi: A = x^T read column-wise from the LDS tile (exact bf16), B = G
+//           split hi + lo; accumulated in the MFMA registers over the chunk.
+// Requires K % 8 == 0 and 16-byte aligned x and grad_x.  Grid (K / 128 column
+// blocks, row chunks); outputs as dynw_bwd_wide_kernel: grad_phi direct
+// with one chunk, else per-chunk partials; workgroup (0, 0) also sums
+// grad_bias and grad_alpha.
+constexpr int kBwdCols = 128;                // columns per workgroup: one 32-column block per wave
+constexpr int kBwdXPitch = kBwdCols + 8;     // bf16 per padded LDS row of the x / grad_x tiles
+constexpr int kBwdGPitch = 28;               // floats per LDS row of the G tile (G, coef, padding)
+
+// NB: 32-row sub-blocks per staged block.  NB = 2 needs 178 VGPRs (2 waves per
+// SIMD against 3) and made the whole call 9% slower, so the launch uses NB = 1.
+template <int NB>
+__global__ __launch_bounds__(kThreads) void dynw_bwd_mfma_kernel(const __bf16* __restrict__ x,
+                                                                 const float* __restrict__ phi,
+                                                                 const float* __restrict__ rowbuf,
+                                                                 __bf16* __restrict__ gx, float* __restrict__ gphi,
+                                                                 float* __restrict__ gphi_part,
+                                                                 float* __restrict__ gbias,
+                                                                 float* __restrict__ galpha, int64_t R, int64_t K,
+                                                                 int64_t RC) {
+  constexpr int TR = 32 * NB;  // rows per staged block
+  __shared__ __attribute__((aligned(16))) __bf16 xs[TR * kBwdXPitch];
+  __shared__ __attribute__((aligned(16))) __bf16 gxs[TR * kBwdXPitch];
+  __shared__ __attribute__((aligned(16))) float gs[TR * kBwdGPitch];
+  if (blockIdx.x == 0 && blockIdx.y == 0 && (gbias || galpha)) {
+    __shared__ float lds[4 * 27];
+    float acc[27];
+#pragma unroll
+    for (int i = 0; i < 27; ++i) acc[i] = 0.f;
+    for (int64_t r = threadIdx.x; r < R; r += kThreads) {
+      const float* rb = rowbuf + r * kRow;
+#pragma unroll
+      for (int i = 0; i < 27; ++i) acc[i] += rb[25 + i];
+    }
+    block_sum<27>(acc, lds);
+    if (threadIdx.x == 0) {
+#pragma unroll
+      for (int j = 0; j < kOut; ++j) if (gbias) gbias[j] = acc[j];
+#pragma unroll
+      for (int g = 0; g < 3; ++g) if (galpha) galpha[g] = acc[24 + g];
+    }
+  }
+  const int wave = threadIdx.x >> 6;
+  const int lane = threadIdx.x & 63;
+  const int64_t k0 = (int64_t)blockIdx.x * kBwdCols;
+  const int64_t r_beg = (int64_t)blockIdx.y * RC;
+  const int64_t r_end = r_beg + RC < R ? r_beg + RC : R;
+  const int col = 32 * wave + (lane & 31);  // this lane's column within the tile
+  // phi^T fragments (B of the grad_x product): lane l, element e -> phi[k0 + col][16 js + 8 (l / 32) + e].
+  bf16x8 bhi[2], blo[2];
+  {
+    const int64_t kk = k0 + col;
+#pragma unroll
+    for (int js = 0; js < 2; ++js) {
+      const int j0 = 16 * js + 8 * (lane >> 5);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const float v = (kk < K && j0 + e < kOut) ? phi[kk * kOut + j0 + e] : 0.f;
+        const __bf16 h = (__bf16)v;
+        bhi[js][e] = h;
+        blo[js][e] = (__bf16)(v - (float)h);
+      }
+    }
+  }
+  // Tile loads: x rows t/16 + 16 i (16 bytes at column 8 (t % 16)); G rows t/8 + 32 i, floats 4 (t % 8)..+3.
+  const int xr = threadIdx.x >> 4;
+  const int xc = (threadIdx.x & 15) * 8;
+  const bool xcol_ok = k0 + xc < K;
+  const int grow = threadIdx.x >> 3;
+  const int gcol = (threadIdx.x & 7) * 4;
+  u32x4 xv[2 * NB];
+  f32x4 gv[NB];
+  auto load_block = [&](int64_t r0) {
+#pragma unroll
+    for (int i = 0; i < 2 * NB; ++i) {
+      const int64_t r = r0 + xr + 16 * i;
+      xv[i] = (r < r_end && xcol_ok) ? *reinterpret_cast<const u32x4*>(x + r * K + k0 + xc)
+                                     : u32x4{0u, 0u, 0u, 0u};
+    }
+#pragma unroll
+    for (int i = 0; i < NB; ++i) {
+      const int64_t r = r0 + grow + 32 * i;
+      gv[i] = (r < r_end && gcol < kBwdGPitch) ? *reinterpret_cast<const f32x4*>(rowbuf + r * kRow + gcol)
+                                               : f32x4{0.f, 0.f, 0.f, 0.f};
+    }
+  };
+  f32x16 zero, dphi;
+#pragma unroll
+  for (int i = 0; i < 16; ++i) zero[i] = 0.f;
+  dphi = zero;
+  if (r_beg < r_end) load_block(r_beg);
+  for (int64_t r0 = r_beg; r0 < r_end; r0 += TR) {
+    // Stage this block.
+#pragma unroll
+    for (int i = 0; i < 2 * NB; ++i) *reinterpret_cast<u32x4*>(&xs[(xr + 16 * i) * kBwdXPitch + xc]) = xv[i];
+#pragma unroll
+    for (int i = 0; i < NB; ++i)
+      if (gcol < kBwdGPitch) *reinterpret_cast<f32x4*>(&gs[(grow + 32 * i) * kBwdGPitch + gcol]) = gv[i];
+    __syncthreads();
+    if (r0 + TR < r_end) load_block(r0 + TR);  // in flight during the compute below
+#pragma unroll
+    for (int sb = 0; sb < NB; ++sb) {
+      const int rs = 32 * sb;  // first row of this 32-row sub-block
+      // grad_x = G phi^T: A = G rows (lane l: row rs + l % 32, j 16 js + 8 (l / 32) + e, 0 past 24).
+      f32x16 d = zero;
+#pragma unroll
+      for (int js = 0; js < 2; ++js) {
+        const int j0 = 16 * js + 8 * (lane >> 5);
+        const f32x4 p0 = *reinterpret_cast<const f32x4*>(&gs[(rs + (lane & 31)) * kBwdGPitch + j0]);
+        const f32x4 p1 = *reinterpret_cast<const f32x4*>(&gs[(rs + (lane & 31)) * kBwdGPitch + j0 + 4]);
+        bf16x8 ahi, alo;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          const float v = j0 + e < kOut ? (e < 4 ? p0[e] : p1[e - 4]) : 0.f;
+          const __bf16 h = (__bf16)v;
+          ahi[e] = h;
+          alo[e] = (__bf16)(v - (float)h);
+        }
+        // smallest products first, the two hi x hi products last
+        d = __builtin_amdgcn_mfma_f32_32x32x16_bf16(alo, bhi[js], d, 0, 0, 0);
+        d = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ahi, blo[js], d, 0, 0, 0);
+        d = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ahi, bhi[js], d, 0, 0, 0);
+      }
+      // Epilogue in the output layout: lane l, element i -> row rs + 8 (i / 4) + 4 (l / 32) + i % 4.
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        const int row = rs + 8 * (i >> 2) + 4 * (lane >> 5) + (i & 3);
+        const float xval = (float)xs[row * kBwdXPitch + col];
+        gxs[row * kBwdXPitch + col] = (__bf16)(d[i] + gs[row * kBwdGPitch + kOut] * xval);
+      }
+      // grad_phi += x^T G over the sub-block's two 16-row steps: A = x^T (lane l: column col,
+      // rows rs + 16 st + 8 (l / 32) + e), B = G (same rows, j = l % 32).
+#pragma unroll
+      for (int st = 0; st < 2; ++st) {
+        const int rb = rs + 16 * st + 8 * (lane >> 5);
+        bf16x8 a2, b2hi, b2lo;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          a2[e] = xs[(rb + e) * kBwdXPitch + col];
+          const float gval = (lane & 31) < kOut ? gs[(rb + e) * kBwdGPitch + (lane & 31)] : 0.f;
+          const __bf16 h = (__bf16)gval;
+          b2hi[e] = h;
+          b2lo[e] = (__bf16)(gval - (float)h);
+        }
+        dphi = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a2, b2lo, dphi, 0, 0, 0);
+        dphi = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a2, b2hi, dphi, 0, 0, 0);
+      }
+    }
+    __syncthreads();
+    // grad_x tile out: rows xr + 16 i, 16 bytes at column xc.
+    if (gx && xcol_ok) {
+#pragma unroll
+      for (int i = 0; i < 2 * NB; ++i) {
+        const int64_t r = r0 + xr + 16 * i;
+        if (r < r_end)
+          *reinterpret_cast<u32x4*>(gx + r * K + k0 + xc) =
+              *reinterpret_cast<const u32x4*>(&gxs[(xr + 16 * i) * kBwdXPitch + xc]);
+      }
+    }
+    __syncthreads();  // the tiles are rewritten by the next block
+  }
+  // grad_phi: lane l, element i -> k = k0 + 32 wave + 8 (i / 4) + 4 (l / 32) + i % 4, j = l % 32.
+  const int j = lane & 31;
+  float* o = gphi_part ? gphi_part + (int64_t)blockIdx.y * K * kOut : gphi;
+  if (j >= kOut || !o) return;
+#pragma unroll
+  for (int i = 0; i < 16; ++i) {
+    const int64_t kk = k0 + 32 * wave + 8 * (i >> 2) + 4 * (lane >> 5) + (i & 3);
+    if (kk < K) o[kk * kOut + j] = dphi[i];
+  }
+}
+
 // grad_phi[i] = sum over row chunks c (in order) of gphi_part[c][i], i < K * 24.
 template <int = 0>
 __global__ __launch_bounds__(kThreads) void dynw_gphi_reduce_kernel(const float* __restrict__ part,

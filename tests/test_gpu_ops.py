@@ -206,6 +206,10 @@ def test_dynamic_weights_forward_backward(R, K, xdtype):
     gx, gphi, gbias, ga = O.dynamic_weights_backward(*args, to_np(gp), to_np(gq), to_np(gr), 20, 1e-6)
     assert leaves[0].grad.dtype == xdtype
     assert rel_err(to_np(leaves[0].grad), gx) < GTOL[xdtype]
+    if xdtype == torch.bfloat16:
+        # grad_x is formed in fp32 (on MFMA from split bf16 operands for R >= 64) and rounded
+        # once to bf16: within half a bf16 ulp, 2^-9, of the largest element.
+        assert rel_err(to_np(leaves[0].grad), gx) < 4e-3
     assert rel_err(to_np(leaves[1].grad), gphi) < 1e-4
     assert rel_err(to_np(leaves[2].grad), gbias) < 1e-4
     assert rel_err(np.array([a.grad.item() for a in leaves[3:]]), np.array(ga)) < 1e-4
