@@ -93,70 +93,72 @@ template <typename T, typename TB, int W, int U, bool BI, bool RES, bool ADD_BO,
 __global__ __launch_bounds__(kThreads) void mix_fwd_kernel(const T* __restrict__ H, const TB* __restrict__ bo,
                                                            WRow pre, WRow res, WRow post, T* __restrict__ bi,
                                                            T* __restrict__ out, Geom g) {
+  // One workgroup per tile: grid.x == g.ntiles.
   const int64_t b = g.b0 + blockIdx.y;
+  const int64_t D = g.D;
+  const uint32_t tile = blockIdx.x;
+  // Spans start at the tile's first token.
+  const int64_t s_lo = (int64_t)(tile * (kThreads * U)) / g.nch;
+  const int64_t t0 = b * g.S + s_lo;
+  const int64_t rest = g.S - s_lo;
+  const Span<T, BUF> hs(H + t0 * 4 * D, rest * 4 * D);
+  Frag<T, W> hf[U][4];
+  Frag<TB, W> bf[U];
+  uint32_t e4[U], e1[U];  // element offsets in the [.,4,D] and [.,D] spans
+  bool ok[U];
+#pragma unroll
+  for (int u = 0; u < U; ++u) {
+    const uint32_t i = tile * (kThreads * U) + u * kThreads + threadIdx.x;
+    ok[u] = i < g.items;
+    const uint32_t s = ok[u] ? i / g.nch : (uint32_t)s_lo;
+    const uint32_t c = ok[u] ? i - s * g.nch : 0;
+    const uint32_t ds = s - (uint32_t)s_lo;
+    e4[u] = ds * 4 * (uint32_t)D + c * W;
+    e1[u] = ds * (uint32_t)D + c * W;
+    if (ok[u]) {
+#pragma unroll
+      for (int n = 0; n < 4; ++n) hf[u][n].template load<(NT & 1) != 0>(hs, e4[u] + n * (uint32_t)D);
+      if constexpr (ADD_BO) {
+        const Span<TB, BUF> bs(bo + t0 * D, rest * D);
+        bf[u].template load<(NT & 1) != 0>(bs, e1[u]);
+      }
+    }
+  }
+  loads_issued();
+  // The weights are fetched behind the tile's loads: waiting for them first
+  // cost the closure forward 2.5% (195 -> 190 us at config-3 size).
   float wp[4], wr[16], wq[4];
   if constexpr (BI) load_w4(pre, b, wp);
   if constexpr (RES) load_w16(res, b, wr);
   if constexpr (ADD_BO) load_w4(post, b, wq);
-  const int64_t D = g.D;
-  for (uint32_t tile = blockIdx.x; tile < g.ntiles; tile += gridDim.x) {
-    // Spans start at the tile's first token.
-    const int64_t s_lo = (int64_t)(tile * (kThreads * U)) / g.nch;
-    const int64_t t0 = b * g.S + s_lo;
-    const int64_t rest = g.S - s_lo;
-    const Span<T, BUF> hs(H + t0 * 4 * D, rest * 4 * D);
-    Frag<T, W> hf[U][4];
-    Frag<TB, W> bf[U];
-    uint32_t e4[U], e1[U];  // element offsets in the [.,4,D] and [.,D] spans
-    bool ok[U];
 #pragma unroll
-    for (int u = 0; u < U; ++u) {
-      const uint32_t i = tile * (kThreads * U) + u * kThreads + threadIdx.x;
-      ok[u] = i < g.items;
-      const uint32_t s = ok[u] ? i / g.nch : (uint32_t)s_lo;
-      const uint32_t c = ok[u] ? i - s * g.nch : 0;
-      const uint32_t ds = s - (uint32_t)s_lo;
-      e4[u] = ds * 4 * (uint32_t)D + c * W;
-      e1[u] = ds * (uint32_t)D + c * W;
-      if (ok[u]) {
+  for (int u = 0; u < U; ++u) {
+    if (!ok[u]) continue;
+    float h[4][W], bv[W];
 #pragma unroll
-        for (int n = 0; n < 4; ++n) hf[u][n].template load<(NT & 1) != 0>(hs, e4[u] + n * (uint32_t)D);
-        if constexpr (ADD_BO) {
-          const Span<TB, BUF> bs(bo + t0 * D, rest * D);
-          bf[u].template load<(NT & 1) != 0>(bs, e1[u]);
-        }
-      }
+    for (int n = 0; n < 4; ++n) hf[u][n].unpack(h[n]);
+    if constexpr (ADD_BO) bf[u].unpack(bv);
+    if constexpr (BI) {
+      float r[W];
+#pragma unroll
+      for (int e = 0; e < W; ++e)
+        r[e] = wp[0] * h[0][e] + wp[1] * h[1][e] + wp[2] * h[2][e] + wp[3] * h[3][e];
+      const Span<T, BUF> bis(bi + t0 * D, rest * D);
+      st<T, W, (NT & 2) != 0>(bis, e1[u], r);
     }
-    loads_issued();
+    if constexpr (RES) {
+      const Span<T, BUF> os(out + t0 * 4 * D, rest * 4 * D);
 #pragma unroll
-    for (int u = 0; u < U; ++u) {
-      if (!ok[u]) continue;
-      float h[4][W], bv[W];
-#pragma unroll
-      for (int n = 0; n < 4; ++n) hf[u][n].unpack(h[n]);
-      if constexpr (ADD_BO) bf[u].unpack(bv);
-      if constexpr (BI) {
+      for (int n = 0; n < 4; ++n) {
         float r[W];
 #pragma unroll
-        for (int e = 0; e < W; ++e)
-          r[e] = wp[0] * h[0][e] + wp[1] * h[1][e] + wp[2] * h[2][e] + wp[3] * h[3][e];
-        const Span<T, BUF> bis(bi + t0 * D, rest * D);
-        st<T, W, (NT & 2) != 0>(bis, e1[u], r);
-      }
-      if constexpr (RES) {
-        const Span<T, BUF> os(out + t0 * 4 * D, rest * 4 * D);
-#pragma unroll
-        for (int n = 0; n < 4; ++n) {
-          float r[W];
-#pragma unroll
-          for (int e = 0; e < W; ++e) {
-            float v = wr[4 * n] * h[0][e] + wr[4 * n + 1] * h[1][e] + wr[4 * n + 2] * h[2][e] +
-                      wr[4 * n + 3] * h[3][e];
-            if constexpr (ADD_BO) v += wq[n] * bv[e];
-            r[e] = v;
-          }
-          st<T, W, (NT & 2) != 0>(os, e4[u] + n * (uint32_t)D, r);
+        for (int e = 0; e < W; ++e) {
+          float v = wr[4 * n] * h[0][e] + wr[4 * n + 1] * h[1][e] + wr[4 * n + 2] * h[2][e] +
+                    wr[4 * n + 3] * h[3][e];
+          if constexpr (ADD_BO) v += wq[n] * bv[e];
+          r[e] = v;
         }
+        st<T, W, (NT & 2) != 0>(os, e4[u] + n * (uint32_t)D, r);
       }
     }
   }
@@ -170,50 +172,50 @@ template <typename T, typename TB, int W, int U, int NT = 0, bool BUF = (W > 1)>
 __global__ __launch_bounds__(kThreads) void add_residual_fwd_kernel(const T* __restrict__ hr,
                                                                     const TB* __restrict__ bo, WRow post,
                                                                     T* __restrict__ out, Geom g) {
+  // One workgroup per tile (grid.x == g.ntiles); the weights are fetched behind the tile's loads.
   const int64_t b = g.b0 + blockIdx.y;
+  const int64_t D = g.D;
+  const uint32_t tile = blockIdx.x;
+  const int64_t s_lo = (int64_t)(tile * (kThreads * U)) / g.nch;
+  const int64_t t0 = b * g.S + s_lo;
+  const int64_t rest = g.S - s_lo;
+  const Span<T, BUF> hs(hr + t0 * 4 * D, rest * 4 * D);
+  const Span<TB, BUF> bs(bo + t0 * D, rest * D);
+  Frag<T, W> hf[U][4];
+  Frag<TB, W> bf[U];
+  uint32_t e4[U];
+  bool ok[U];
+#pragma unroll
+  for (int u = 0; u < U; ++u) {
+    const uint32_t i = tile * (kThreads * U) + u * kThreads + threadIdx.x;
+    ok[u] = i < g.items;
+    const uint32_t s = ok[u] ? i / g.nch : (uint32_t)s_lo;
+    const uint32_t c = ok[u] ? i - s * g.nch : 0;
+    const uint32_t ds = s - (uint32_t)s_lo;
+    e4[u] = ds * 4 * (uint32_t)D + c * W;
+    if (ok[u]) {
+#pragma unroll
+      for (int n = 0; n < 4; ++n) hf[u][n].template load<(NT & 1) != 0>(hs, e4[u] + n * (uint32_t)D);
+      bf[u].template load<(NT & 1) != 0>(bs, ds * (uint32_t)D + c * W);
+    }
+  }
+  loads_issued();
   float wq[4];
   load_w4(post, b, wq);
-  const int64_t D = g.D;
-  for (uint32_t tile = blockIdx.x; tile < g.ntiles; tile += gridDim.x) {
-    const int64_t s_lo = (int64_t)(tile * (kThreads * U)) / g.nch;
-    const int64_t t0 = b * g.S + s_lo;
-    const int64_t rest = g.S - s_lo;
-    const Span<T, BUF> hs(hr + t0 * 4 * D, rest * 4 * D);
-    const Span<TB, BUF> bs(bo + t0 * D, rest * D);
-    Frag<T, W> hf[U][4];
-    Frag<TB, W> bf[U];
-    uint32_t e4[U];
-    bool ok[U];
+  const Span<T, BUF> os(out + t0 * 4 * D, rest * 4 * D);
 #pragma unroll
-    for (int u = 0; u < U; ++u) {
-      const uint32_t i = tile * (kThreads * U) + u * kThreads + threadIdx.x;
-      ok[u] = i < g.items;
-      const uint32_t s = ok[u] ? i / g.nch : (uint32_t)s_lo;
-      const uint32_t c = ok[u] ? i - s * g.nch : 0;
-      const uint32_t ds = s - (uint32_t)s_lo;
-      e4[u] = ds * 4 * (uint32_t)D + c * W;
-      if (ok[u]) {
+  for (int u = 0; u < U; ++u) {
+    if (!ok[u]) continue;
+    float h[4][W], bv[W];
 #pragma unroll
-        for (int n = 0; n < 4; ++n) hf[u][n].template load<(NT & 1) != 0>(hs, e4[u] + n * (uint32_t)D);
-        bf[u].template load<(NT & 1) != 0>(bs, ds * (uint32_t)D + c * W);
-      }
-    }
-    loads_issued();
-    const Span<T, BUF> os(out + t0 * 4 * D, rest * 4 * D);
+    for (int n = 0; n < 4; ++n) hf[u][n].unpack(h[n]);
+    bf[u].unpack(bv);
 #pragma unroll
-    for (int u = 0; u < U; ++u) {
-      if (!ok[u]) continue;
-      float h[4][W], bv[W];
+    for (int n = 0; n < 4; ++n) {
+      float r[W];
 #pragma unroll
-      for (int n = 0; n < 4; ++n) hf[u][n].unpack(h[n]);
-      bf[u].unpack(bv);
-#pragma unroll
-      for (int n = 0; n < 4; ++n) {
-        float r[W];
-#pragma unroll
-        for (int e = 0; e < W; ++e) r[e] = h[n][e] + wq[n] * bv[e];
-        st<T, W, (NT & 2) != 0>(os, e4[u] + n * (uint32_t)D, r);
-      }
+      for (int e = 0; e < W; ++e) r[e] = h[n][e] + wq[n] * bv[e];
+      st<T, W, (NT & 2) != 0>(os, e4[u] + n * (uint32_t)D, r);
     }
   }
 }
