@@ -15,7 +15,7 @@ import torch.nn as nn
 
 from . import _layer, _library
 from ._kernels import mean_pool
-from .ops import sinkhorn_knopp
+from .ops import fused_dynamic_weights, sinkhorn_knopp
 
 
 class HyperConnection(nn.Module):
@@ -117,6 +117,35 @@ class HyperConnection(nn.Module):
         else:
             H_res = sinkhorn_knopp(M, self.sinkhorn_iters)
         return torch.cat([H_pre, H_post, H_res.reshape(B, n * n)], dim=1)
+
+    def _compute_weights(self, H: torch.Tensor) -> Tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
+        """(H_post [B,4], H_pre [B,4], H_res [B,4,4]), fp32 and differentiable, in the order
+        of the reference's ``_compute_weights`` (reference src/mhc/module.py:103-163).
+
+        ``forward`` does not call this: the layer kernels derive the same weights inside
+        the fused path.  It serves callers that inspect or log the mixing weights, on the
+        same HIP ops (mean-pool, ``fused_dynamic_weights``, ``sinkhorn_knopp``).  The
+        mean-pool is taken in fp32, as in ``forward``.
+        """
+        self._check_input(H)
+        B = H.shape[0]
+        n = self.num_streams
+        traced = torch.compiler.is_compiling()
+        if not self.dynamic:
+            H_post = torch.sigmoid(self.H_post_base).unsqueeze(0).expand(B, -1)
+            sg = torch.sigmoid(self.H_pre_base)
+            H_pre = (sg / (sg.sum() + 1e-8)).unsqueeze(0).expand(B, -1)
+            H_res = sinkhorn_knopp(self.H_res_base.unsqueeze(0).expand(B, -1, -1).contiguous(),
+                                   self.sinkhorn_iters)
+            return H_post.contiguous(), H_pre.contiguous(), H_res.contiguous()
+        if self.use_fused_weights:
+            x = torch.ops.mhc.mean_pool(H) if traced else _MeanPool.apply(H)
+            bias = torch.cat([self.H_pre_base, self.H_post_base, self.H_res_base.flatten()])
+            H_pre, H_post, H_res = fused_dynamic_weights(x, self.phi, bias, self.alpha_pre, self.alpha_post,
+                                                         self.alpha_res, self.sinkhorn_iters, self.eps)
+            return H_post, H_pre, H_res
+        w = self._unfused_weights(H, traced=traced)
+        return w[:, 4:8].contiguous(), w[:, 0:4].contiguous(), w[:, 8:].reshape(B, n, n).contiguous()
 
     def forward(self, H: torch.Tensor) -> Tuple[torch.Tensor, Callable[[torch.Tensor], torch.Tensor]]:
         """H (batch, seq, 4, dim) -> (branch_input (batch, seq, dim), add_residual)."""

@@ -113,6 +113,27 @@ def test_ragged_dim_bf16():
     check_layer(hc, H, bo, dHn, dbi, 2e-2, 2e-2, 1e-3)
 
 
+@pytest.mark.parametrize("dynamic,fused", [(True, True), (False, True), (True, False)])
+def test_compute_weights_matches_oracle_and_layer(dynamic, fused):
+    """_compute_weights returns the oracle layer's (H_post, H_pre, H_res); the layer mixes
+    with the same H_pre; gradients reach every parameter."""
+    hc, H, bo, _, _ = make_case(2, 16, 64, torch.float32, dynamic=dynamic, fused=fused, phi_std=0.05,
+                                res_std=0.5, layer_idx=1)
+    H_post, H_pre, H_res = hc._compute_weights(H)
+    _, _, cache = O.layer_forward(params_np(hc), to_np(H), to_np(bo), dynamic, fused or not dynamic,
+                                  hc.sinkhorn_iters, hc.eps)
+    assert H_post.shape == (2, 4) and H_pre.shape == (2, 4) and H_res.shape == (2, 4, 4)
+    for got, key in ((H_post, "H_post"), (H_pre, "H_pre"), (H_res, "H_res")):
+        assert got.dtype == torch.float32
+        assert rel_err(to_np(got), np.broadcast_to(cache[key], got.shape)) < 1e-5, key
+    bi, _ = hc(H)
+    bi_ref = (H_pre.detach()[:, None, :, None] * H).sum(dim=2)
+    assert rel_err(to_np(bi), to_np(bi_ref)) < 1e-5
+    (H_post.sum() + H_pre.square().sum() + H_res.square().sum()).backward()
+    for name, p in hc.named_parameters():
+        assert p.grad is not None and torch.isfinite(p.grad).all(), name
+
+
 # --------------------------------------------------------------------------- closure edge cases
 
 def _oracle_grads(hc, H, bo, dHn, dbi):
