@@ -284,6 +284,103 @@ def test_stream_expand_collapse_closed_forms_adjoint_and_autograd():
     assert np.allclose(O.stream_collapse(Y, 0.25), Y.mean(axis=2), rtol=1e-13, atol=1e-15)
 
 
+# --------------------------------------------------------------------------- mean-pool, static and unfused weights
+
+def test_mean_pool_closed_form_and_layout():
+    """H[b,s,n,d] = b + s + 10 n + 100 d: the mean over s is b + (S-1)/2 + 10 n + 100 d, at
+    flat index n*D + d (stream-major), which pins mean (not sum) and the flatten order."""
+    B, S, D = 2, 7, 3
+    b, s, n, d = np.meshgrid(np.arange(B), np.arange(S), np.arange(4), np.arange(D), indexing="ij")
+    H = (b + s + 10 * n + 100 * d).astype(np.float64)
+    x = O.mean_pool(H)
+    assert x.shape == (B, 4 * D)
+    for bb in range(B):
+        for nn_ in range(4):
+            for dd in range(D):
+                assert x[bb, nn_ * D + dd] == bb + (S - 1) / 2 + 10 * nn_ + 100 * dd
+
+
+def _sig(z):
+    return 1.0 / (1.0 + np.exp(-z))
+
+
+@pytest.mark.parametrize("layer_idx", [0, 3])
+def test_static_weights_default_init_known_answer(layer_idx):
+    """Default parameters (H_post_base = 1, H_pre_base = onehot, H_res_base = I): H_post is
+    sigmoid(1) = 0.7310585786300049 with no factor 2, H_pre puts sigmoid(1) / (sigmoid(1) + 1.5 +
+    1e-8) on the layer's stream and 0.5 / (...) elsewhere, and H_res is the Sinkhorn of I + 1e-8,
+    which is I to 1e-8."""
+    pre = np.zeros(4)
+    pre[layer_idx % 4] = 1.0
+    H_post, H_pre, H_res = O.static_weights(pre, np.ones(4), np.eye(4), B=3)
+    assert H_post.shape == (3, 4) and H_pre.shape == (3, 4) and H_res.shape == (3, 4, 4)
+    assert np.all(H_post == _sig(1.0)) and abs(_sig(1.0) - 0.7310585786300049) < 1e-16
+    den = _sig(1.0) + 1.5 + 1e-8
+    want = np.full(4, 0.5 / den)
+    want[layer_idx % 4] = _sig(1.0) / den
+    assert np.allclose(H_pre, want, rtol=1e-15, atol=0)
+    assert np.abs(H_res - np.eye(4)).max() < 5e-8
+
+
+def test_unfused_weights_with_zero_linears_equal_static():
+    """With W_pre = W_post = W_res = 0 the unfused path cannot see x, and must equal the
+    static path on the same bases (sigmoid H_post without x2, 1e-8 in the H_pre normalisation
+    and in the Sinkhorn); a nonzero W_res must then move H_res."""
+    B, K = 3, 8
+    x = RNG.standard_normal((B, K))
+    bq, bp, br = RNG.standard_normal(4), RNG.standard_normal(4), RNG.standard_normal((4, 4))
+    Wq, Wp, Wr = np.zeros((4, K)), np.zeros((4, K)), np.zeros((16, K))
+    got = O.unfused_weights(x, Wq, Wp, Wr, 0.3, 0.2, 0.1, bq, bp, br)
+    want = O.static_weights(bq, bp, br, B)
+    for g_, w_ in zip(got, want):
+        assert np.allclose(g_, w_, rtol=1e-13, atol=1e-15)
+    moved = O.unfused_weights(x, Wq, Wp, RNG.standard_normal((16, K)), 0.3, 0.2, 0.1, bq, bp, br)
+    assert np.abs(moved[2] - want[2]).max() > 1e-3
+
+
+def test_static_weights_backward_finite_differences():
+    bq, bp, br = RNG.standard_normal(4), RNG.standard_normal(4), RNG.standard_normal((4, 4))
+    B = 2
+    gp, gq, gr = RNG.standard_normal((B, 4)), RNG.standard_normal((B, 4)), RNG.standard_normal((B, 4, 4))
+
+    def loss(q, p_, r):
+        Hp, Hq, Hr = O.static_weights(q, p_, r, B, iters=5)
+        return float((Hp * gp).sum() + (Hq * gq).sum() + (Hr * gr).sum())
+
+    g_q, g_p, g_r = O.static_weights_backward(bq, bp, br, gp, gq, gr, iters=5)
+    assert rel_err(g_q, _fd(lambda v: loss(v, bp, br), bq.copy())) < 1e-6
+    assert rel_err(g_p, _fd(lambda v: loss(bq, v, br), bp.copy())) < 1e-6
+    assert rel_err(g_r, _fd(lambda v: loss(bq, bp, v), br.copy())) < 1e-6
+
+
+def test_unfused_weights_backward_finite_differences():
+    B, K = 2, 6
+    x = RNG.standard_normal((B, K))
+    args = {
+        "W_pre": 0.3 * RNG.standard_normal((4, K)), "W_post": 0.3 * RNG.standard_normal((4, K)),
+        "W_res": 0.3 * RNG.standard_normal((16, K)), "scale_pre": 0.3, "scale_post": 0.2, "scale_res": 0.4,
+        "H_pre_base": RNG.standard_normal(4), "H_post_base": RNG.standard_normal(4),
+        "H_res_base": RNG.standard_normal((4, 4)),
+    }
+    gp, gq, gr = RNG.standard_normal((B, 4)), RNG.standard_normal((B, 4)), RNG.standard_normal((B, 4, 4))
+    order = ["W_pre", "W_post", "W_res", "scale_pre", "scale_post", "scale_res", "H_pre_base", "H_post_base",
+             "H_res_base"]
+
+    def loss(xx, a):
+        Hp, Hq, Hr = O.unfused_weights(xx, *[a[k] for k in order], iters=5, eps=1e-6)
+        return float((Hp * gp).sum() + (Hq * gq).sum() + (Hr * gr).sum())
+
+    g = O.unfused_weights_backward(x, *[args[k] for k in order], gp, gq, gr, iters=5, eps=1e-6)
+    assert rel_err(g["x"], _fd(lambda v: loss(v, args), x.copy())) < 1e-6
+    for k in order:
+        def f(v, k=k):
+            a = dict(args)
+            a[k] = v if np.ndim(args[k]) else float(v)
+            return loss(x, a)
+        want = _fd(f, np.array(args[k], dtype=np.float64).copy())
+        assert rel_err(np.asarray(g[k]).reshape(np.shape(want)), want) < 1e-6, k
+
+
 # --------------------------------------------------------------------------- whole layer
 
 def _layer_params(dynamic, fused, D, rng, zero_phi=False):
