@@ -125,8 +125,12 @@ extern "C" int mhc_dynamic_weights_forward(const void* x, int dtype_x, const flo
     nK = p.nK;
   }
   DynParams P{bias, bias + 4, bias + 8, alpha_pre, alpha_post, alpha_res};
-  dynw_finalize_kernel<><<<dim3((unsigned)((R + 3) / 4)), kThreads, 0, st>>>(
-      part, nK, R, K, P, OutRow{H_pre, 4}, OutRow{H_post, 4}, OutRow{H_res, 16}, aux, iters, eps);
+  if (R >= kMfmaMinRows && nK <= 64)
+    dynw_finalize_rows_kernel<><<<dim3((unsigned)((R + kFinRowsWg - 1) / kFinRowsWg)), kThreads, 0, st>>>(
+        part, nK, R, K, P, OutRow{H_pre, 4}, OutRow{H_post, 4}, OutRow{H_res, 16}, aux, iters, eps);
+  else
+    dynw_finalize_kernel<><<<dim3((unsigned)((R + 3) / 4)), kThreads, 0, st>>>(
+        part, nK, R, K, P, OutRow{H_pre, 4}, OutRow{H_post, 4}, OutRow{H_res, 16}, aux, iters, eps);
   return hip_status(hipGetLastError(), "dynamic_weights_forward finalize launch");
 }
 

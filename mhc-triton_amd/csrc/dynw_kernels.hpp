@@ -7,7 +7,9 @@
 //                         row per k, contiguous across lanes (no transpose).
 //   dynw_finalize_kernel  per row: fixed-order sum of the K-chunk partials,
 //                         inv_rms, scale + bias, sigmoid / normalise, 2*sigmoid
-//                         and the register-resident Sinkhorn of H_res.
+//                         and the register-resident Sinkhorn of H_res
+//                         (dynw_finalize_rows_kernel: the same for many rows
+//                         with few K chunks, one 16-lane group per row).
 // Layer path: colsum_reduce_kernel<PROJ=true> produces the same 25 partials
 // per column chunk while it finishes the sequence mean, so the projection
 // costs no extra pass over HBM.
@@ -288,11 +290,41 @@ __device__ __forceinline__ void dyn_scaled(const DynParams& P, const float (&raw
   for (int j = 0; j < 16; ++j) s[8 + j] = inv_rms * ar * raw[8 + j] + P.bias_res[j];
 }
 
+// Eq. 14-19 epilogue of one row in 16-lane form: lane e owns H_res element e;
+// lanes 0..3 also H_pre[e], lanes 4..7 H_post[e - 4].  raw_res = raw[8 + e],
+// raw_pp = raw[e & 7] and sumsq (the row's sum of x^2) are the row's totals.
+// All 16 lanes of the row must take part (DPP sums); lanes with !store
+// compute and write nothing.
+__device__ __forceinline__ void finalize_row16(int e, int64_t r, float raw_res, float raw_pp, float sumsq,
+                                               int64_t K, const DynParams& P, OutRow o_pre, OutRow o_post,
+                                               OutRow o_res, float* __restrict__ aux, int iters, float eps,
+                                               bool store) {
+  const int j = e & 3;
+  const bool is_pre = e < 4;
+  const float inv_rms = 1.f / sqrtf(sumsq / (float)K + eps);
+  // Eq. 19: H_res = Sinkhorn(|s_res| + eps)
+  const float m = sk16_forward(inv_rms * *P.alpha_res * raw_res + P.bias_res[e], iters, eps);
+  // Eq. 17: H_pre = sigmoid / (sum + eps); Eq. 18: H_post = 2 sigmoid
+  const float s_pp = inv_rms * (is_pre ? *P.alpha_pre : *P.alpha_post) * raw_pp +
+                     (is_pre ? P.bias_pre[j] : P.bias_post[j]);
+  const float sg = sigmoidf(s_pp);
+  const float den = sum_row16(sg) + eps;  // quad 0: the four H_pre sigmoids
+  if (!store) return;
+  o_res.p[r * o_res.stride + e] = m;
+  if (is_pre) o_pre.p[r * o_pre.stride + j] = sg / den;
+  else if (e < 8) o_post.p[r * o_post.stride + j] = 2.f * sg;
+  if (aux) {
+    aux[r * kPart + 8 + e] = raw_res;
+    if (e < 8) aux[r * kPart + e] = raw_pp;
+    if (e == 0) aux[r * kPart + kOut] = inv_rms;
+  }
+}
+
 // One wave per row.  Lane l sums the partial records l, l+64, l+128, ... (25
 // floats each) in chunk order, the wave then adds the 64 lane sums with a
-// fixed butterfly, and lane 0 runs the epilogue.  Keeping 64 independent load
-// streams per row instead of one serial chain matters: R is the batch (4 at
-// dim 4096) and this kernel sits between two full passes over H.
+// fixed butterfly, and lanes 0..15 run the epilogue.  Keeping 64 independent
+// load streams per row instead of one serial chain matters: R is the batch (4
+// at dim 4096) and this kernel sits between two full passes over H.
 template <int = 0>
 __global__ __launch_bounds__(kThreads) void dynw_finalize_kernel(const float* __restrict__ part, int nK, int64_t R,
                                                                  int64_t K, DynParams P, OutRow o_pre,
@@ -318,31 +350,37 @@ __global__ __launch_bounds__(kThreads) void dynw_finalize_kernel(const float* __
     for (int j = 0; j < kPart; ++j) tot[wave][j] = acc[j];
   }
   __syncthreads();
-  // Epilogue on lanes 0..15 in 16-lane form: lane e owns H_res element e;
-  // lanes 0..3 also H_pre[e], lanes 4..7 H_post[e - 4].
   if (!live || lane >= 16) return;
   const float* t = tot[wave];
-  const int e = lane;
-  const int j = e & 3;
-  const bool is_pre = e < 4;
-  const float inv_rms = 1.f / sqrtf(t[kOut] / (float)K + eps);
-  const float raw_res = t[8 + e];
-  const float raw_pp = t[e & 7];
-  // Eq. 19: H_res = Sinkhorn(|s_res| + eps)
-  const float m = sk16_forward(inv_rms * *P.alpha_res * raw_res + P.bias_res[e], iters, eps);
-  o_res.p[r * o_res.stride + e] = m;
-  // Eq. 17: H_pre = sigmoid / (sum + eps); Eq. 18: H_post = 2 sigmoid
-  const float s_pp = inv_rms * (is_pre ? *P.alpha_pre : *P.alpha_post) * raw_pp +
-                     (is_pre ? P.bias_pre[j] : P.bias_post[j]);
-  const float sg = sigmoidf(s_pp);
-  const float den = sum_row16(sg) + eps;  // quad 0: the four H_pre sigmoids
-  if (is_pre) o_pre.p[r * o_pre.stride + j] = sg / den;
-  else if (e < 8) o_post.p[r * o_post.stride + j] = 2.f * sg;
-  if (aux) {
-    aux[r * kPart + e] = t[e];
-    if (e < 8) aux[r * kPart + 16 + e] = t[16 + e];
-    if (e == 0) aux[r * kPart + kOut] = inv_rms;
+  finalize_row16(lane, r, t[8 + lane], t[lane & 7], t[kOut], K, P, o_pre, o_post, o_res, aux, iters, eps, true);
+}
+
+// The same for many rows with few chunks (the MFMA projection at R = tokens:
+// R = 16384, nK = 16): one 16-lane group per row, 16 rows per workgroup.  Lane
+// e sums, in chunk order, only the three record entries its epilogue reads
+// (raw[8 + e], raw[e & 7] and the sum of squares), so no cross-lane reduction
+// is needed.  One wave per row left three quarters of each wave idle in the
+// epilogue and spent 25 butterflies per row (33 us at R = 16384).
+constexpr int kFinRowsWg = 16;
+
+template <int = 0>
+__global__ __launch_bounds__(kThreads) void dynw_finalize_rows_kernel(const float* __restrict__ part, int nK,
+                                                                      int64_t R, int64_t K, DynParams P,
+                                                                      OutRow o_pre, OutRow o_post, OutRow o_res,
+                                                                      float* __restrict__ aux, int iters,
+                                                                      float eps) {
+  const int e = threadIdx.x & 15;
+  const int64_t r_grp = (int64_t)blockIdx.x * kFinRowsWg + (threadIdx.x >> 4);
+  const bool live = r_grp < R;
+  const int64_t r = live ? r_grp : R - 1;  // idle groups redo the last row and store nothing
+  const float* p = part + r * nK * kPart;
+  float raw_res = 0.f, raw_pp = 0.f, sumsq = 0.f;
+  for (int k = 0; k < nK; ++k, p += kPart) {
+    raw_res += p[8 + e];
+    raw_pp += p[e & 7];
+    sumsq += p[kOut];
   }
+  finalize_row16(e, r, raw_res, raw_pp, sumsq, K, P, o_pre, o_post, o_res, aux, iters, eps, live);
 }
 
 // Per-row backward record rowbuf[r][0:52]:
