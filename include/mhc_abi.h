@@ -21,7 +21,9 @@
  *   - Reductions are deterministic: fixed-order trees, no float atomics.
  *
  * Shapes: B batch, S sequence, D dim (per stream), 4 streams, K = 4*D,
- * R rows of the dynamic-weight projection, N 4x4 matrices.
+ * R rows of the dynamic-weight projection, N 4x4 matrices.  Entry points
+ * over the stream tensor require S*D <= 2^32 - 2^16 (per-batch element
+ * indices are 32-bit) and return MHC_ERR_ARG otherwise; B is unbounded.
  */
 #ifndef MHC_ABI_H
 #define MHC_ABI_H

@@ -601,8 +601,10 @@ inline int check_bsd(const char* who, int64_t B, int64_t S, int64_t D) {
     set_error("%s: negative size (B=%lld S=%lld D=%lld)", who, (long long)B, (long long)S, (long long)D);
     return MHC_ERR_ARG;
   }
-  if (S * D >= (int64_t)1 << 32) {
-    set_error("%s: S*D = %lld exceeds the 2^32 per-batch item limit", who, (long long)(S * D));
+  // Per-batch element indices are 32-bit, and a tile's first index (a multiple
+  // of 256 items of up to 2 elements each) must stay below 2^32 as well.
+  if (S * D > ((int64_t)1 << 32) - ((int64_t)1 << 16)) {
+    set_error("%s: S*D = %lld exceeds the per-batch limit of 2^32 - 2^16 elements", who, (long long)(S * D));
     return MHC_ERR_ARG;
   }
   return MHC_OK;

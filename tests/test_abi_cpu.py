@@ -83,6 +83,9 @@ def test_host_side_validation_without_gpu(lib):
     assert lib.mhc_stream_mix_backward(16, 16, 16, 16, 16, 16, 16, 16, 2, 3, 4, 0, None, 0, None) == 3
     assert b"workspace" in lib.mhc_last_error()
     assert lib.mhc_stream_mix_forward(16, 16, 16, 16, 16, 1, 1 << 20, 1 << 13, 0, None) == 1  # S*D >= 2^32
+    # just under 2^32: the last tile's first index would wrap a 32-bit counter
+    assert lib.mhc_stream_mix_forward(16, 16, 16, 16, 16, 1, (1 << 32) - 1, 1, 0, None) == 1
+    assert b"2^32 - 2^16" in lib.mhc_last_error()
     assert lib.mhc_layer_dynamic_forward(None, 0, *([None] * 11), 1, 1, 1, -1, 1e-6, None, 0, None) == 1
 
 
