@@ -4,7 +4,6 @@ on arity, and host-side argument validation returns the documented status
 codes before any device work.
 """
 
-import ctypes
 import os
 import re
 
