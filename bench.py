@@ -456,7 +456,21 @@ def _cpu_leg(cfg, target_s):
         "sample": (f"torch CPU fp32 restatement of the reference's pure-PyTorch layer fwd+bwd, "
                    f"B={B} S={S} D={D} ({'dynamic' if cfg['dynamic'] else 'static'}), "
                    f"{reps} reps in {el:.1f} s"),
+        "host_cpus": os.cpu_count(),
+        "host_cpu_model": _cpu_model(),
     }
+
+
+def _cpu_model() -> str | None:
+    """The host CPU's model name from /proc/cpuinfo (None where that file is absent)."""
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return None
 
 
 def main() -> int:

@@ -67,3 +67,19 @@ def test_stash_sums_repeated_closure_gradients():
     dh, dp = s.take()
     assert torch.equal(dh, torch.full((2, 3), 4.0)) and torch.equal(dp, torch.full((2, 4), 12.0))
     assert s.take() == (None, None)
+
+
+def test_bench_cpu_baseline_fields():
+    """bench.py's cpu_baseline leg (the reference's torch layer restated, on the host cores) reports
+    the contract's fields plus the host it ran on, on a short sample."""
+    import importlib.util
+    import os
+
+    path = os.path.join(os.path.dirname(os.path.dirname(os.path.abspath(__file__))), "bench.py")
+    spec = importlib.util.spec_from_file_location("mhc_bench", path)
+    bench = importlib.util.module_from_spec(spec)
+    spec.loader.exec_module(bench)
+    r = bench._cpu_leg(dict(bench.WORKLOADS["config5"]), 0.2)
+    assert set(r) >= {"value", "unit", "cores", "kind", "sample", "host_cpus", "host_cpu_model"}
+    assert r["value"] > 0 and r["unit"] == "tokens/s" and r["kind"] == "port"
+    assert r["cores"] == torch.get_num_threads() and r["host_cpus"] == os.cpu_count()
