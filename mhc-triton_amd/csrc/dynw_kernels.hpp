@@ -141,83 +141,79 @@ __global__ __launch_bounds__(kThreads) void dynw_pack_phi_kernel(const float* __
 }
 
 // One workgroup per 128-row tile and K chunk (wave w owns rows 32w..32w+31).
-// x is staged through LDS so that global loads are whole 128-byte row
-// segments: per 64-k slab, thread t loads 16 bytes of rows t/8 + 32i
-// (i = 0..3) at k offset 8 (t % 8) -- every 8 lanes read one full line -- two
-// slabs ahead of the one the MFMAs consume (two LDS buffers plus registers):
-// with one slab in flight per workgroup the load path, not the MFMAs, set the
-// pace (3.3 TB/s).  A fragments are then
-// read from LDS rows padded to 144 bytes.  Each 16-k step's three MFMAs start
-// from zero and the step result is added into `acc` with fp32 VALU adds (a
-// long MFMA accumulation chain drifts by ~1e-5 relative over 1024 steps; the
+// Each wave loads its A fragments straight from global memory (lane l: row
+// l % 32, the 16 bytes at k = 16 s + 8 (l / 32)), a group of kMfmaGrpSteps
+// steps ahead of the MFMAs.  The phi fragments of a group are the same for
+// all four waves, so the workgroup stages them once in double-buffered LDS
+// (one barrier per group) instead of every wave loading them from L2: the
+// per-wave phi loads competing with the x stream had cost ~45 us of 175 at
+// R = K = 16384 (149 us this way).  Each 16-k step's three MFMAs start from
+// zero and the step result is added into `acc` with fp32 VALU adds (a long
+// MFMA accumulation chain drifts by ~1e-5 relative over 1024 steps; the
 // round-to-nearest adds do not).  Writes the same 25-float partial records as
 // dynw_partial_kernel: part[r][kc][0:24] and the row's sum of squares [24],
-// which the VALU forms from the A fragments alongside the MFMAs.
+// which the VALU forms from the A fragments alongside the MFMAs.  Requires
+// K % 16 == 0 and a 16-byte aligned x.
 constexpr int kMfmaRowsWg = 128;
-constexpr int kMfmaSlabK = 64;
-constexpr int kMfmaLdsRow = kMfmaSlabK + 8;  // bf16 per padded LDS row (144 bytes)
+constexpr int kMfmaGrpSteps = 4;                             // 16-k steps per group
+constexpr int kMfmaPhiGrp = kMfmaGrpSteps * 3 * 64;          // 16-byte phi chunks per group
+constexpr int kMfmaPhiPerThread = kMfmaPhiGrp / kThreads;    // 3
+static_assert(kMfmaPhiGrp % kThreads == 0, "phi chunks split evenly over the workgroup");
 
 template <int = 0>
 __global__ __launch_bounds__(kThreads) void dynw_mfma_kernel(const __bf16* __restrict__ x,
                                                              const u32x4* __restrict__ packed,
                                                              float* __restrict__ part, int64_t R, int64_t K, int nK,
                                                              int64_t steps_per_chunk) {
-  __shared__ __attribute__((aligned(16))) __bf16 tile[2][kMfmaRowsWg * kMfmaLdsRow];
+  constexpr int G = kMfmaGrpSteps;
+  __shared__ __attribute__((aligned(16))) u32x4 phs[2][kMfmaPhiGrp];
   const int wave = threadIdx.x >> 6;
   const int lane = threadIdx.x & 63;
-  const int64_t row0 = (int64_t)blockIdx.x * kMfmaRowsWg;
+  const int64_t rb0 = (int64_t)blockIdx.x * kMfmaRowsWg + wave * 32;
   const int kc = blockIdx.y;
   const int64_t nsteps = K / 16;
   const int64_t s_beg = (int64_t)kc * steps_per_chunk;
   const int64_t s_end = s_beg + steps_per_chunk < nsteps ? s_beg + steps_per_chunk : nsteps;
-  // Global-load role: rows lr + 32 i, 16 bytes at k offset 8 * (t % 8) of the slab.
-  const int lr = threadIdx.x >> 3;
-  const int lk = (threadIdx.x & 7) * 8;
-  const u32x4* gp[4];
-  bool gok[4];
+  const int64_t ngrp = (s_end - s_beg + G - 1) / G;
+  const int64_t row = rb0 + (lane & 31);
+  const bool rok = row < R;
+  // Rows past R read nothing and contribute zeros.
+  const u32x4* ap = reinterpret_cast<const u32x4*>(x + (rok ? row : 0) * K + 8 * (lane >> 5));
+  u32x4 a[2][G];
+  u32x4 pv[kMfmaPhiPerThread];
+  auto aload = [&](int64_t g, u32x4 (&d)[G]) {
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const int64_t r = row0 + lr + 32 * i;
-    gok[i] = r < R;
-    gp[i] = reinterpret_cast<const u32x4*>(x + (gok[i] ? r : 0) * K + lk);
-  }
-  auto gload = [&](int64_t s0, int64_t s1, u32x4 (&v)[4]) {
-    // 16-k steps s0 .. s1-1 of this slab; k offset lk lies in step s0 + lk / 16.
-    // Out-of-range rows / steps read x[0..7] (always valid) and are zeroed.
-    const bool in = s0 + lk / 16 < s1;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const bool ok = gok[i] && in;
-      const u32x4 t = *(ok ? gp[i] + s0 * 2 : reinterpret_cast<const u32x4*>(x));
-      v[i] = ok ? t : u32x4{0u, 0u, 0u, 0u};
+    for (int j = 0; j < G; ++j) {
+      const int64_t s = s_beg + g * G + j;
+      d[j] = (rok && s < s_end) ? ap[s * 2] : u32x4{0u, 0u, 0u, 0u};
     }
   };
-  auto lstore = [&](int buf, const u32x4 (&v)[4]) {
+  // Group g's phi chunks are packed[(s_beg + g G) * 192 + c], c < kMfmaPhiGrp (0 past the end).
+  auto pload = [&](int64_t g) {
+    const int64_t base = (s_beg + g * G) * 3 * 64;
+    const int64_t lim = nsteps * 3 * 64;
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
-      *reinterpret_cast<u32x4*>(&tile[buf][(lr + 32 * i) * kMfmaLdsRow + lk]) = v[i];
+    for (int i = 0; i < kMfmaPhiPerThread; ++i) {
+      const int64_t c = base + threadIdx.x + kThreads * i;
+      pv[i] = c < lim ? packed[c] : u32x4{0u, 0u, 0u, 0u};
+    }
+  };
+  auto pstore = [&](int buf) {
+#pragma unroll
+    for (int i = 0; i < kMfmaPhiPerThread; ++i) phs[buf][threadIdx.x + kThreads * i] = pv[i];
   };
   f32x16 acc, zero;
 #pragma unroll
   for (int i = 0; i < 16; ++i) acc[i] = zero[i] = 0.f;
   float ss = 0.f;
-  const int arow = wave * 32 + (lane & 31);
-  const int akoff = (lane >> 5) * 8;
-  // Two slabs of x are in flight per thread while a third is consumed from
-  // LDS.  The loop is unrolled by two so the register sets va / vb swap roles
-  // without copies (a copy would wait on the load just issued):
-  //   phase 0: slab s in tile[buf], s + 1 in va (issued a phase ago), s + 2 -> vb
-  //   phase 1: slab s + 1 in tile[buf], s + 2 in vb, s + 3 -> va
-  constexpr int kSS = kMfmaSlabK / 16;  // steps per slab
-  auto compute = [&](int64_t s, int bsel) {
+  auto compute = [&](int64_t g, const u32x4 (&d)[G], int buf) {
 #pragma unroll
-    for (int q = 0; q < kSS; ++q) {
-      if (s + q < s_end) {
-        const u32x4 a = *reinterpret_cast<const u32x4*>(&tile[bsel][arow * kMfmaLdsRow + q * 16 + akoff]);
-        const u32x4 b0 = packed[((s + q) * 3 + 0) * 64 + lane];
-        const u32x4 b1 = packed[((s + q) * 3 + 1) * 64 + lane];
-        const u32x4 b2 = packed[((s + q) * 3 + 2) * 64 + lane];
-        const bf16x8 av = __builtin_bit_cast(bf16x8, a);
+    for (int j = 0; j < G; ++j) {
+      if (s_beg + g * G + j < s_end) {
+        const u32x4 b0 = phs[buf][(j * 3 + 0) * 64 + lane];
+        const u32x4 b1 = phs[buf][(j * 3 + 1) * 64 + lane];
+        const u32x4 b2 = phs[buf][(j * 3 + 2) * 64 + lane];
+        const bf16x8 av = __builtin_bit_cast(bf16x8, d[j]);
         // smallest part first: the step sum sees the corrections before the bulk
         f32x16 st = __builtin_amdgcn_mfma_f32_32x32x16_bf16(av, __builtin_bit_cast(bf16x8, b2), zero, 0, 0, 0);
         st = __builtin_amdgcn_mfma_f32_32x32x16_bf16(av, __builtin_bit_cast(bf16x8, b1), st, 0, 0, 0);
@@ -225,46 +221,45 @@ __global__ __launch_bounds__(kThreads) void dynw_mfma_kernel(const __bf16* __res
         acc += st;
 #pragma unroll
         for (int c = 0; c < 4; ++c) {
-          const float lo_ = __uint_as_float(a[c] << 16);
-          const float hi_ = __uint_as_float(a[c] & 0xffff0000u);
+          const float lo_ = __uint_as_float(d[j][c] << 16);
+          const float hi_ = __uint_as_float(d[j][c] & 0xffff0000u);
           ss += lo_ * lo_ + hi_ * hi_;
         }
       }
     }
   };
-  u32x4 va[4], vb[4];
-  int buf = 0;
-  if (s_beg < s_end) {
-    gload(s_beg, s_end, vb);
-    lstore(0, vb);
+  // Group g's A fragments sit in a[g % 2] and its phi in phs[g % 2]; the loop is
+  // unrolled by two so that neither register set is copied.
+  if (ngrp > 0) {
+    aload(0, a[0]);
+    pload(0);
+    pstore(0);
   }
-  if (s_beg + kSS < s_end) gload(s_beg + kSS, s_end, va);
+  if (ngrp > 1) pload(1);
   __syncthreads();
-  for (int64_t s = s_beg; s < s_end; s += 2 * kSS) {
-    if (s + 2 * kSS < s_end) gload(s + 2 * kSS, s_end, vb);
-    compute(s, buf);
-    if (s + kSS < s_end) lstore(buf ^ 1, va);
+  for (int64_t g = 0; g < ngrp; g += 2) {
+    if (g + 1 < ngrp) aload(g + 1, a[1]);
+    compute(g, a[0], 0);
+    if (g + 1 < ngrp) pstore(1);
+    if (g + 2 < ngrp) pload(g + 2);
     __syncthreads();
-    buf ^= 1;
-    if (s + kSS >= s_end) break;  // uniform
-    if (s + 3 * kSS < s_end) gload(s + 3 * kSS, s_end, va);
-    compute(s + kSS, buf);
-    if (s + 2 * kSS < s_end) lstore(buf ^ 1, vb);
+    if (g + 1 >= ngrp) break;  // uniform
+    if (g + 2 < ngrp) aload(g + 2, a[0]);
+    compute(g + 1, a[1], 1);
+    if (g + 2 < ngrp) pstore(0);
+    if (g + 3 < ngrp) pload(g + 3);
     __syncthreads();
-    buf ^= 1;
   }
   const int col = lane & 31;
-  const int64_t wr0 = row0 + wave * 32;
   if (col < kOut) {
 #pragma unroll
     for (int i = 0; i < 16; ++i) {
-      const int64_t r = wr0 + (i >> 2) * 8 + (lane >> 5) * 4 + (i & 3);
+      const int64_t r = rb0 + (i >> 2) * 8 + (lane >> 5) * 4 + (i & 3);
       if (r < R) part[(r * nK + kc) * kPart + col] = acc[i];
     }
   }
   const float sst = ss + __shfl_xor(ss, 32, 64);  // the two k halves of one row
-  const int64_t row = wr0 + (lane & 31);
-  if (lane < 32 && row < R) part[(row * nK + kc) * kPart + kOut] = sst;
+  if (lane < 32 && rok) part[(row * nK + kc) * kPart + kOut] = sst;
 }
 
 struct DynParams {
