@@ -209,9 +209,9 @@ extern "C" int mhc_dynamic_weights_backward(const void* x, int dtype_x, const fl
       (w.nR > 1 && grad_phi) ? (float*)((char*)workspace + align256((size_t)R * kRow * sizeof(float))) : nullptr;
   int rc;
   if (dtype_x == MHC_DTYPE_BF16 && R >= kMfmaMinRows && K % 8 == 0 && aligned16(x) && (!grad_x || aligned16(grad_x))) {
-    // bf16 rows in bulk: grad_x on MFMA, grad_phi on the VALU.
+    // bf16 rows in bulk: grad_x and grad_phi on MFMA.
     const unsigned ncb = (unsigned)((K + kBwdCols - 1) / kBwdCols);
-    dynw_bwd_mfma_kernel<1><<<dim3(ncb, (unsigned)w.nR), kThreads, 0, st>>>(
+    dynw_bwd_mfma_kernel<><<<dim3(ncb, (unsigned)w.nR), kThreads, 0, st>>>(
         (const __bf16*)x, phi, rowbuf, (__bf16*)grad_x, grad_phi, gphi_part, grad_bias, grad_alpha, R, K, w.RC);
     rc = hip_status(hipGetLastError(), "dynamic_weights_backward mfma launch");
   } else {

@@ -559,28 +559,42 @@ __global__ __launch_bounds__(kThreads) void dynw_bwd_wide_kernel(const TX* __res
 //   grad_phi [K, 24] = x^T [K, R] G [R, 24]                      (f32, per chunk)
 // with G = grad_raw = rowbuf[r][0:24] and coef = rowbuf[r][24].  A workgroup
 // owns 128 columns (wave w: the 32-column block at 32 w) and a chunk of RC
-// rows, walked in blocks of 32 NB rows.  Per block the x tile (bf16) and the G
-// rows (25 floats each) are staged in LDS with 16-byte loads, the next block's
-// loads being in flight meanwhile; then, per 32-row sub-block,
-//   grad_x: A = G rows from LDS, B = phi^T (registers for the whole kernel);
-//           G and phi are split into bf16 hi + lo and three products summed
-//           (relative error ~2^-16); the epilogue adds coef * x in the MFMA
-//           output layout, writes bf16 to an LDS tile, and the tile leaves as
-//           coalesced 16-byte stores (direct 2-byte stores from the MFMA
-//           layout made the whole call 10% slower);
-//   grad_phi: A = x^T read column-wise from the LDS tile (exact bf16), B = G
-//           split hi + lo; accumulated in the MFMA registers over the chunk.
-// Requires K % 8 == 0 and 16-byte aligned x and grad_x.  Grid (K / 128 column
-// blocks, row chunks); outputs as dynw_bwd_wide_kernel: grad_phi direct
-// with one chunk, else per-chunk partials; workgroup (0, 0) also sums
-// grad_bias and grad_alpha.
-constexpr int kBwdCols = 128;                // columns per workgroup: one 32-column block per wave
-constexpr int kBwdXPitch = kBwdCols + 8;     // bf16 per padded LDS row of the x / grad_x tiles
-constexpr int kBwdGPitch = 28;               // floats per LDS row of the G tile (G, coef, padding)
+// rows, walked in 32-row blocks.  Per block the x tile (bf16) and the G rows
+// are staged in LDS with 16-byte loads, the next block's loads being in flight
+// meanwhile.  G is split into bf16 hi + lo planes once, as it is staged (fp32
+// products then take hi*hi + hi*lo + lo*hi, relative error ~2^-16):
+//   grad_x: computed transposed, grad_x^T = phi G^T, so that the A operand is
+//           the workgroup's phi fragments (registers for the whole kernel) and
+//           the B operand 16-byte reads of the G planes.  Each lane then holds
+//           one row and four runs of four consecutive columns: the epilogue
+//           adds coef * x with 8-byte LDS reads and writes bf16 to an LDS tile
+//           with 8-byte writes, and the tile leaves as coalesced 16-byte
+//           stores (8-byte stores straight from registers were 30% slower);
+//   grad_phi: A = x^T and B = G from the LDS tiles by transpose reads
+//           (ds_read_b64_tr_b16: within each 16-lane group, lane i receives
+//           element i % 4 of the 8 bytes lane 4 j + i / 4 addresses, j = 0..3),
+//           accumulated in the MFMA registers over the chunk.
+// Against per-wave splits, 2-byte LDS gathers and a column-per-lane epilogue
+// the kernel is 10% faster with bit-identical results.  Requires K % 8 == 0
+// and 16-byte aligned x and grad_x.  Grid (K / 128 column blocks, row chunks);
+// outputs as dynw_bwd_wide_kernel: grad_phi direct with one chunk, else
+// per-chunk partials; workgroup (0, 0) also sums grad_bias and grad_alpha.
+constexpr int kBwdCols = 128;             // columns per workgroup: one 32-column block per wave
+constexpr int kBwdRows = 32;              // rows per staged block
+constexpr int kBwdXPitch = kBwdCols + 8;  // bf16 per padded LDS row of the x / grad_x tiles
+constexpr int kBwdGPitch = 40;            // bf16 per LDS row of the split G planes (columns 24..31 zero)
 
-// NB: 32-row sub-blocks per staged block.  NB = 2 needs 178 VGPRs (2 waves per
-// SIMD against 3) and made the whole call 9% slower, so the launch uses NB = 1.
-template <int NB>
+typedef short s16x4 __attribute__((ext_vector_type(4)));
+typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
+typedef unsigned u32x2 __attribute__((ext_vector_type(2)));
+
+// 64-bit LDS transpose read of 16-bit elements (see above).
+__device__ __forceinline__ u32x2 lds_read_tr16(const __bf16* p) {
+  typedef __attribute__((address_space(3))) s16x4 lds_s16x4;
+  return __builtin_bit_cast(u32x2, __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(p)));
+}
+
+template <int = 0>
 __global__ __launch_bounds__(kThreads) void dynw_bwd_mfma_kernel(const __bf16* __restrict__ x,
                                                                  const float* __restrict__ phi,
                                                                  const float* __restrict__ rowbuf,
@@ -589,10 +603,12 @@ __global__ __launch_bounds__(kThreads) void dynw_bwd_mfma_kernel(const __bf16* _
                                                                  float* __restrict__ gbias,
                                                                  float* __restrict__ galpha, int64_t R, int64_t K,
                                                                  int64_t RC) {
-  constexpr int TR = 32 * NB;  // rows per staged block
+  constexpr int TR = kBwdRows;
   __shared__ __attribute__((aligned(16))) __bf16 xs[TR * kBwdXPitch];
   __shared__ __attribute__((aligned(16))) __bf16 gxs[TR * kBwdXPitch];
-  __shared__ __attribute__((aligned(16))) float gs[TR * kBwdGPitch];
+  __shared__ __attribute__((aligned(16))) __bf16 ghi[TR * kBwdGPitch];
+  __shared__ __attribute__((aligned(16))) __bf16 glo[TR * kBwdGPitch];
+  __shared__ float cf[TR];
   if (blockIdx.x == 0 && blockIdx.y == 0 && (gbias || galpha)) {
     __shared__ float lds[4 * 27];
     float acc[27];
@@ -616,11 +632,10 @@ __global__ __launch_bounds__(kThreads) void dynw_bwd_mfma_kernel(const __bf16* _
   const int64_t k0 = (int64_t)blockIdx.x * kBwdCols;
   const int64_t r_beg = (int64_t)blockIdx.y * RC;
   const int64_t r_end = r_beg + RC < R ? r_beg + RC : R;
-  const int col = 32 * wave + (lane & 31);  // this lane's column within the tile
-  // phi^T fragments (B of the grad_x product): lane l, element e -> phi[k0 + col][16 js + 8 (l / 32) + e].
+  // phi fragments: lane l, element e -> phi[k0 + 32 wave + l % 32][16 js + 8 (l / 32) + e].
   bf16x8 bhi[2], blo[2];
   {
-    const int64_t kk = k0 + col;
+    const int64_t kk = k0 + 32 * wave + (lane & 31);
 #pragma unroll
     for (int js = 0; js < 2; ++js) {
       const int j0 = 16 * js + 8 * (lane >> 5);
@@ -633,95 +648,101 @@ __global__ __launch_bounds__(kThreads) void dynw_bwd_mfma_kernel(const __bf16* _
       }
     }
   }
-  // Tile loads: x rows t/16 + 16 i (16 bytes at column 8 (t % 16)); G rows t/8 + 32 i, floats 4 (t % 8)..+3.
+  // Tile loads: x rows t/16 + 16 i (16 bytes at column 8 (t % 16)); record row t/8, floats 4 (t % 8)..+3.
   const int xr = threadIdx.x >> 4;
   const int xc = (threadIdx.x & 15) * 8;
   const bool xcol_ok = k0 + xc < K;
   const int grow = threadIdx.x >> 3;
   const int gcol = (threadIdx.x & 7) * 4;
-  u32x4 xv[2 * NB];
-  f32x4 gv[NB];
+  u32x4 xv[2];
+  f32x4 gv;
   auto load_block = [&](int64_t r0) {
 #pragma unroll
-    for (int i = 0; i < 2 * NB; ++i) {
+    for (int i = 0; i < 2; ++i) {
       const int64_t r = r0 + xr + 16 * i;
       xv[i] = (r < r_end && xcol_ok) ? *reinterpret_cast<const u32x4*>(x + r * K + k0 + xc)
                                      : u32x4{0u, 0u, 0u, 0u};
     }
-#pragma unroll
-    for (int i = 0; i < NB; ++i) {
-      const int64_t r = r0 + grow + 32 * i;
-      gv[i] = (r < r_end && gcol < kBwdGPitch) ? *reinterpret_cast<const f32x4*>(rowbuf + r * kRow + gcol)
-                                               : f32x4{0.f, 0.f, 0.f, 0.f};
-    }
+    const int64_t r = r0 + grow;
+    gv = (r < r_end && gcol < 28) ? *reinterpret_cast<const f32x4*>(rowbuf + r * kRow + gcol)
+                                  : f32x4{0.f, 0.f, 0.f, 0.f};
   };
+  // Transpose-read addresses: 16-lane group gi = lane / 16 covers columns 16 (gi & 1) .. +15 of
+  // the wave's 32 and rows 8 (gi >> 1) + 0..3 of a 16-row step (+4 for the second read).
+  const int gi = lane >> 4, l16 = lane & 15;
+  const int tr_row = 8 * (gi >> 1) + (l16 >> 2);
+  const int tr_col = 16 * (gi & 1) + 4 * (l16 & 3);
   f32x16 zero, dphi;
 #pragma unroll
   for (int i = 0; i < 16; ++i) zero[i] = 0.f;
   dphi = zero;
   if (r_beg < r_end) load_block(r_beg);
   for (int64_t r0 = r_beg; r0 < r_end; r0 += TR) {
-    // Stage this block.
+    // Stage this block: x as loaded, G split into hi + lo planes, coef apart.
 #pragma unroll
-    for (int i = 0; i < 2 * NB; ++i) *reinterpret_cast<u32x4*>(&xs[(xr + 16 * i) * kBwdXPitch + xc]) = xv[i];
+    for (int i = 0; i < 2; ++i) *reinterpret_cast<u32x4*>(&xs[(xr + 16 * i) * kBwdXPitch + xc]) = xv[i];
+    {
+      bf16x4 h4, l4;
 #pragma unroll
-    for (int i = 0; i < NB; ++i)
-      if (gcol < kBwdGPitch) *reinterpret_cast<f32x4*>(&gs[(grow + 32 * i) * kBwdGPitch + gcol]) = gv[i];
+      for (int e = 0; e < 4; ++e) {
+        const float v = gcol < kOut ? gv[e] : 0.f;
+        const __bf16 h = (__bf16)v;
+        h4[e] = h;
+        l4[e] = (__bf16)(v - (float)h);
+      }
+      *reinterpret_cast<bf16x4*>(&ghi[grow * kBwdGPitch + gcol]) = h4;
+      *reinterpret_cast<bf16x4*>(&glo[grow * kBwdGPitch + gcol]) = l4;
+      if (gcol == kOut) cf[grow] = gv[0];
+    }
     __syncthreads();
     if (r0 + TR < r_end) load_block(r0 + TR);  // in flight during the compute below
+    // grad_x^T = phi G^T (see above); smallest products first, hi x hi last.
+    f32x16 d = zero;
 #pragma unroll
-    for (int sb = 0; sb < NB; ++sb) {
-      const int rs = 32 * sb;  // first row of this 32-row sub-block
-      // grad_x = G phi^T: A = G rows (lane l: row rs + l % 32, j 16 js + 8 (l / 32) + e, 0 past 24).
-      f32x16 d = zero;
+    for (int js = 0; js < 2; ++js) {
+      const int j0 = 16 * js + 8 * (lane >> 5);
+      const bf16x8 ghv = *reinterpret_cast<const bf16x8*>(&ghi[(lane & 31) * kBwdGPitch + j0]);
+      const bf16x8 glv = *reinterpret_cast<const bf16x8*>(&glo[(lane & 31) * kBwdGPitch + j0]);
+      d = __builtin_amdgcn_mfma_f32_32x32x16_bf16(bhi[js], glv, d, 0, 0, 0);
+      d = __builtin_amdgcn_mfma_f32_32x32x16_bf16(blo[js], ghv, d, 0, 0, 0);
+      d = __builtin_amdgcn_mfma_f32_32x32x16_bf16(bhi[js], ghv, d, 0, 0, 0);
+    }
+    // Epilogue: lane l holds row l % 32, columns 32 wave + 8 q + 4 (l / 32) + 0..3 in d[4 q ..].
+    {
+      const int row = lane & 31;
+      const float c = cf[row];
 #pragma unroll
-      for (int js = 0; js < 2; ++js) {
-        const int j0 = 16 * js + 8 * (lane >> 5);
-        const f32x4 p0 = *reinterpret_cast<const f32x4*>(&gs[(rs + (lane & 31)) * kBwdGPitch + j0]);
-        const f32x4 p1 = *reinterpret_cast<const f32x4*>(&gs[(rs + (lane & 31)) * kBwdGPitch + j0 + 4]);
-        bf16x8 ahi, alo;
+      for (int q = 0; q < 4; ++q) {
+        const int cc = 32 * wave + 8 * q + 4 * (lane >> 5);
+        const bf16x4 x4 = *reinterpret_cast<const bf16x4*>(&xs[row * kBwdXPitch + cc]);
+        bf16x4 o4;
 #pragma unroll
-        for (int e = 0; e < 8; ++e) {
-          const float v = j0 + e < kOut ? (e < 4 ? p0[e] : p1[e - 4]) : 0.f;
-          const __bf16 h = (__bf16)v;
-          ahi[e] = h;
-          alo[e] = (__bf16)(v - (float)h);
-        }
-        // smallest products first, the two hi x hi products last
-        d = __builtin_amdgcn_mfma_f32_32x32x16_bf16(alo, bhi[js], d, 0, 0, 0);
-        d = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ahi, blo[js], d, 0, 0, 0);
-        d = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ahi, bhi[js], d, 0, 0, 0);
+        for (int r = 0; r < 4; ++r) o4[r] = (__bf16)(d[4 * q + r] + c * (float)x4[r]);
+        *reinterpret_cast<bf16x4*>(&gxs[row * kBwdXPitch + cc]) = o4;
       }
-      // Epilogue in the output layout: lane l, element i -> row rs + 8 (i / 4) + 4 (l / 32) + i % 4.
+    }
+    // grad_phi += x^T G over the block's two 16-row steps.  A = x^T (lane l: column
+    // 32 wave + l % 32, rows 16 st + 8 (l / 32) + e), B = G (same rows, j = l % 32).
 #pragma unroll
-      for (int i = 0; i < 16; ++i) {
-        const int row = rs + 8 * (i >> 2) + 4 * (lane >> 5) + (i & 3);
-        const float xval = (float)xs[row * kBwdXPitch + col];
-        gxs[row * kBwdXPitch + col] = (__bf16)(d[i] + gs[row * kBwdGPitch + kOut] * xval);
-      }
-      // grad_phi += x^T G over the sub-block's two 16-row steps: A = x^T (lane l: column col,
-      // rows rs + 16 st + 8 (l / 32) + e), B = G (same rows, j = l % 32).
-#pragma unroll
-      for (int st = 0; st < 2; ++st) {
-        const int rb = rs + 16 * st + 8 * (lane >> 5);
-        bf16x8 a2, b2hi, b2lo;
-#pragma unroll
-        for (int e = 0; e < 8; ++e) {
-          a2[e] = xs[(rb + e) * kBwdXPitch + col];
-          const float gval = (lane & 31) < kOut ? gs[(rb + e) * kBwdGPitch + (lane & 31)] : 0.f;
-          const __bf16 h = (__bf16)gval;
-          b2hi[e] = h;
-          b2lo[e] = (__bf16)(gval - (float)h);
-        }
-        dphi = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a2, b2lo, dphi, 0, 0, 0);
-        dphi = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a2, b2hi, dphi, 0, 0, 0);
-      }
+    for (int st = 0; st < 2; ++st) {
+      const int rb = 16 * st + tr_row;
+      const u32x2 x0 = lds_read_tr16(&xs[rb * kBwdXPitch + 32 * wave + tr_col]);
+      const u32x2 x1 = lds_read_tr16(&xs[(rb + 4) * kBwdXPitch + 32 * wave + tr_col]);
+      const u32x2 h0 = lds_read_tr16(&ghi[rb * kBwdGPitch + tr_col]);
+      const u32x2 h1 = lds_read_tr16(&ghi[(rb + 4) * kBwdGPitch + tr_col]);
+      const u32x2 q0 = lds_read_tr16(&glo[rb * kBwdGPitch + tr_col]);
+      const u32x2 q1 = lds_read_tr16(&glo[(rb + 4) * kBwdGPitch + tr_col]);
+      const bf16x8 a2 = __builtin_bit_cast(bf16x8, u32x4{x0[0], x0[1], x1[0], x1[1]});
+      const bf16x8 b2hi = __builtin_bit_cast(bf16x8, u32x4{h0[0], h0[1], h1[0], h1[1]});
+      const bf16x8 b2lo = __builtin_bit_cast(bf16x8, u32x4{q0[0], q0[1], q1[0], q1[1]});
+      dphi = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a2, b2lo, dphi, 0, 0, 0);
+      dphi = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a2, b2hi, dphi, 0, 0, 0);
     }
     __syncthreads();
     // grad_x tile out: rows xr + 16 i, 16 bytes at column xc.
     if (gx && xcol_ok) {
 #pragma unroll
-      for (int i = 0; i < 2 * NB; ++i) {
+      for (int i = 0; i < 2; ++i) {
         const int64_t r = r0 + xr + 16 * i;
         if (r < r_end)
           *reinterpret_cast<u32x4*>(gx + r * K + k0 + xc) =
