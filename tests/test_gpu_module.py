@@ -134,6 +134,29 @@ def test_compute_weights_matches_oracle_and_layer(dynamic, fused):
         assert p.grad is not None and torch.isfinite(p.grad).all(), name
 
 
+def test_non_contiguous_inputs():
+    """H as a transposed view and branch_output as a strided slice: the layer copies what it
+    must and matches the oracle; gradients come back in the inputs' shapes."""
+    hc, H, bo, dHn, dbi = make_case(2, 24, 64, torch.float32, phi_std=0.05)
+    Ht = H.permute(0, 1, 3, 2).contiguous().permute(0, 1, 3, 2)  # same values, [B,S,4,D] view of [B,S,D,4]
+    assert not Ht.is_contiguous()
+    wide = torch.zeros(2, 24, 2 * 64, device=DEV)
+    wide[:, :, ::2] = bo
+    bos = wide[:, :, ::2]
+    assert not bos.is_contiguous()
+    Hl = Ht.detach().requires_grad_(True)
+    bol = bos.detach().requires_grad_(True)
+    bi, add = hc(Hl)
+    Hn = add(bol)
+    torch.autograd.backward([Hn, bi], [dHn, dbi])
+    p = params_np(hc)
+    obi, oHn, cache = O.layer_forward(p, to_np(H), to_np(bo))
+    og = O.layer_backward(p, cache, to_np(dHn), to_np(dbi))
+    assert rel_err(to_np(bi), obi) < 1e-5 and rel_err(to_np(Hn), oHn) < 1e-5
+    assert Hl.grad.shape == Hl.shape and bol.grad.shape == bol.shape
+    assert rel_err(to_np(Hl.grad), og["H"]) < 1e-4 and rel_err(to_np(bol.grad), og["bo"]) < 1e-4
+
+
 # --------------------------------------------------------------------------- closure edge cases
 
 def _oracle_grads(hc, H, bo, dHn, dbi):
