@@ -33,7 +33,7 @@ static size_t al(size_t v) { return (v + 255) & ~(size_t)255; }
 struct LayerWs {
   size_t colpart;    // mean-pool column partials [B][nS][4D]
   size_t pool_part;  // projection partials [B][nrc][25]
-  size_t red_part;   // [B][nblk][20]
+  size_t red_part;   // [B][nblk][20] (pass B) or [B][tiles][4] (closure backward)
   size_t dpre;       // [B][4]
   size_t dres;       // [B][16]
   size_t rowbuf;     // [B][52]
@@ -47,7 +47,11 @@ static LayerWs layer_ws(int64_t B, int64_t S, int64_t D, int dtype) {
   size_t o = 0;
   w.colpart = o;   o += al(mean_pool_colpart_bytes(dtype, B, S, D));
   w.pool_part = o; o += al((size_t)B * (nrc > 0 ? nrc : 1) * kPart * sizeof(float));
-  w.red_part = o;  o += al(partial_bytes(B, 20));
+  {
+    // pass B's [B][nblk][20] and the closure backward's per-tile [B][tiles][4] share the region
+    const size_t pb = partial_bytes(B, 20), ab = add_bwd_partial_bytes(B, S, D);
+    w.red_part = o;  o += al(pb > ab ? pb : ab);
+  }
   w.dpre = o;      o += al((size_t)B * 4 * sizeof(float));
   w.dres = o;      o += al((size_t)B * 16 * sizeof(float));
   w.rowbuf = o;    o += al((size_t)B * kRow * sizeof(float));
@@ -245,8 +249,9 @@ extern "C" int mhc_layer_dynamic_forward(const void* H, int dtype, const float* 
   if (int rc = check_bsd("layer_dynamic_forward", B, S, D)) return rc;
   if (iters < 0) { set_error("layer_dynamic_forward: negative iters"); return MHC_ERR_ARG; }
   if (B == 0) return MHC_OK;
-  if (!H || !phi || !H_pre_base || !H_post_base || !H_res_base || !alpha_pre || !alpha_post || !alpha_res ||
-      !branch_input || !x || !w || !aux) {
+  const bool nz = S * D != 0;  // bulk tensors may be empty (null) when S * D == 0
+  if ((nz && (!H || !branch_input)) || !phi || !H_pre_base || !H_post_base || !H_res_base || !alpha_pre ||
+      !alpha_post || !alpha_res || !x || !w || !aux) {
     set_error("layer_dynamic_forward: null pointer");
     return MHC_ERR_ARG;
   }
@@ -268,7 +273,8 @@ extern "C" int mhc_layer_static_forward(const void* H, int dtype, const float* H
   if (int rc = check_bsd("layer_static_forward", B, S, D)) return rc;
   if (iters < 0) { set_error("layer_static_forward: negative iters"); return MHC_ERR_ARG; }
   if (B == 0) return MHC_OK;
-  if (!H || !H_pre_base || !H_post_base || !H_res_base || !branch_input || !w) {
+  const bool nz = S * D != 0;  // bulk tensors may be empty (null) when S * D == 0
+  if ((nz && (!H || !branch_input)) || !H_pre_base || !H_post_base || !H_res_base || !w) {
     set_error("layer_static_forward: null pointer");
     return MHC_ERR_ARG;
   }
@@ -314,7 +320,8 @@ extern "C" int mhc_layer_add_backward(const void* dH_new, int dtype_h, const voi
   const int dtype = dtype_h;
   if (int rc = check_bsd("layer_add_backward", B, S, D)) return rc;
   if (B == 0) return MHC_OK;
-  if (!dH_new || !branch_output || !w || !d_branch_output || !dH_post) {
+  const bool nz = S * D != 0;  // bulk tensors may be empty (null) when S * D == 0
+  if ((nz && (!dH_new || !branch_output || !d_branch_output)) || !w || !dH_post) {
     set_error("layer_add_backward: null pointer");
     return MHC_ERR_ARG;
   }
@@ -334,8 +341,9 @@ extern "C" int mhc_layer_dynamic_backward(const void* H, int dtype, const void* 
   if (int rc = check_bsd("layer_dynamic_backward", B, S, D)) return rc;
   if (iters < 0) { set_error("layer_dynamic_backward: negative iters"); return MHC_ERR_ARG; }
   if (B == 0) return MHC_OK;
-  if (!H || !d_branch_input || !phi || !H_pre_base || !H_post_base || !H_res_base || !alpha_pre || !alpha_post ||
-      !alpha_res || !x || !w || !aux) {
+  const bool nz = S * D != 0;  // bulk tensors may be empty (null) when S * D == 0
+  if ((nz && (!H || !d_branch_input)) || !phi || !H_pre_base || !H_post_base || !H_res_base || !alpha_pre ||
+      !alpha_post || !alpha_res || !x || !w || !aux) {
     set_error("layer_dynamic_backward: null pointer");
     return MHC_ERR_ARG;
   }
@@ -376,7 +384,8 @@ extern "C" int mhc_layer_static_backward(const void* H, int dtype, const void* d
   if (int rc = check_bsd("layer_static_backward", B, S, D)) return rc;
   if (iters < 0) { set_error("layer_static_backward: negative iters"); return MHC_ERR_ARG; }
   if (B == 0) return MHC_OK;
-  if (!H || !d_branch_input || !H_pre_base || !H_post_base || !H_res_base || !w || !grad_bias) {
+  const bool nz = S * D != 0;  // bulk tensors may be empty (null) when S * D == 0
+  if ((nz && (!H || !d_branch_input)) || !H_pre_base || !H_post_base || !H_res_base || !w || !grad_bias) {
     set_error("layer_static_backward: null pointer");
     return MHC_ERR_ARG;
   }
@@ -419,7 +428,8 @@ extern "C" int mhc_layer_mix_backward(const void* H, int dtype, const void* d_br
                                       mhc_stream_t stream) {
   if (int rc = check_bsd("layer_mix_backward", B, S, D)) return rc;
   if (B == 0) return MHC_OK;
-  if (!H || !d_branch_input || !w || !dH_pre || !dH_res) {
+  const bool nz = S * D != 0;  // bulk tensors may be empty (null) when S * D == 0
+  if ((nz && (!H || !d_branch_input)) || !w || !dH_pre || !dH_res) {
     set_error("layer_mix_backward: null pointer");
     return MHC_ERR_ARG;
   }

@@ -225,15 +225,17 @@ __global__ __launch_bounds__(kThreads) void add_residual_fwd_kernel(const T* __r
 //   d_bo[s,:] = sum_n post[n] dHn[s,n,:]              (written, dtype TB)
 //   part[k]   = sum dHn[s,k,:] * bo[s,:]   k < 4      (reduced -> dH_post)
 // ---------------------------------------------------------------------------
-template <typename T, typename TB, int W, int U, int NT = 0, bool BUF = (W > 1)>
+template <typename T, typename TB, int W, int U, int NT = 0, bool BUF = (W > 1), bool ONE = false>
 __global__ __launch_bounds__(kThreads) void add_residual_bwd_kernel(const T* __restrict__ dhn,
                                                                     const TB* __restrict__ bo, WRow post,
                                                                     TB* __restrict__ dbo, float* __restrict__ part,
                                                                     Geom g) {
+  // ONE: one workgroup per tile (grid.x == g.ntiles), the weights fetched behind the tile's loads;
+  // otherwise workgroups stride over the tiles.
   __shared__ float lds[4 * 4];
   const int64_t b = g.b0 + blockIdx.y;
   float wq[4];
-  load_w4(post, b, wq);
+  if constexpr (!ONE) load_w4(post, b, wq);
   const int64_t D = g.D;
   float acc[4] = {0.f, 0.f, 0.f, 0.f};
   for (uint32_t tile = blockIdx.x; tile < g.ntiles; tile += gridDim.x) {
@@ -262,6 +264,7 @@ __global__ __launch_bounds__(kThreads) void add_residual_bwd_kernel(const T* __r
         ld<TB, W, (NT & 1) != 0>(bs, e1[u], bv[u]);
       }
     }
+    if constexpr (ONE) load_w4(post, b, wq);
 #pragma unroll
     for (int u = 0; u < U; ++u) {
       if (!ok[u]) continue;
@@ -274,6 +277,7 @@ __global__ __launch_bounds__(kThreads) void add_residual_bwd_kernel(const T* __r
       }
       st<TB, W, (NT & 2) != 0>(ds_, e1[u], r);
     }
+    if constexpr (ONE) break;
   }
   block_sum<4>(acc, lds);
   if (threadIdx.x == 0) {
@@ -530,16 +534,25 @@ template <int NV, int SPLIT>
 __global__ __launch_bounds__(kThreads) void reduce_split_kernel(const float* __restrict__ part,
                                                                 float* __restrict__ out0,
                                                                 float* __restrict__ out1, int nblk) {
+  // Records are NV floats (NV % 4 == 0, 16-byte aligned in the workspace) and
+  // are read as 16-byte vectors; each thread sums its records in index order.
+  static_assert(NV % 4 == 0, "records of whole 16-byte vectors");
   __shared__ float lds[4 * NV];
   const int64_t b = blockIdx.x;
-  const float* p = part + b * nblk * NV;
-  float acc[NV];
+  const f32x4* p = reinterpret_cast<const f32x4*>(part + b * nblk * NV);
+  f32x4 a4[NV / 4];
 #pragma unroll
-  for (int i = 0; i < NV; ++i) acc[i] = 0.f;
+  for (int q = 0; q < NV / 4; ++q) a4[q] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll 8
   for (int k = threadIdx.x; k < nblk; k += kThreads) {
 #pragma unroll
-    for (int i = 0; i < NV; ++i) acc[i] += p[(int64_t)k * NV + i];
+    for (int q = 0; q < NV / 4; ++q) a4[q] += p[(int64_t)k * (NV / 4) + q];
   }
+  float acc[NV];
+#pragma unroll
+  for (int q = 0; q < NV / 4; ++q)
+#pragma unroll
+    for (int c = 0; c < 4; ++c) acc[4 * q + c] = a4[q][c];
   block_sum<NV>(acc, lds);
   if (threadIdx.x == 0) {
 #pragma unroll
@@ -583,6 +596,18 @@ inline uint32_t reduce_blocks(uint32_t ntiles, int64_t B) {
 inline size_t partial_bytes(int64_t B, int nv) {
   const int64_t per_b = kRedBlocks / (B > 0 ? B : 1) > 1 ? kRedBlocks / (B > 0 ? B : 1) : 1;
   return (size_t)(B * per_b * nv) * sizeof(float);
+}
+
+// Bytes of the closure backward's partials (add_residual_bwd_kernel, 4 floats
+// per workgroup): on the vector path one workgroup per tile, on the ragged
+// path the reduce_blocks count.  Sized for the narrowest vector width (fp32,
+// 4 elements per lane), because the path is chosen per call from the pointers'
+// alignment.
+inline size_t add_bwd_partial_bytes(int64_t B, int64_t S, int64_t D) {
+  const int64_t tiles = (S * D / 4 + kThreads - 1) / kThreads;
+  const size_t vec = (size_t)(B > 0 ? B : 1) * (size_t)(tiles > 0 ? tiles : 1) * 4 * sizeof(float);
+  const size_t rag = partial_bytes(B, 4);
+  return vec > rag ? vec : rag;
 }
 
 // Launch fn(b0, nb) for consecutive batch chunks that fit grid.y.

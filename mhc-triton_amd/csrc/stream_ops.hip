@@ -51,12 +51,21 @@ static int add_res_fwd(const TH* hr, const TB* bo, const float* post, TH* out, i
 template <typename TH, typename TB, int W>
 static int add_res_bwd(const TH* dhn, const TB* bo, WRow post, TB* dbo, float* dpost, int64_t B, int64_t S,
                        int64_t D, float* part, hipStream_t st) {
+  // Vector path: one workgroup per tile at 4 per CU (the closure backward at
+  // config-3 size: 134 -> 128 us against 512 looping workgroups per batch at
+  // 2 per CU).  Ragged path: a capped count of looping workgroups.
   const Geom g0 = make_geom<W, kU>(S, D, 0);
-  const uint32_t nblk = reduce_blocks(g0.ntiles, B);
+  // At least one workgroup: with no tiles it writes zero partials, so dH_post comes out zero.
+  uint32_t nblk = W > 1 ? g0.ntiles : reduce_blocks(g0.ntiles, B);
+  if (nblk == 0) nblk = 1;
   int rc = for_batch_chunks(B, [&](int64_t b0, int64_t nb) {
     const Geom g = make_geom<W, kU>(S, D, b0);
-    add_residual_bwd_kernel<TH, TB, W, kU, kNt><<<dim3(nblk, nb), kThreads, occupancy_lds(2), st>>>(
-        dhn, bo, post, dbo, part, g);
+    if constexpr (W > 1)
+      add_residual_bwd_kernel<TH, TB, W, kU, kNt, true, true><<<dim3(nblk, nb), kThreads, occupancy_lds(4), st>>>(
+          dhn, bo, post, dbo, part, g);
+    else
+      add_residual_bwd_kernel<TH, TB, W, kU, kNt><<<dim3(nblk, nb), kThreads, occupancy_lds(2), st>>>(
+          dhn, bo, post, dbo, part, g);
     return hip_status(hipGetLastError(), "add_residual_backward launch");
   });
   if (rc) return rc;
@@ -180,8 +189,8 @@ extern "C" int mhc_add_residual_forward(const void* H_residual, int dtype_h, con
 }
 
 extern "C" size_t mhc_add_residual_backward_workspace_bytes(int64_t B, int64_t S, int64_t D, int dtype_h) {
-  (void)S; (void)D; (void)dtype_h;
-  return partial_bytes(B, 4);
+  (void)dtype_h;
+  return add_bwd_partial_bytes(B, S, D);
 }
 
 extern "C" int mhc_add_residual_backward(const void* dH_new, int dtype_h, const void* branch_output, int dtype_bo,

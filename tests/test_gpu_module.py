@@ -157,6 +157,26 @@ def test_non_contiguous_inputs():
     assert rel_err(to_np(Hl.grad), og["H"]) < 1e-4 and rel_err(to_np(bol.grad), og["bo"]) < 1e-4
 
 
+@pytest.mark.parametrize("dynamic", [False, True])
+def test_empty_sequence(dynamic):
+    """S = 0: empty outputs and no launch errors.  dH_post is an empty sum, so the static layer's
+    H_post_base gradient is exactly zero (the dynamic layer's mean over no tokens is NaN, as
+    torch's H.mean is)."""
+    import mhc
+
+    hc = mhc.HyperConnection(64, dynamic=dynamic).to(DEV)
+    H = torch.zeros((2, 0, 4, 64), device=DEV, requires_grad=True)
+    bo = torch.zeros((2, 0, 64), device=DEV, requires_grad=True)
+    bi, add = hc(H)
+    Hn = add(bo)
+    assert bi.shape == (2, 0, 64) and Hn.shape == (2, 0, 4, 64)
+    (Hn.sum() + bi.sum()).backward()
+    torch.cuda.synchronize()
+    assert H.grad.shape == H.shape and bo.grad.shape == bo.shape
+    if not dynamic:
+        assert float(hc.H_post_base.grad.abs().sum()) == 0.0
+
+
 # --------------------------------------------------------------------------- closure edge cases
 
 def _oracle_grads(hc, H, bo, dHn, dbi):
