@@ -33,7 +33,7 @@ static size_t al(size_t v) { return (v + 255) & ~(size_t)255; }
 struct LayerWs {
   size_t colpart;    // mean-pool column partials [B][nS][4D]
   size_t pool_part;  // projection partials [B][nrc][25]
-  size_t red_part;   // [B][nblk][20] (pass B) or [B][tiles][4] (closure backward)
+  size_t red_part;   // [B][nblk][20] (pass B), [B][tiles][20] (pass BC) or [B][tiles][4] (closure backward)
   size_t dpre;       // [B][4]
   size_t dres;       // [B][16]
   size_t rowbuf;     // [B][52]
@@ -48,9 +48,8 @@ static LayerWs layer_ws(int64_t B, int64_t S, int64_t D, int dtype) {
   w.colpart = o;   o += al(mean_pool_colpart_bytes(dtype, B, S, D));
   w.pool_part = o; o += al((size_t)B * (nrc > 0 ? nrc : 1) * kPart * sizeof(float));
   {
-    // pass B's [B][nblk][20] and the closure backward's per-tile [B][tiles][4] share the region
-    const size_t pb = partial_bytes(B, 20), ab = add_bwd_partial_bytes(B, S, D);
-    w.red_part = o;  o += al(pb > ab ? pb : ab);
+    // the partials of pass B, pass BC and the closure backward share the region
+    w.red_part = o;  o += al(tile_partial_bytes(B, S, D, 20));
   }
   w.dpre = o;      o += al((size_t)B * 4 * sizeof(float));
   w.dres = o;      o += al((size_t)B * 16 * sizeof(float));
@@ -157,19 +156,23 @@ __global__ __launch_bounds__(kThreads) void static_weights_bwd_kernel(
 template <typename T, int W, bool HAS_DHN, bool REDUCE, bool WRITE_DH>
 static int launch_mix_bwd(const T* dbi, const T* dhn, const T* H, const float* w, T* dH, float* part, int64_t B,
                           int64_t S, int64_t D, uint32_t* nblk_out, hipStream_t st) {
-  // Pass B writes nothing bulk: two items per lane and full occupancy.  The
-  // passes that write dH take one item per lane and capped occupancy.
+  // Pass B writes nothing bulk: two items per lane, full occupancy, workgroups
+  // striding over the tiles.  The passes that write dH take one item per lane;
+  // on the vector path one workgroup per tile with the weights fetched behind
+  // its loads, up to 6 per CU (static pass BC at config-3 size 285.7 -> 280.2
+  // us, at config-5 size 298.7 -> 263.6 us), and a partial per tile.
   constexpr int U = WRITE_DH ? kLU : kLRU;
-  const size_t lds = WRITE_DH ? occupancy_lds(REDUCE ? 3 : 4) : 0;
+  constexpr bool ONE = WRITE_DH && W > 1;
+  const size_t lds = WRITE_DH ? occupancy_lds(ONE ? 6 : (REDUCE ? 3 : 4)) : 0;
   const Geom g0 = make_geom<W, U>(S, D, 0);
-  const uint32_t nblk = REDUCE ? reduce_blocks(g0.ntiles, B) : g0.ntiles;
+  const uint32_t nblk = REDUCE && !ONE ? reduce_blocks(g0.ntiles, B) : g0.ntiles;
   if (nblk_out) *nblk_out = nblk;
   if (nblk == 0) return MHC_OK;
   return for_batch_chunks(B, [&](int64_t b0, int64_t nb) {
     const Geom g = make_geom<W, U>(S, D, b0);
     // Pass B (REDUCE only): nt on the H loads alone; d_bi and dH_new are read again by pass C.
     constexpr int NT = WRITE_DH ? kNt : 4;
-    mix_bwd_kernel<T, W, U, HAS_DHN, REDUCE, WRITE_DH, NT><<<dim3(nblk, nb), kThreads, lds, st>>>(
+    mix_bwd_kernel<T, W, U, HAS_DHN, REDUCE, WRITE_DH, NT, (W > 1), ONE><<<dim3(nblk, nb), kThreads, lds, st>>>(
         dbi, dhn, H, WRow{w, kOut}, WRow{w + 8, kOut}, dH, part, g);
     return hip_status(hipGetLastError(), "layer mix backward launch");
   });
@@ -404,7 +407,7 @@ extern "C" int mhc_layer_static_backward(const void* H, int dtype, const void* d
                                                    &nblk, st);
   });
   if (rc) return rc;
-  reduce_split_kernel<20, 4><<<dim3((unsigned)B), kThreads, 0, st>>>(part, dpre, dres, (int)nblk);
+  reduce_split_kernel<20, 4><<<dim3((unsigned)B, 5), kThreads, 0, st>>>(part, dpre, dres, (int)nblk);
   if ((rc = hip_status(hipGetLastError(), "layer static reduce launch"))) return rc;
   static_weights_bwd_kernel<<<1, kThreads, 0, st>>>(H_pre_base, H_post_base, H_res_base, w, dpre, dH_post, dres,
                                                     grad_bias, B, iters);
@@ -445,6 +448,6 @@ extern "C" int mhc_layer_mix_backward(const void* H, int dtype, const void* d_br
                                                    &nblk, st);
   });
   if (rc) return rc;
-  reduce_split_kernel<20, 4><<<dim3((unsigned)B), kThreads, 0, st>>>(part, dH_pre, dH_res, (int)nblk);
+  reduce_split_kernel<20, 4><<<dim3((unsigned)B, 5), kThreads, 0, st>>>(part, dH_pre, dH_res, (int)nblk);
   return hip_status(hipGetLastError(), "layer mix backward reduce launch");
 }

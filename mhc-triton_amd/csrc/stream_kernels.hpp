@@ -299,14 +299,17 @@ __global__ __launch_bounds__(kThreads) void add_residual_bwd_kernel(const T* __r
 // reads H for the last time but d_bi and dH_new again in pass C, which then
 // finds part of them in the 256 MB memory-side cache.
 // ---------------------------------------------------------------------------
-template <typename T, int W, int U, bool HAS_DHN, bool REDUCE, bool WRITE_DH, int NT = 0, bool BUF = (W > 1)>
+template <typename T, int W, int U, bool HAS_DHN, bool REDUCE, bool WRITE_DH, int NT = 0, bool BUF = (W > 1),
+          bool ONE = false>
 __global__ __launch_bounds__(kThreads) void mix_bwd_kernel(const T* __restrict__ dbi, const T* __restrict__ dhn,
                                                            const T* __restrict__ H, WRow pre, WRow res,
                                                            T* __restrict__ dH, float* __restrict__ part, Geom g) {
+  // ONE: one workgroup per tile (grid.x == g.ntiles), the weights fetched behind the tile's loads;
+  // otherwise workgroups stride over the tiles.
   __shared__ float lds[4 * 20];
   const int64_t b = g.b0 + blockIdx.y;
   float wp[4], wr[16];
-  if constexpr (WRITE_DH) {
+  if constexpr (WRITE_DH && !ONE) {
     load_w4(pre, b, wp);
     if constexpr (HAS_DHN) load_w16(res, b, wr);
   }
@@ -346,6 +349,11 @@ __global__ __launch_bounds__(kThreads) void mix_bwd_kernel(const T* __restrict__
         }
       }
     }
+    if constexpr (WRITE_DH && ONE) {
+      loads_issued();
+      load_w4(pre, b, wp);
+      if constexpr (HAS_DHN) load_w16(res, b, wr);
+    }
     const Span<T, BUF> dHs(dH + t0 * 4 * D, rest * 4 * D);
 #pragma unroll
     for (int u = 0; u < U; ++u) {
@@ -382,6 +390,7 @@ __global__ __launch_bounds__(kThreads) void mix_bwd_kernel(const T* __restrict__
         }
       }
     }
+    if constexpr (ONE) break;
   }
   if constexpr (REDUCE) {
     block_sum<20>(acc, lds);
@@ -530,35 +539,30 @@ __global__ __launch_bounds__(kThreads) void collapse_kernel(const TH* __restrict
 
 // Final reduction of [B][nblk][NV] partials into up to two outputs:
 // out0[b*SPLIT + k] for k < SPLIT, out1[b*(NV-SPLIT) + k-SPLIT] otherwise.
+// Grid: x = batch, y = one 16-byte column (4 consecutive elements) of the
+// NV-float records (NV % 4 == 0, 16-byte aligned in the workspace).  Thread t
+// sums records t, t + 256, ... in index order, then block_sum adds the 256
+// per-thread sums: a fixed order, the same for every column split.
 template <int NV, int SPLIT>
 __global__ __launch_bounds__(kThreads) void reduce_split_kernel(const float* __restrict__ part,
                                                                 float* __restrict__ out0,
                                                                 float* __restrict__ out1, int nblk) {
-  // Records are NV floats (NV % 4 == 0, 16-byte aligned in the workspace) and
-  // are read as 16-byte vectors; each thread sums its records in index order.
   static_assert(NV % 4 == 0, "records of whole 16-byte vectors");
-  __shared__ float lds[4 * NV];
+  __shared__ float lds[4 * 4];
   const int64_t b = blockIdx.x;
-  const f32x4* p = reinterpret_cast<const f32x4*>(part + b * nblk * NV);
-  f32x4 a4[NV / 4];
-#pragma unroll
-  for (int q = 0; q < NV / 4; ++q) a4[q] = f32x4{0.f, 0.f, 0.f, 0.f};
+  const int q = blockIdx.y;
+  const f32x4* p = reinterpret_cast<const f32x4*>(part + b * nblk * NV) + q;
+  f32x4 a4 = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll 8
-  for (int k = threadIdx.x; k < nblk; k += kThreads) {
-#pragma unroll
-    for (int q = 0; q < NV / 4; ++q) a4[q] += p[(int64_t)k * (NV / 4) + q];
-  }
-  float acc[NV];
-#pragma unroll
-  for (int q = 0; q < NV / 4; ++q)
-#pragma unroll
-    for (int c = 0; c < 4; ++c) acc[4 * q + c] = a4[q][c];
-  block_sum<NV>(acc, lds);
+  for (int k = threadIdx.x; k < nblk; k += kThreads) a4 += p[(int64_t)k * (NV / 4)];
+  float acc[4] = {a4[0], a4[1], a4[2], a4[3]};
+  block_sum<4>(acc, lds);
   if (threadIdx.x == 0) {
 #pragma unroll
-    for (int i = 0; i < NV; ++i) {
-      if (i < SPLIT) out0[b * SPLIT + i] = acc[i];
-      else out1[b * (NV - SPLIT) + (i - SPLIT)] = acc[i];
+    for (int c = 0; c < 4; ++c) {
+      const int i = 4 * q + c;
+      if (i < SPLIT) out0[b * SPLIT + i] = acc[c];
+      else out1[b * (NV - SPLIT) + (i - SPLIT)] = acc[c];
     }
   }
 }
@@ -598,15 +602,15 @@ inline size_t partial_bytes(int64_t B, int nv) {
   return (size_t)(B * per_b * nv) * sizeof(float);
 }
 
-// Bytes of the closure backward's partials (add_residual_bwd_kernel, 4 floats
-// per workgroup): on the vector path one workgroup per tile, on the ragged
-// path the reduce_blocks count.  Sized for the narrowest vector width (fp32,
-// 4 elements per lane), because the path is chosen per call from the pointers'
-// alignment.
-inline size_t add_bwd_partial_bytes(int64_t B, int64_t S, int64_t D) {
+// Bytes of the partials of a reduction kernel that runs one workgroup per tile
+// on the vector path (nv floats per workgroup) and the reduce_blocks count on
+// the ragged path.  Sized for the narrowest vector width (fp32, 4 elements per
+// lane, one item per lane), because the path is chosen per call from the
+// pointers' alignment.
+inline size_t tile_partial_bytes(int64_t B, int64_t S, int64_t D, int nv) {
   const int64_t tiles = (S * D / 4 + kThreads - 1) / kThreads;
-  const size_t vec = (size_t)(B > 0 ? B : 1) * (size_t)(tiles > 0 ? tiles : 1) * 4 * sizeof(float);
-  const size_t rag = partial_bytes(B, 4);
+  const size_t vec = (size_t)(B > 0 ? B : 1) * (size_t)(tiles > 0 ? tiles : 1) * nv * sizeof(float);
+  const size_t rag = partial_bytes(B, nv);
   return vec > rag ? vec : rag;
 }
 

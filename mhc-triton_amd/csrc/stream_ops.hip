@@ -23,16 +23,24 @@ template <typename T, int W>
 static int stream_mix_bwd(const T* dbi, const T* dhr, const T* H, const float* pre, const float* res, T* dH,
                           float* dpre, float* dres, int64_t B, int64_t S, int64_t D, float* part,
                           hipStream_t st) {
+  // Vector path: one workgroup per tile, weights fetched behind its loads, up
+  // to 6 per CU, a partial per tile.  Ragged path: workgroups stride over the
+  // tiles at 3 per CU.
   const Geom g0 = make_geom<W, kU>(S, D, 0);
-  const uint32_t nblk = reduce_blocks(g0.ntiles, B);
-  int rc = for_batch_chunks(B, [&](int64_t b0, int64_t nb) {
+  const uint32_t nblk = W > 1 ? g0.ntiles : reduce_blocks(g0.ntiles, B);
+  // With no tiles nothing is launched and the reduce writes zeros.
+  int rc = nblk == 0 ? (int)MHC_OK : for_batch_chunks(B, [&](int64_t b0, int64_t nb) {
     const Geom g = make_geom<W, kU>(S, D, b0);
-    mix_bwd_kernel<T, W, kU, true, true, true, kNt><<<dim3(nblk, nb), kThreads, occupancy_lds(3), st>>>(
-        dbi, dhr, H, WRow{pre, 4}, WRow{res, 16}, dH, part, g);
+    if constexpr (W > 1)
+      mix_bwd_kernel<T, W, kU, true, true, true, kNt, true, true><<<dim3(nblk, nb), kThreads, occupancy_lds(6), st>>>(
+          dbi, dhr, H, WRow{pre, 4}, WRow{res, 16}, dH, part, g);
+    else
+      mix_bwd_kernel<T, W, kU, true, true, true, kNt><<<dim3(nblk, nb), kThreads, occupancy_lds(3), st>>>(
+          dbi, dhr, H, WRow{pre, 4}, WRow{res, 16}, dH, part, g);
     return hip_status(hipGetLastError(), "stream_mix_backward launch");
   });
   if (rc) return rc;
-  reduce_split_kernel<20, 4><<<dim3((unsigned)B), kThreads, 0, st>>>(part, dpre, dres, (int)nblk);
+  reduce_split_kernel<20, 4><<<dim3((unsigned)B, 5), kThreads, 0, st>>>(part, dpre, dres, (int)nblk);
   return hip_status(hipGetLastError(), "stream_mix_backward reduce launch");
 }
 
@@ -69,7 +77,7 @@ static int add_res_bwd(const TH* dhn, const TB* bo, WRow post, TB* dbo, float* d
     return hip_status(hipGetLastError(), "add_residual_backward launch");
   });
   if (rc) return rc;
-  reduce_split_kernel<4, 4><<<dim3((unsigned)B), kThreads, 0, st>>>(part, dpost, nullptr, (int)nblk);
+  reduce_split_kernel<4, 4><<<dim3((unsigned)B, 1), kThreads, 0, st>>>(part, dpost, nullptr, (int)nblk);
   return hip_status(hipGetLastError(), "add_residual_backward reduce launch");
 }
 
@@ -132,7 +140,7 @@ extern "C" int mhc_stream_mix_forward(const void* H, const float* H_pre, const f
 
 extern "C" size_t mhc_stream_mix_backward_workspace_bytes(int64_t B, int64_t S, int64_t D, int dtype) {
   (void)S; (void)D; (void)dtype;
-  return partial_bytes(B, 20);
+  return tile_partial_bytes(B, S, D, 20);
 }
 
 extern "C" int mhc_stream_mix_backward(const void* d_branch_input, const void* dH_residual, const void* H,
@@ -190,7 +198,7 @@ extern "C" int mhc_add_residual_forward(const void* H_residual, int dtype_h, con
 
 extern "C" size_t mhc_add_residual_backward_workspace_bytes(int64_t B, int64_t S, int64_t D, int dtype_h) {
   (void)dtype_h;
-  return add_bwd_partial_bytes(B, S, D);
+  return tile_partial_bytes(B, S, D, 4);
 }
 
 extern "C" int mhc_add_residual_backward(const void* dH_new, int dtype_h, const void* branch_output, int dtype_bo,
