@@ -54,7 +54,10 @@ __global__ __launch_bounds__(kThreads) void sinkhorn_bwd_kernel(const T* __restr
   float m[16], d[16];
   load_mat<T, VEC>(M + i * 16, m);
   load_mat<TD, VEC>(dP + i * 16, d);
-  sk_backward(m, d, iters, eps);
+  // The element-wise loads of the unaligned path need more registers: there
+  // five checkpoints keep 3 waves per SIMD (ten would leave one).  The result
+  // does not depend on the checkpoint count.
+  sk_backward<VEC ? 10 : 5>(m, d, iters, eps);
   store_mat<T, VEC>(dM + i * 16, d);
 }
 

@@ -17,7 +17,10 @@
 // checkpointed every L = ceil(T / NCK) rounds in registers and each state is
 // recomputed from the nearest checkpoint; the recomputed states are
 // bit-identical to the ones a full recompute produces (same instruction
-// sequence), at 66 instead of 210 rounds for T = 20.
+// sequence), at 48 instead of 210 rounds for T = 20 with NCK = 10.  The ten
+// checkpoints hold 160 registers (234 VGPRs, 2 waves per SIMD); at 2^20
+// matrices that runs in 163 us against 191 us with NCK = 5 (66 rounds, 154
+// VGPRs, 3 waves per SIMD) -- the kernel is VALU-bound, so fewer rounds win.
 #pragma once
 
 #include "common.hpp"
@@ -88,7 +91,7 @@ __device__ __forceinline__ void sk_round_backward(const float (&m)[16], float (&
 
 // Gradient of Sinkhorn(M) w.r.t. M.  On entry `mat` holds M and `d` holds the
 // gradient w.r.t. the output P; on exit `d` holds dM.
-template <int NCK = 5>
+template <int NCK = 10>
 __device__ __forceinline__ void sk_backward(const float (&mat)[16], float (&d)[16], int iters, float eps) {
   float m[16];
 #pragma unroll
