@@ -332,6 +332,20 @@ __device__ __forceinline__ void block_sum(float (&v)[NV], float* lds) {
   }
 }
 
+// block_sum for a workgroup of NT threads: one wave (the wave sum alone) or
+// kThreads.  The result is valid in thread 0 only.  With one wave the result
+// equals block_sum's whenever only the first wave holds non-zero values.
+template <int NT, int NV>
+__device__ __forceinline__ void group_sum(float (&v)[NV], float* lds) {
+  static_assert(NT == 64 || NT == kThreads, "one wave or a full workgroup");
+  if constexpr (NT == 64) {
+#pragma unroll
+    for (int i = 0; i < NV; ++i) v[i] = wave_sum(v[i]);
+  } else {
+    block_sum<NV>(v, lds);
+  }
+}
+
 // Zero-fills n floats.  A kernel rather than hipMemsetAsync so that callers may
 // capture the work in a HIP graph.
 template <int = 0>

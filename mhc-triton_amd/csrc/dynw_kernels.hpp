@@ -499,9 +499,15 @@ __global__ __launch_bounds__(kThreads) void dynw_bwd_rows_kernel(const float* __
 // chunks in order.  The per-row record is the same for every thread of the
 // workgroup (scalar loads).  Workgroup (0, 0) also sums the per-row records
 // into grad_bias [24] and grad_alpha [3] (threads stride over rows, then a
-// fixed-order block sum).
-template <typename TX, typename TG>
-__global__ __launch_bounds__(kThreads) void dynw_bwd_wide_kernel(const TX* __restrict__ x,
+// fixed-order block sum).  Launched with kWideThreads = 64 (one wave) per
+// workgroup: the work is a few loads and ~50 FMAs per k, so the pass is
+// latency-bound and wants every CU busy -- at the layer's R = 4, K = 16384,
+// 256 one-wave workgroups take 3.1 us against 6.6 us for 64 of 256 threads,
+// with the same results.
+constexpr int kWideThreads = 64;
+
+template <typename TX, typename TG, int NT = kThreads>
+__global__ __launch_bounds__(NT) void dynw_bwd_wide_kernel(const TX* __restrict__ x,
                                                                  const float* __restrict__ phi,
                                                                  const float* __restrict__ rowbuf,
                                                                  TG* __restrict__ gx, float* __restrict__ gphi,
@@ -514,12 +520,12 @@ __global__ __launch_bounds__(kThreads) void dynw_bwd_wide_kernel(const TX* __res
     float acc[27];
 #pragma unroll
     for (int i = 0; i < 27; ++i) acc[i] = 0.f;
-    for (int64_t r = threadIdx.x; r < R; r += kThreads) {
+    for (int64_t r = threadIdx.x; r < R; r += NT) {
       const float* rb = rowbuf + r * kRow;
 #pragma unroll
       for (int i = 0; i < 27; ++i) acc[i] += rb[25 + i];
     }
-    block_sum<27>(acc, lds);
+    group_sum<NT, 27>(acc, lds);
     if (threadIdx.x == 0) {
 #pragma unroll
       for (int j = 0; j < kOut; ++j) if (gbias) gbias[j] = acc[j];
@@ -527,7 +533,7 @@ __global__ __launch_bounds__(kThreads) void dynw_bwd_wide_kernel(const TX* __res
       for (int g = 0; g < 3; ++g) if (galpha) galpha[g] = acc[24 + g];
     }
   }
-  const int64_t k = (int64_t)blockIdx.x * kThreads + threadIdx.x;
+  const int64_t k = (int64_t)blockIdx.x * NT + threadIdx.x;
   if (k >= K || (!gx && !gphi)) return;
   const int64_t r_beg = (int64_t)blockIdx.y * RC;
   const int64_t r_end = r_beg + RC < R ? r_beg + RC : R;

@@ -370,8 +370,8 @@ extern "C" int mhc_layer_dynamic_backward(const void* H, int dtype, const void* 
       aux, P, InRow{w, kOut}, InRow{nullptr, 0}, InRow{dH_post, 4}, InRow{nullptr, 0}, part, (int)nblk, rowbuf, B,
       K, iters, eps);
   if ((rc = hip_status(hipGetLastError(), "layer weights backward rows launch"))) return rc;
-  dynw_bwd_wide_kernel<float, float>
-      <<<dim3(K > 0 ? (unsigned)((K + kThreads - 1) / kThreads) : 1u), kThreads, 0, st>>>(
+  dynw_bwd_wide_kernel<float, float, kWideThreads>
+      <<<dim3(K > 0 ? (unsigned)((K + kWideThreads - 1) / kWideThreads) : 1u), kWideThreads, 0, st>>>(
           x, phi, rowbuf, dH ? gx : nullptr, grad_phi, nullptr, grad_bias, grad_alpha, B, K, B, aligned16(phi));
   if ((rc = hip_status(hipGetLastError(), "layer weights backward wide launch"))) return rc;
   if (!dH || S * D == 0) return MHC_OK;
