@@ -57,13 +57,38 @@ __device__ __forceinline__ void load_phi_row(const float* __restrict__ phi, int6
   }
 }
 
+// Sum of NV (<= 256) per-thread values over a 256-thread workgroup, for many
+// values at once: each 16-lane row adds with DPP (sum_all16, full-rate VALU
+// with no LDS crossbar traffic), the 16 row sums of each value go through LDS,
+// and thread i < NV adds value i's row sums in row order.  Returns the total
+// of value threadIdx.x in threads < NV.  A wave butterfly over __shfl_xor costs
+// 6 ds_bpermute per value instead (600 for the 100 partials below).
+template <int NV>
+__device__ __forceinline__ float block_sum_rows(float (&v)[NV], float* lds) {
+  static_assert(NV <= kThreads, "one output per thread");
+  const int row = threadIdx.x >> 4;
+#pragma unroll
+  for (int i = 0; i < NV; ++i) v[i] = sum_all16(v[i]);
+  if ((threadIdx.x & 15) == 0) {
+#pragma unroll
+    for (int i = 0; i < NV; ++i) lds[row * NV + i] = v[i];
+  }
+  __syncthreads();
+  float t = 0.f;
+  if (threadIdx.x < NV) {
+#pragma unroll
+    for (int q = 0; q < kThreads / 16; ++q) t += lds[q * NV + threadIdx.x];
+  }
+  return t;
+}
+
 // part[r][kc][0:24] = sum_{k in chunk kc} x[r,k] phi[k,:],  part[r][kc][24] = sum x[r,k]^2
 template <typename TX, int RT>
 __global__ __launch_bounds__(kThreads) void dynw_partial_kernel(const TX* __restrict__ x,
                                                                 const float* __restrict__ phi,
                                                                 float* __restrict__ part, int64_t R, int64_t K,
                                                                 int nK, int64_t KC, bool phi_vec) {
-  __shared__ float lds[4 * RT * kPart];
+  __shared__ float lds[(kThreads / 16) * RT * kPart];
   const int64_t r0 = (int64_t)blockIdx.x * RT;
   const int kc = blockIdx.y;
   float acc[RT * kPart];
@@ -84,17 +109,9 @@ __global__ __launch_bounds__(kThreads) void dynw_partial_kernel(const TX* __rest
       }
     }
   }
-  block_sum<RT * kPart>(acc, lds);
-  if (threadIdx.x == 0) {
-#pragma unroll
-    for (int r = 0; r < RT; ++r) {
-      if (r0 + r < R) {
-        float* pp = part + ((r0 + r) * nK + kc) * kPart;
-#pragma unroll
-        for (int j = 0; j < kPart; ++j) pp[j] = acc[r * kPart + j];
-      }
-    }
-  }
+  const float tot = block_sum_rows<RT * kPart>(acc, lds);
+  const int r = threadIdx.x / kPart, j = threadIdx.x - r * kPart;
+  if (threadIdx.x < RT * kPart && r0 + r < R) part[((r0 + r) * nK + kc) * kPart + j] = tot;
 }
 
 // ---------------------------------------------------------------------------
@@ -316,16 +333,18 @@ __device__ __forceinline__ void finalize_row16(int e, int64_t r, float raw_res, 
 }
 
 // One wave per row.  Lane l sums the partial records l, l+64, l+128, ... (25
-// floats each) in chunk order, the wave then adds the 64 lane sums with a
-// fixed butterfly, and lanes 0..15 run the epilogue.  Keeping 64 independent
-// load streams per row instead of one serial chain matters: R is the batch (4
-// at dim 4096) and this kernel sits between two full passes over H.
+// floats each) in chunk order; each 16-lane row of the wave then adds its lane
+// sums with DPP (sum_all16), and lanes 0..15 add the four row sums in order
+// and run the epilogue.  Keeping 64 independent load streams per row instead
+// of one serial chain matters: R is the batch (4 at dim 4096) and this kernel
+// sits between two full passes over H.  (A __shfl_xor butterfly took 150
+// ds_bpermute per wave for the same sums.)
 template <int = 0>
 __global__ __launch_bounds__(kThreads) void dynw_finalize_kernel(const float* __restrict__ part, int nK, int64_t R,
                                                                  int64_t K, DynParams P, OutRow o_pre,
                                                                  OutRow o_post, OutRow o_res,
                                                                  float* __restrict__ aux, int iters, float eps) {
-  __shared__ float tot[4][kPart];
+  __shared__ float quarter[4][4][kPart];  // [wave][16-lane row][value]
   const int wave = threadIdx.x >> 6;
   const int lane = threadIdx.x & 63;
   const int64_t r = (int64_t)blockIdx.x * 4 + wave;
@@ -339,15 +358,17 @@ __global__ __launch_bounds__(kThreads) void dynw_finalize_kernel(const float* __
     for (int j = 0; j < kPart; ++j) acc[j] += p[j];
   }
 #pragma unroll
-  for (int j = 0; j < kPart; ++j) acc[j] = wave_sum(acc[j]);
-  if (lane == 0) {
+  for (int j = 0; j < kPart; ++j) acc[j] = sum_all16(acc[j]);
+  if ((lane & 15) == 0) {
 #pragma unroll
-    for (int j = 0; j < kPart; ++j) tot[wave][j] = acc[j];
+    for (int j = 0; j < kPart; ++j) quarter[wave][lane >> 4][j] = acc[j];
   }
   __syncthreads();
   if (!live || lane >= 16) return;
-  const float* t = tot[wave];
-  finalize_row16(lane, r, t[8 + lane], t[lane & 7], t[kOut], K, P, o_pre, o_post, o_res, aux, iters, eps, true);
+  const float(*q)[kPart] = quarter[wave];
+  auto tot = [&](int j) { return ((q[0][j] + q[1][j]) + q[2][j]) + q[3][j]; };
+  finalize_row16(lane, r, tot(8 + lane), tot(lane & 7), tot(kOut), K, P, o_pre, o_post, o_res, aux, iters, eps,
+                 true);
 }
 
 // The same for many rows with few chunks (the MFMA projection at R = tokens:
@@ -408,6 +429,7 @@ __global__ __launch_bounds__(kThreads) void dynw_bwd_rows_kernel(const float* __
   static_assert(RPW == 1 || RPW == 4, "rows per workgroup");
   __shared__ float slots[kSkSlots * 64];
   __shared__ float red[4][20];
+  __shared__ float quarter[4][4][20];  // [wave][16-lane row][value]
   const int wave = threadIdx.x >> 6;
   const int lane = threadIdx.x & 63;
   if (part20) {
@@ -425,20 +447,30 @@ __global__ __launch_bounds__(kThreads) void dynw_bwd_rows_kernel(const float* __
         for (int q = 0; q < 5; ++q) acc[q] += p[q];
       }
     }
+    // Each 16-lane row adds its lane sums with DPP; the row sums then add in
+    // order through LDS (per wave with RPW == 4, over the workgroup with 1).
 #pragma unroll
     for (int q = 0; q < 5; ++q) {
 #pragma unroll
       for (int c = 0; c < 4; ++c) {
-        const float v = wave_sum(acc[q][c]);
-        if (lane == 0) red[wave][4 * q + c] = v;
+        const float v = sum_all16(acc[q][c]);
+        if ((lane & 15) == 0) quarter[wave][lane >> 4][4 * q + c] = v;
       }
     }
+    __syncthreads();
     if (RPW == 1) {
-      __syncthreads();
       if (threadIdx.x < 20) {
         const int v = threadIdx.x;
-        red[0][v] = ((red[0][v] + red[1][v]) + red[2][v]) + red[3][v];
+        float t = 0.f;
+#pragma unroll
+        for (int w = 0; w < 4; ++w)
+#pragma unroll
+          for (int h = 0; h < 4; ++h) t += quarter[w][h][v];
+        red[0][v] = t;
       }
+    } else if (lane < 20) {
+      red[wave][lane] = ((quarter[wave][0][lane] + quarter[wave][1][lane]) + quarter[wave][2][lane]) +
+                        quarter[wave][3][lane];
     }
   }
   __syncthreads();
@@ -853,7 +885,7 @@ __global__ __launch_bounds__(kThreads) void colsum_reduce_kernel(const float* __
                                                                  const float* __restrict__ phi,
                                                                  float* __restrict__ projpart, int64_t K, int nS,
                                                                  float inv_S, int64_t b0, bool phi_vec) {
-  __shared__ float red[4 * kPart];
+  __shared__ float red[(kThreads / 16) * kPart];
   const int64_t b = b0 + blockIdx.y;
   const int64_t c = (int64_t)blockIdx.x * kThreads + threadIdx.x;
   float pv[kPart];
@@ -875,12 +907,8 @@ __global__ __launch_bounds__(kThreads) void colsum_reduce_kernel(const float* __
     }
   }
   if constexpr (PROJ) {
-    block_sum<kPart>(pv, red);
-    if (threadIdx.x == 0) {
-      float* pp = projpart + (b * gridDim.x + blockIdx.x) * kPart;
-#pragma unroll
-      for (int j = 0; j < kPart; ++j) pp[j] = pv[j];
-    }
+    const float tot = block_sum_rows<kPart>(pv, red);
+    if (threadIdx.x < kPart) projpart[(b * gridDim.x + blockIdx.x) * kPart + threadIdx.x] = tot;
   }
 }
 
