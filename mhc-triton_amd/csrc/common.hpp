@@ -332,6 +332,65 @@ __device__ __forceinline__ void block_sum(float (&v)[NV], float* lds) {
   }
 }
 
+// ---------------------------------------------------------------------------
+// Sums inside a 16-lane row of a wave with DPP (full-rate VALU, no LDS):
+// quad-permute adds give the sum over a quad (sum_row16: lanes e ^ 1, e ^ 2),
+// two row-rotate adds the sum over lanes e, e ^ 4, e ^ 8, e ^ 12 (sum_col16).
+// Both trees add the same pairs in every lane, so all lanes that share a sum
+// see bit-identical values.  All 16 lanes of a row must be active.  The
+// Sinkhorn kernels use the pair as the row and column sums of a 4x4 matrix
+// held one element per lane (lane e = 4 i + j).
+// ---------------------------------------------------------------------------
+template <int CTRL>
+__device__ __forceinline__ float dpp(float v) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, 0xF, 0xF, false));
+}
+
+constexpr int kDppQuadXor1 = 0xB1;  // quad_perm [1,0,3,2]
+constexpr int kDppQuadXor2 = 0x4E;  // quad_perm [2,3,0,1]
+constexpr int kDppRowRor4 = 0x124;  // row_ror:4
+constexpr int kDppRowRor8 = 0x128;  // row_ror:8
+
+// Sum over j of P[i][j] (the 4 lanes of a quad).
+__device__ __forceinline__ float sum_row16(float v) {
+  v += dpp<kDppQuadXor1>(v);
+  return v + dpp<kDppQuadXor2>(v);
+}
+
+// Sum over i of P[i][j] (lanes e, e^4, e^8, e^12 of the 16-lane row).
+__device__ __forceinline__ float sum_col16(float v) {
+  v += dpp<kDppRowRor8>(v);
+  return v + dpp<kDppRowRor4>(v);
+}
+
+__device__ __forceinline__ float sum_all16(float v) { return sum_col16(sum_row16(v)); }
+
+// Sum of NV (<= 256) per-thread values over a 256-thread workgroup, for many
+// values at once: each 16-lane row adds with DPP (sum_all16, full-rate VALU
+// with no LDS crossbar traffic), the 16 row sums of each value go through LDS,
+// and thread i < NV adds value i's row sums in row order.  Returns the total
+// of value threadIdx.x in threads < NV.  A wave butterfly over __shfl_xor costs
+// 6 ds_bpermute per value instead (600 for the weights projection's 100
+// partials).
+template <int NV>
+__device__ __forceinline__ float block_sum_rows(float (&v)[NV], float* lds) {
+  static_assert(NV <= kThreads, "one output per thread");
+  const int row = threadIdx.x >> 4;
+#pragma unroll
+  for (int i = 0; i < NV; ++i) v[i] = sum_all16(v[i]);
+  if ((threadIdx.x & 15) == 0) {
+#pragma unroll
+    for (int i = 0; i < NV; ++i) lds[row * NV + i] = v[i];
+  }
+  __syncthreads();
+  float t = 0.f;
+  if (threadIdx.x < NV) {
+#pragma unroll
+    for (int q = 0; q < kThreads / 16; ++q) t += lds[q * NV + threadIdx.x];
+  }
+  return t;
+}
+
 // block_sum for a workgroup of NT threads: one wave (the wave sum alone) or
 // kThreads.  The result is valid in thread 0 only.  With one wave the result
 // equals block_sum's whenever only the first wave holds non-zero values.

@@ -57,31 +57,6 @@ __device__ __forceinline__ void load_phi_row(const float* __restrict__ phi, int6
   }
 }
 
-// Sum of NV (<= 256) per-thread values over a 256-thread workgroup, for many
-// values at once: each 16-lane row adds with DPP (sum_all16, full-rate VALU
-// with no LDS crossbar traffic), the 16 row sums of each value go through LDS,
-// and thread i < NV adds value i's row sums in row order.  Returns the total
-// of value threadIdx.x in threads < NV.  A wave butterfly over __shfl_xor costs
-// 6 ds_bpermute per value instead (600 for the 100 partials below).
-template <int NV>
-__device__ __forceinline__ float block_sum_rows(float (&v)[NV], float* lds) {
-  static_assert(NV <= kThreads, "one output per thread");
-  const int row = threadIdx.x >> 4;
-#pragma unroll
-  for (int i = 0; i < NV; ++i) v[i] = sum_all16(v[i]);
-  if ((threadIdx.x & 15) == 0) {
-#pragma unroll
-    for (int i = 0; i < NV; ++i) lds[row * NV + i] = v[i];
-  }
-  __syncthreads();
-  float t = 0.f;
-  if (threadIdx.x < NV) {
-#pragma unroll
-    for (int q = 0; q < kThreads / 16; ++q) t += lds[q * NV + threadIdx.x];
-  }
-  return t;
-}
-
 // part[r][kc][0:24] = sum_{k in chunk kc} x[r,k] phi[k,:],  part[r][kc][24] = sum x[r,k]^2
 template <typename TX, int RT>
 __global__ __launch_bounds__(kThreads) void dynw_partial_kernel(const TX* __restrict__ x,

@@ -164,30 +164,7 @@ __device__ __forceinline__ void sk_backward(const float (&mat)[16], float (&d)[1
 // The serial one-matrix-per-lane form above stays the throughput choice for
 // large batches of matrices (fewer instructions per matrix).
 // ---------------------------------------------------------------------------
-template <int CTRL>
-__device__ __forceinline__ float dpp(float v) {
-  return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, 0xF, 0xF, false));
-}
-
-constexpr int kDppQuadXor1 = 0xB1;  // quad_perm [1,0,3,2]
-constexpr int kDppQuadXor2 = 0x4E;  // quad_perm [2,3,0,1]
-constexpr int kDppRowRor4 = 0x124;  // row_ror:4
-constexpr int kDppRowRor8 = 0x128;  // row_ror:8
-
-// Sum over j of P[i][j] (the 4 lanes of a quad).
-__device__ __forceinline__ float sum_row16(float v) {
-  v += dpp<kDppQuadXor1>(v);
-  return v + dpp<kDppQuadXor2>(v);
-}
-
-// Sum over i of P[i][j] (lanes e, e^4, e^8, e^12 of the 16-lane row).
-__device__ __forceinline__ float sum_col16(float v) {
-  v += dpp<kDppRowRor8>(v);
-  return v + dpp<kDppRowRor4>(v);
-}
-
-__device__ __forceinline__ float sum_all16(float v) { return sum_col16(sum_row16(v)); }
-
+// (dpp, sum_row16, sum_col16 and sum_all16 are in common.hpp.)
 __device__ __forceinline__ float sk16_round(float m, float eps) {
   m *= fast_rcp(sum_row16(m) + eps);
   return m * fast_rcp(sum_col16(m) + eps);

@@ -232,7 +232,7 @@ __global__ __launch_bounds__(kThreads) void add_residual_bwd_kernel(const T* __r
                                                                     Geom g) {
   // ONE: one workgroup per tile (grid.x == g.ntiles), the weights fetched behind the tile's loads;
   // otherwise workgroups stride over the tiles.
-  __shared__ float lds[4 * 4];
+  __shared__ float lds[16 * 4];
   const int64_t b = g.b0 + blockIdx.y;
   float wq[4];
   if constexpr (!ONE) load_w4(post, b, wq);
@@ -279,12 +279,8 @@ __global__ __launch_bounds__(kThreads) void add_residual_bwd_kernel(const T* __r
     }
     if constexpr (ONE) break;
   }
-  block_sum<4>(acc, lds);
-  if (threadIdx.x == 0) {
-    float* pp = part + (b * gridDim.x + blockIdx.x) * 4;
-#pragma unroll
-    for (int k = 0; k < 4; ++k) pp[k] = acc[k];
-  }
+  const float tot = block_sum_rows<4>(acc, lds);
+  if (threadIdx.x < 4) part[(b * gridDim.x + blockIdx.x) * 4 + threadIdx.x] = tot;
 }
 
 // ---------------------------------------------------------------------------
@@ -306,7 +302,7 @@ __global__ __launch_bounds__(kThreads) void mix_bwd_kernel(const T* __restrict__
                                                            T* __restrict__ dH, float* __restrict__ part, Geom g) {
   // ONE: one workgroup per tile (grid.x == g.ntiles), the weights fetched behind the tile's loads;
   // otherwise workgroups stride over the tiles.
-  __shared__ float lds[4 * 20];
+  __shared__ float lds[16 * 20];
   const int64_t b = g.b0 + blockIdx.y;
   float wp[4], wr[16];
   if constexpr (WRITE_DH && !ONE) {
@@ -393,12 +389,8 @@ __global__ __launch_bounds__(kThreads) void mix_bwd_kernel(const T* __restrict__
     if constexpr (ONE) break;
   }
   if constexpr (REDUCE) {
-    block_sum<20>(acc, lds);
-    if (threadIdx.x == 0) {
-      float* pp = part + (b * gridDim.x + blockIdx.x) * 20;
-#pragma unroll
-      for (int k = 0; k < 20; ++k) pp[k] = acc[k];
-    }
+    const float tot = block_sum_rows<20>(acc, lds);
+    if (threadIdx.x < 20) part[(b * gridDim.x + blockIdx.x) * 20 + threadIdx.x] = tot;
   }
 }
 
