@@ -133,19 +133,26 @@ __global__ __launch_bounds__(kThreads) void dynw_pack_phi_kernel(const float* __
 }
 
 // One workgroup per 128-row tile and K chunk (wave w owns rows 32w..32w+31).
-// Each wave loads its A fragments straight from global memory (lane l: row
-// l % 32, the 16 bytes at k = 16 s + 8 (l / 32)), a group of kMfmaGrpSteps
-// steps ahead of the MFMAs.  The phi fragments of a group are the same for
-// all four waves, so the workgroup stages them once in double-buffered LDS
-// (one barrier per group) instead of every wave loading them from L2: the
-// per-wave phi loads competing with the x stream had cost ~45 us of 175 at
-// R = K = 16384 (149 us this way).  Each 16-k step's three MFMAs start from
-// zero and the step result is added into `acc` with fp32 VALU adds (a long
-// MFMA accumulation chain drifts by ~1e-5 relative over 1024 steps; the
+// A group of kMfmaGrpSteps = 4 steps covers 128 bytes of each row.  A wave
+// loads its 32 rows x 128 bytes with fully coalesced 16-byte loads (load j:
+// rows 8j .. 8j+7, lane l at row 8j + l/8, chunk l%8), one group ahead of the
+// MFMAs, and passes them through its own LDS tile into the fragment layout
+// (step j of lane l: row l%32, chunk 2j + l/32; chunk c of row r is stored in
+// slot c ^ (r & 7), so neither side has bank conflicts).  Loading the
+// fragments straight from global memory (32 rows x 32 bytes per load) ran at
+// 158 us against 128 us this way at R = K = 16384, with the same results.
+// The x rows go through one buffer span per workgroup: rows past R read as
+// zeros; chunks of steps past the K chunk are read but never used.  The phi
+// fragments of a group are the same for all four waves, so the workgroup
+// stages them once in double-buffered LDS (one barrier per group) instead of
+// every wave loading them from L2 (per-wave phi loads competing with the x
+// stream had cost ~45 us).  Each 16-k step's three MFMAs start from zero and
+// the step result is added into `acc` with fp32 VALU adds (a long MFMA
+// accumulation chain drifts by ~1e-5 relative over 1024 steps; the
 // round-to-nearest adds do not).  Writes the same 25-float partial records as
 // dynw_partial_kernel: part[r][kc][0:24] and the row's sum of squares [24],
 // which the VALU forms from the A fragments alongside the MFMAs.  Requires
-// K % 16 == 0 and a 16-byte aligned x.
+// K % 16 == 0, a 16-byte aligned x and 128 rows of K under 2^31 bytes.
 constexpr int kMfmaRowsWg = 128;
 constexpr int kMfmaGrpSteps = 4;                             // 16-k steps per group
 constexpr int kMfmaPhiGrp = kMfmaGrpSteps * 3 * 64;          // 16-byte phi chunks per group
@@ -159,6 +166,7 @@ __global__ __launch_bounds__(kThreads) void dynw_mfma_kernel(const __bf16* __res
                                                              int64_t steps_per_chunk) {
   constexpr int G = kMfmaGrpSteps;
   __shared__ __attribute__((aligned(16))) u32x4 phs[2][kMfmaPhiGrp];
+  __shared__ __attribute__((aligned(16))) u32x4 ast[4][32 * 8];  // per wave: 32 rows x 8 chunks
   const int wave = threadIdx.x >> 6;
   const int lane = threadIdx.x & 63;
   const int64_t rb0 = (int64_t)blockIdx.x * kMfmaRowsWg + wave * 32;
@@ -169,16 +177,29 @@ __global__ __launch_bounds__(kThreads) void dynw_mfma_kernel(const __bf16* __res
   const int64_t ngrp = (s_end - s_beg + G - 1) / G;
   const int64_t row = rb0 + (lane & 31);
   const bool rok = row < R;
-  // Rows past R read nothing and contribute zeros.
-  const u32x4* ap = reinterpret_cast<const u32x4*>(x + (rok ? row : 0) * K + 8 * (lane >> 5));
+  const int lrow = lane >> 3, lchk = lane & 7;
+  const int64_t rbw = (int64_t)blockIdx.x * kMfmaRowsWg;
+  const int64_t nrow = R - rbw < kMfmaRowsWg ? R - rbw : kMfmaRowsWg;
+  const Span<__bf16, true> xs(x + rbw * K, nrow * K);
+  const uint32_t lbase = (uint32_t)((wave * 32 + lrow) * K + 8 * lchk);
   u32x4 a[2][G];
   u32x4 pv[kMfmaPhiPerThread];
   auto aload = [&](int64_t g, u32x4 (&d)[G]) {
+    const uint32_t kofs = (uint32_t)((s_beg + g * G) * 16);
 #pragma unroll
-    for (int j = 0; j < G; ++j) {
-      const int64_t s = s_beg + g * G + j;
-      d[j] = (rok && s < s_end) ? ap[s * 2] : u32x4{0u, 0u, 0u, 0u};
-    }
+    for (int j = 0; j < G; ++j) d[j] = xs.load16<false>(lbase + (uint32_t)(8 * j) * (uint32_t)K + kofs);
+  };
+  u32x4* tile = ast[wave];
+  auto astage = [&](const u32x4 (&raw)[G], u32x4 (&d)[G]) {
+#pragma unroll
+    for (int j = 0; j < G; ++j) tile[(8 * j + lrow) * 8 + (lchk ^ (lrow & 7))] = raw[j];
+    // Lanes read what other lanes of the wave wrote: keep the order.
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    const int fr = lane & 31;
+#pragma unroll
+    for (int j = 0; j < G; ++j) d[j] = tile[fr * 8 + ((2 * j + (lane >> 5)) ^ (fr & 7))];
   };
   // Group g's phi chunks are packed[(s_beg + g G) * 192 + c], c < kMfmaPhiGrp (0 past the end).
   auto pload = [&](int64_t g) {
@@ -220,7 +241,7 @@ __global__ __launch_bounds__(kThreads) void dynw_mfma_kernel(const __bf16* __res
       }
     }
   };
-  // Group g's A fragments sit in a[g % 2] and its phi in phs[g % 2]; the loop is
+  // Group g's loads sit in a[g % 2] and its phi in phs[g % 2]; the loop is
   // unrolled by two so that neither register set is copied.
   if (ngrp > 0) {
     aload(0, a[0]);
@@ -231,13 +252,17 @@ __global__ __launch_bounds__(kThreads) void dynw_mfma_kernel(const __bf16* __res
   __syncthreads();
   for (int64_t g = 0; g < ngrp; g += 2) {
     if (g + 1 < ngrp) aload(g + 1, a[1]);
-    compute(g, a[0], 0);
+    u32x4 f0[G];
+    astage(a[0], f0);
+    compute(g, f0, 0);
     if (g + 1 < ngrp) pstore(1);
     if (g + 2 < ngrp) pload(g + 2);
     __syncthreads();
     if (g + 1 >= ngrp) break;  // uniform
     if (g + 2 < ngrp) aload(g + 2, a[0]);
-    compute(g + 1, a[1], 1);
+    u32x4 f1[G];
+    astage(a[1], f1);
+    compute(g + 1, f1, 1);
     if (g + 2 < ngrp) pstore(0);
     if (g + 3 < ngrp) pload(g + 3);
     __syncthreads();
