@@ -407,7 +407,7 @@ extern "C" int mhc_layer_static_backward(const void* H, int dtype, const void* d
                                                    &nblk, st);
   });
   if (rc) return rc;
-  reduce_split_kernel<20, 4><<<dim3((unsigned)B, 5), kThreads, 0, st>>>(part, dpre, dres, (int)nblk);
+  reduce_split_kernel<20, 4><<<dim3((unsigned)B, 5), kRedThreads, 0, st>>>(part, dpre, dres, (int)nblk);
   if ((rc = hip_status(hipGetLastError(), "layer static reduce launch"))) return rc;
   static_weights_bwd_kernel<<<1, kThreads, 0, st>>>(H_pre_base, H_post_base, H_res_base, w, dpre, dH_post, dres,
                                                     grad_bias, B, iters);
@@ -448,6 +448,6 @@ extern "C" int mhc_layer_mix_backward(const void* H, int dtype, const void* d_br
                                                    &nblk, st);
   });
   if (rc) return rc;
-  reduce_split_kernel<20, 4><<<dim3((unsigned)B, 5), kThreads, 0, st>>>(part, dH_pre, dH_res, (int)nblk);
+  reduce_split_kernel<20, 4><<<dim3((unsigned)B, 5), kRedThreads, 0, st>>>(part, dH_pre, dH_res, (int)nblk);
   return hip_status(hipGetLastError(), "layer mix backward reduce launch");
 }

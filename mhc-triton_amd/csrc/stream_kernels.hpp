@@ -532,30 +532,41 @@ __global__ __launch_bounds__(kThreads) void collapse_kernel(const TH* __restrict
 // Final reduction of [B][nblk][NV] partials into up to two outputs:
 // out0[b*SPLIT + k] for k < SPLIT, out1[b*(NV-SPLIT) + k-SPLIT] otherwise.
 // Grid: x = batch, y = one 16-byte column (4 consecutive elements) of the
-// NV-float records (NV % 4 == 0, 16-byte aligned in the workspace).  Thread t
-// sums records t, t + 256, ... in index order, then block_sum adds the 256
-// per-thread sums: a fixed order, the same for every column split.
+// NV-float records (NV % 4 == 0, 16-byte aligned in the workspace), 1024
+// threads per workgroup.  Thread t sums records t, t + 1024, ... in index
+// order; each 16-lane row adds its threads' sums with DPP, and threads 0..3
+// add the 64 row sums in row order: a fixed order, the same for every column
+// split.  (With one batch the closure backward leaves 28672 records at config
+// 4; 256 threads took 8.3 us over them.)
+constexpr int kRedThreads = 1024;
+
 template <int NV, int SPLIT>
-__global__ __launch_bounds__(kThreads) void reduce_split_kernel(const float* __restrict__ part,
-                                                                float* __restrict__ out0,
-                                                                float* __restrict__ out1, int nblk) {
+__global__ __launch_bounds__(kRedThreads) void reduce_split_kernel(const float* __restrict__ part,
+                                                                   float* __restrict__ out0,
+                                                                   float* __restrict__ out1, int nblk) {
   static_assert(NV % 4 == 0, "records of whole 16-byte vectors");
-  __shared__ float lds[4 * 4];
+  constexpr int kRows = kRedThreads / 16;
+  __shared__ float lds[kRows * 4];
   const int64_t b = blockIdx.x;
   const int q = blockIdx.y;
   const f32x4* p = reinterpret_cast<const f32x4*>(part + b * nblk * NV) + q;
   f32x4 a4 = f32x4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll 8
-  for (int k = threadIdx.x; k < nblk; k += kThreads) a4 += p[(int64_t)k * (NV / 4)];
-  float acc[4] = {a4[0], a4[1], a4[2], a4[3]};
-  block_sum<4>(acc, lds);
-  if (threadIdx.x == 0) {
+#pragma unroll 4
+  for (int k = threadIdx.x; k < nblk; k += kRedThreads) a4 += p[(int64_t)k * (NV / 4)];
 #pragma unroll
-    for (int c = 0; c < 4; ++c) {
-      const int i = 4 * q + c;
-      if (i < SPLIT) out0[b * SPLIT + i] = acc[c];
-      else out1[b * (NV - SPLIT) + (i - SPLIT)] = acc[c];
-    }
+  for (int c = 0; c < 4; ++c) {
+    const float v = sum_all16(a4[c]);
+    if ((threadIdx.x & 15) == 0) lds[(threadIdx.x >> 4) * 4 + c] = v;
+  }
+  __syncthreads();
+  if (threadIdx.x < 4) {
+    const int c = threadIdx.x;
+    float t = 0.f;
+#pragma unroll 8
+    for (int r = 0; r < kRows; ++r) t += lds[r * 4 + c];
+    const int i = 4 * q + c;
+    if (i < SPLIT) out0[b * SPLIT + i] = t;
+    else out1[b * (NV - SPLIT) + (i - SPLIT)] = t;
   }
 }
 
