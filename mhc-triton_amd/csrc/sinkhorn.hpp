@@ -97,20 +97,24 @@ __device__ __forceinline__ void sk_round_backward(const float (&m)[16], float (&
 #pragma unroll
     for (int i = 0; i < 4; ++i) mc[4 * i + j] = mr[4 * i + j] * c[j];
   }
-  // Column normalisation: dmr[:,j] = (d[:,j] - <d[:,j], mc[:,j]>) / colsum_j.
+  // Column normalisation: dmr[:,j] = (d[:,j] - <d[:,j], mc[:,j]>) / colsum_j,
+  // evaluated as d c - <.,.> c: one FMA per element and one multiply per
+  // column instead of a subtract and a multiply per element.
 #pragma unroll
   for (int j = 0; j < 4; ++j) {
     const float dot = d[j] * mc[j] + d[4 + j] * mc[4 + j] + d[8 + j] * mc[8 + j] + d[12 + j] * mc[12 + j];
+    const float dc = dot * c[j];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) d[4 * i + j] = (d[4 * i + j] - dot) * c[j];
+    for (int i = 0; i < 4; ++i) d[4 * i + j] = __builtin_fmaf(d[4 * i + j], c[j], -dc);
   }
   // Row normalisation: dm[i,:] = (dmr[i,:] - <dmr[i,:], mr[i,:]>) / rowsum_i.
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
     const float dot = d[4 * i] * mr[4 * i] + d[4 * i + 1] * mr[4 * i + 1] + d[4 * i + 2] * mr[4 * i + 2] +
                       d[4 * i + 3] * mr[4 * i + 3];
+    const float dr = dot * r[i];
 #pragma unroll
-    for (int j = 0; j < 4; ++j) d[4 * i + j] = (d[4 * i + j] - dot) * r[i];
+    for (int j = 0; j < 4; ++j) d[4 * i + j] = __builtin_fmaf(d[4 * i + j], r[i], -dr);
   }
 }
 
