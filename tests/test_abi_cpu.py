@@ -68,6 +68,14 @@ def test_version_and_workspace_queries(lib):
     ws = lib.mhc_layer_workspace_bytes(4, 4096, 4096, 1)
     # grad_x [B, 4D] f32 dominates: at least 256 KiB here, and 256-byte granular
     assert ws >= 4 * 4 * 4096 * 4 and ws % 256 == 0
+    # The backward passes that run one workgroup per tile keep one partial record
+    # per tile: 256 lanes x one 16-byte vector, sized for the narrowest (fp32, 4
+    # elements); 20 floats for the mixing backward, 4 for the closure backward.
+    for B, S, D in ((4, 4096, 4096), (1, 8192, 7168), (16, 2048, 2048), (3, 5, 12)):
+        tiles = (S * D // 4 + 255) // 256
+        assert lib.mhc_stream_mix_backward_workspace_bytes(B, S, D, 1) >= B * tiles * 20 * 4
+        assert lib.mhc_add_residual_backward_workspace_bytes(B, S, D, 1) >= B * tiles * 4 * 4
+        assert lib.mhc_layer_workspace_bytes(B, S, D, 1) >= B * tiles * 20 * 4 + B * 4 * D * 4
 
 
 def test_host_side_validation_without_gpu(lib):
