@@ -787,7 +787,9 @@ __global__ __launch_bounds__(kThreads) void dynw_bwd_mfma_kernel(const __bf16* _
               *reinterpret_cast<const u32x4*>(&gxs[(xr + 16 * i) * kBwdXPitch + xc]);
       }
     }
-    __syncthreads();  // the tiles are rewritten by the next block
+    // No barrier here: every read of xs / ghi / glo / cf in this block came
+    // before the barrier above, and gxs is next written after the next
+    // block's first barrier, which waits for these reads.
   }
   // grad_phi: lane l, element i -> k = k0 + 32 wave + 8 (i / 4) + 4 (l / 32) + i % 4, j = l % 32.
   const int j = lane & 31;
