@@ -109,7 +109,8 @@ def test_sinkhorn_edge_cases():
 
 # --------------------------------------------------------------------------- stream mix
 
-MIX_SHAPES = [(2, 64, 256), (3, 7, 100), (1, 5, 130), (2, 1, 8)]
+# (2, 33, 136): several tiles with a partial last one on the 16-byte vector path for every dtype
+MIX_SHAPES = [(2, 64, 256), (3, 7, 100), (1, 5, 130), (2, 1, 8), (2, 33, 136)]
 
 
 def _weights(B, g):
