@@ -197,21 +197,21 @@ static int mix_bwd_dispatch(const void* dbi, const void* dhn, const void* H, con
                                                        D, nblk, st);
 }
 
-// Pass C of the dynamic backward: two tokens per workgroup (grad_x loaded
-// once for both), 2 workgroups per CU; both measured best at config-3 size.
+// Pass C of the dynamic backward: two tokens per lane (grad_x loaded once for
+// both), 2 workgroups per CU; both measured best at config-3 size.
 constexpr int kDhTokens = 2;
 
 template <typename T, int W, bool HAS_DHN>
 static int launch_dh(const T* dbi, const T* dhn, const float* gx, const float* w, T* dH, int64_t B, int64_t S,
                      int64_t D, hipStream_t st) {
-  const uint32_t ncb = (uint32_t)((D / W + kThreads - 1) / kThreads);
   const int64_t groups = (S + kDhTokens - 1) / kDhTokens;
-  if (ncb == 0 || groups == 0) return MHC_OK;
+  const int64_t items = groups * (D / W);  // (token group, column vector) pairs, < 2^32 by check_bsd
+  if (items == 0) return MHC_OK;
+  const unsigned nwg = (unsigned)((items + kThreads - 1) / kThreads);
   const float inv_S = 1.f / (float)S;
   return for_batch_chunks(B, [&](int64_t b0, int64_t nb) {
-    dh_kernel<T, W, kDhTokens, HAS_DHN, kNt>
-        <<<dim3((unsigned)(groups * ncb), (unsigned)nb), kThreads, occupancy_lds(2), st>>>(
-            dbi, dhn, gx, inv_S, WRow{w, kOut}, WRow{w + 8, kOut}, dH, S, D, ncb, b0);
+    dh_kernel<T, W, kDhTokens, HAS_DHN, kNt><<<dim3(nwg, (unsigned)nb), kThreads, occupancy_lds(2), st>>>(
+        dbi, dhn, gx, inv_S, WRow{w, kOut}, WRow{w + 8, kOut}, dH, S, D, (uint32_t)groups, b0);
     return hip_status(hipGetLastError(), "layer dH launch");
   });
 }

@@ -397,27 +397,34 @@ __global__ __launch_bounds__(kThreads) void mix_bwd_kernel(const T* __restrict__
 // ---------------------------------------------------------------------------
 // dH of the dynamic layer (pass C):
 //   dH[s,m,:] = pre[m] d_bi[s,:] + sum_n res[n,m] dHn[s,n,:] + grad_x[m,:] / S
-// grad_x (f32, [4][D] per batch) is the same for every token, so a workgroup
-// walks TT consecutive tokens of one 256*W-column block and loads its grad_x
-// slice once: per token a lane then issues 5 loads instead of 13 (at config-3
+// grad_x (f32, [4][D] per batch) is the same for every token, so a lane
+// handles one column vector for TT consecutive tokens and loads its grad_x
+// slice once: per token it then issues 5 loads instead of 13 (at config-3
 // size 212 -> 200 us).  Same arithmetic, in the same order, as the WRITE_DH
 // path of mix_bwd_kernel, so the results are bit-identical.
-// Grid: x = token group * ncb + column block (ncb blocks of 256 items), y =
-// batch within the launch.
+// Items are (token group, column vector) pairs, flattened as in the mixing
+// kernels: item i = blockIdx.x * 256 + lane is group i / nch, column i % nch,
+// so every lane has work whatever D is (with 256-wide column blocks, D = 7168
+// left one block in four half idle: pass C at config 4 ran at 76% of 8 TB/s).
+// Grid: x = ceil(groups * nch / 256), y = batch within the launch.
 // ---------------------------------------------------------------------------
 template <typename T, int W, int TT, bool HAS_DHN, int NT = 0, bool BUF = (W > 1)>
 __global__ __launch_bounds__(kThreads) void dh_kernel(const T* __restrict__ dbi, const T* __restrict__ dhn,
                                                       const float* __restrict__ gx, float inv_S, WRow pre,
                                                       WRow res, T* __restrict__ dH, int64_t S, int64_t D,
-                                                      uint32_t ncb, int64_t b0) {
+                                                      uint32_t groups, int64_t b0) {
   const int64_t b = b0 + blockIdx.y;
-  const uint32_t cblk = blockIdx.x % ncb;
-  const int64_t s0 = (int64_t)(blockIdx.x / ncb) * TT;
-  const int64_t c = (int64_t)cblk * kThreads + threadIdx.x;
-  if (c >= D / W) return;
-  const int64_t cw = c * W;
-  const int64_t t0 = b * S + s0;
-  const int64_t rest = S - s0;
+  const uint32_t nch = (uint32_t)(D / W);
+  const uint32_t i = blockIdx.x * (uint32_t)kThreads + threadIdx.x;
+  const uint32_t grp = i / nch;
+  if (grp >= groups) return;
+  const int64_t cw = (int64_t)(i - grp * nch) * W;
+  // Spans start at the workgroup's first token; dt0 is this lane's token offset in them.
+  const int64_t s_lo = (int64_t)((blockIdx.x * (uint32_t)kThreads) / nch) * TT;
+  const int64_t s0 = (int64_t)grp * TT;
+  const uint32_t dt0 = (uint32_t)(s0 - s_lo);
+  const int64_t t0 = b * S + s_lo;
+  const int64_t rest = S - s_lo;
   const Span<T, BUF> dbs(dbi + t0 * D, rest * D);
   const Span<T, BUF> dns(dhn + t0 * 4 * D, rest * 4 * D);
   const Span<T, BUF> dHs(dH + t0 * 4 * D, rest * 4 * D);
@@ -431,10 +438,11 @@ __global__ __launch_bounds__(kThreads) void dh_kernel(const T* __restrict__ dbi,
   for (int t = 0; t < TT; ++t) {
     const int64_t s = s0 + t;
     if (s >= S) break;
-    const uint32_t e4 = (uint32_t)t * 4 * (uint32_t)D + (uint32_t)cw;
+    const uint32_t dt = dt0 + (uint32_t)t;
+    const uint32_t e4 = dt * 4 * (uint32_t)D + (uint32_t)cw;
     Frag<T, W> bf;
     Frag<T, W> nf[4];
-    bf.template load<(NT & 1) != 0>(dbs, (uint32_t)t * (uint32_t)D + (uint32_t)cw);
+    bf.template load<(NT & 1) != 0>(dbs, dt * (uint32_t)D + (uint32_t)cw);
     if constexpr (HAS_DHN) {
 #pragma unroll
       for (int n = 0; n < 4; ++n) nf[n].template load<(NT & 1) != 0>(dns, e4 + n * (uint32_t)D);
