@@ -5,7 +5,7 @@
 // One matrix per lane: a wave handles 64 matrices, a 256-thread workgroup
 // 256.  Each lane reads its 16 entries with 16-byte loads (4 for fp32, 2 for
 // bf16/fp16); across the wave the accesses cover one contiguous span.  The
-// forward is VALU-bound at 20 rounds (48 VALU ops and 8 v_rcp per round in
+// forward is VALU-bound at 20 rounds (40 VALU ops and 8 v_rcp per round in
 // the scaling-vector form of sk_forward); the backward runs the checkpointed
 // reverse sweep of sinkhorn.hpp.
 #include "sinkhorn.hpp"

@@ -3,7 +3,7 @@
 // Forward (reference src/mhc/_torch_baseline.py:27-35, _kernels.py:75-112):
 //   P = |M| + eps;  repeat iters: P /= (rowsum(P) + eps); P /= (colsum(P) + eps)
 // Row and column sums are accumulated left to right as in the reference
-// (sk_forward carries the same iteration as two scaling vectors, below).
+// (sk_forward carries the same iteration as two reciprocal scaling vectors, below).
 // A division P/r is computed as P * rcp(r): one v_rcp_f32 per row/column
 // instead of four IEEE divides; the result stays within a few ulp of the
 // divided form (checked against an fp64 oracle by the parity tests).
@@ -53,27 +53,42 @@ __device__ __forceinline__ void sk_init(float (&m)[16], float eps) {
 }
 
 // The forward kernel's iteration in scaling-vector form: after any number of
-// rounds P = diag(u) P0 diag(v), so a row normalisation only updates u,
-//   u_i <- u_i * rcp(u_i * (P0 v)_i + eps)      ((P0 v)_i: one mul + 3 FMAs),
-// and a column normalisation only v, with P formed once at the end.  That is
-// the same sequence of normalisations, at 48 VALU + 8 v_rcp per round instead
-// of 64 + 8: at 2^20 matrices 41.4 us against 51.6 us for sk_round's explicit
-// update, with the same error against an fp64 evaluation of the explicit form
-// (2.2e-7 normwise).  The backward keeps sk_round for its recomputed states.
+// rounds P = diag(u) P0 diag(v), and the kernel carries w = 1/u and z = 1/v.
+// A row normalisation u_i <- u_i / (u_i (P0 v)_i + eps) is then
+//   w_i <- (P0 v)_i + eps w_i          (one mul + 3 FMAs for the dot, one FMA)
+// with v = rcp(z), and a column normalisation likewise updates z from
+// u = rcp(w); P is formed once at the end.  That is the same sequence of
+// normalisations at 40 VALU + 8 v_rcp per round, against 64 + 8 for
+// sk_round's explicit update (at 2^20 matrices 41 us against 52 us; 48 + 8
+// when carrying u and v themselves), with a normwise error against an fp64
+// evaluation of the explicit form of 1.7e-7 (2.2e-7 for the explicit fp32
+// update).  The backward keeps sk_round for its recomputed states.
 __device__ __forceinline__ void sk_forward(float (&m)[16], int iters, float eps) {
   sk_init(m, eps);
-  float u[4] = {1.f, 1.f, 1.f, 1.f}, v[4] = {1.f, 1.f, 1.f, 1.f};
+  float w[4] = {1.f, 1.f, 1.f, 1.f}, z[4] = {1.f, 1.f, 1.f, 1.f};
   for (int t = 0; t < iters; ++t) {
+    float v[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) v[j] = fast_rcp(z[j]);
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const float dot = m[4 * i] * v[0] + m[4 * i + 1] * v[1] + m[4 * i + 2] * v[2] + m[4 * i + 3] * v[3];
-      u[i] *= fast_rcp(u[i] * dot + eps);
+      w[i] = __builtin_fmaf(eps, w[i], dot);
     }
+    float u[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) u[i] = fast_rcp(w[i]);
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
       const float dot = u[0] * m[j] + u[1] * m[4 + j] + u[2] * m[8 + j] + u[3] * m[12 + j];
-      v[j] *= fast_rcp(v[j] * dot + eps);
+      z[j] = __builtin_fmaf(eps, z[j], dot);
     }
+  }
+  float u[4], v[4];
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    u[k] = fast_rcp(w[k]);
+    v[k] = fast_rcp(z[k]);
   }
 #pragma unroll
   for (int i = 0; i < 4; ++i)
