@@ -205,7 +205,6 @@ extern "C" int mhc_dynamic_weights_backward(const void* x, int dtype_x, const fl
       rowbuf, R, K, iters, eps);
   if (int rc = hip_status(hipGetLastError(), "dynamic_weights_backward rows launch")) return rc;
   const bool phi_vec = aligned16(phi);
-  const unsigned nwide = K > 0 ? (unsigned)((K + kWideThreads - 1) / kWideThreads) : 1u;
   const WidePlan w = wide_plan(R, K);
   float* gphi_part =
       (w.nR > 1 && grad_phi) ? (float*)((char*)workspace + align256((size_t)R * kRow * sizeof(float))) : nullptr;
@@ -218,9 +217,9 @@ extern "C" int mhc_dynamic_weights_backward(const void* x, int dtype_x, const fl
     rc = hip_status(hipGetLastError(), "dynamic_weights_backward mfma launch");
   } else {
     rc = MHC_DISPATCH_DTYPE(dtype_x, [&] {
-      dynw_bwd_wide_kernel<T, T, kWideThreads><<<dim3(nwide, (unsigned)w.nR), kWideThreads, 0, st>>>(
-          (const T*)x, phi, rowbuf, (T*)grad_x, grad_phi, gphi_part, grad_bias, grad_alpha, R, K, w.RC, phi_vec);
-      return hip_status(hipGetLastError(), "dynamic_weights_backward wide launch");
+      return hip_status(launch_dynw_bwd_wide<T, T>((const T*)x, phi, rowbuf, (T*)grad_x, grad_phi, gphi_part,
+                                                   grad_bias, grad_alpha, R, K, w.RC, (unsigned)w.nR, phi_vec, st),
+                        "dynamic_weights_backward wide launch");
     });
   }
   if (rc || !gphi_part) return rc;

@@ -531,11 +531,12 @@ __global__ __launch_bounds__(kThreads) void dynw_bwd_rows_kernel(const float* __
 // chunks in order.  The per-row record is the same for every thread of the
 // workgroup (scalar loads).  Workgroup (0, 0) also sums the per-row records
 // into grad_bias [24] and grad_alpha [3] (threads stride over rows, then a
-// fixed-order block sum).  Launched with kWideThreads = 64 (one wave) per
-// workgroup: the work is a few loads and ~50 FMAs per k, so the pass is
-// latency-bound and wants every CU busy -- at the layer's R = 4, K = 16384,
-// 256 one-wave workgroups take 3.1 us against 6.6 us for 64 of 256 threads,
-// with the same results.
+// fixed-order block sum).  launch_dynw_bwd_wide picks one-wave workgroups
+// (kWideThreads = 64) when R <= 64: the work is then a few loads and ~50 FMAs
+// per k, so the pass is latency-bound and wants every CU busy -- at the
+// layer's R = 4, K = 16384, 256 one-wave workgroups take 3.1 us against 6.6 us
+// for 64 of 256 threads, with the same results.  With more rows it keeps 256
+// threads, so that workgroup (0, 0)'s walk over the rows stays short.
 constexpr int kWideThreads = 64;
 
 template <typename TX, typename TG, int NT = kThreads>
@@ -589,6 +590,22 @@ __global__ __launch_bounds__(NT) void dynw_bwd_wide_kernel(const TX* __restrict_
 #pragma unroll
     for (int j = 0; j < kOut; ++j) o[(gphi_part ? 0 : k * kOut) + j] = gp[j];
   }
+}
+
+template <typename TX, typename TG>
+inline hipError_t launch_dynw_bwd_wide(const TX* x, const float* phi, const float* rowbuf, TG* gx, float* gphi,
+                                       float* gphi_part, float* gbias, float* galpha, int64_t R, int64_t K,
+                                       int64_t RC, unsigned nR, bool phi_vec, hipStream_t st) {
+  if (R <= kWideThreads) {
+    const unsigned ncol = K > 0 ? (unsigned)((K + kWideThreads - 1) / kWideThreads) : 1u;
+    dynw_bwd_wide_kernel<TX, TG, kWideThreads><<<dim3(ncol, nR), kWideThreads, 0, st>>>(
+        x, phi, rowbuf, gx, gphi, gphi_part, gbias, galpha, R, K, RC, phi_vec);
+  } else {
+    const unsigned ncol = K > 0 ? (unsigned)((K + kThreads - 1) / kThreads) : 1u;
+    dynw_bwd_wide_kernel<TX, TG, kThreads><<<dim3(ncol, nR), kThreads, 0, st>>>(
+        x, phi, rowbuf, gx, gphi, gphi_part, gbias, galpha, R, K, RC, phi_vec);
+  }
+  return hipGetLastError();
 }
 
 // The wide pass for many bf16 rows (the standalone op at R = tokens), both

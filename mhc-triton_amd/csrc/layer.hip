@@ -370,10 +370,10 @@ extern "C" int mhc_layer_dynamic_backward(const void* H, int dtype, const void* 
       aux, P, InRow{w, kOut}, InRow{nullptr, 0}, InRow{dH_post, 4}, InRow{nullptr, 0}, part, (int)nblk, rowbuf, B,
       K, iters, eps);
   if ((rc = hip_status(hipGetLastError(), "layer weights backward rows launch"))) return rc;
-  dynw_bwd_wide_kernel<float, float, kWideThreads>
-      <<<dim3(K > 0 ? (unsigned)((K + kWideThreads - 1) / kWideThreads) : 1u), kWideThreads, 0, st>>>(
-          x, phi, rowbuf, dH ? gx : nullptr, grad_phi, nullptr, grad_bias, grad_alpha, B, K, B, aligned16(phi));
-  if ((rc = hip_status(hipGetLastError(), "layer weights backward wide launch"))) return rc;
+  if ((rc = hip_status(launch_dynw_bwd_wide<float, float>(x, phi, rowbuf, dH ? gx : nullptr, grad_phi, nullptr,
+                                                          grad_bias, grad_alpha, B, K, B, 1u, aligned16(phi), st),
+                       "layer weights backward wide launch")))
+    return rc;
   if (!dH || S * D == 0) return MHC_OK;
   // Pass C: dH.
   return MHC_DISPATCH_DTYPE(dtype, [&] { return dh_dispatch<T>(d_branch_input, dH_new, gx, w, dH, B, S, D, st); });
