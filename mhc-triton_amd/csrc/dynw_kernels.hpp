@@ -614,9 +614,10 @@ inline hipError_t launch_dynw_bwd_wide(const TX* x, const float* phi, const floa
 //   grad_phi [K, 24] = x^T [K, R] G [R, 24]                      (f32, per chunk)
 // with G = grad_raw = rowbuf[r][0:24] and coef = rowbuf[r][24].  A workgroup
 // owns 128 columns (wave w: the 32-column block at 32 w) and a chunk of RC
-// rows, walked in 32-row blocks.  Per block the x tile (bf16) and the G rows
-// are staged in LDS with 16-byte loads, the next block's loads being in flight
-// meanwhile.  G is split into bf16 hi + lo planes once, as it is staged (fp32
+// rows, walked in 64-row blocks (two barriers each; with 32-row blocks the
+// kernel took 234.9 us against 224.3 us at R = K = 16384, same results).  Per
+// block the x tile (bf16) and the G rows are staged in LDS with 16-byte loads,
+// the next block's loads being in flight meanwhile.  G is split into bf16 hi + lo planes once, as it is staged (fp32
 // products then take hi*hi + hi*lo + lo*hi, relative error ~2^-16):
 //   grad_x: computed transposed, grad_x^T = phi G^T, so that the A operand is
 //           the workgroup's phi fragments (registers for the whole kernel) and
@@ -635,7 +636,7 @@ inline hipError_t launch_dynw_bwd_wide(const TX* x, const float* phi, const floa
 // outputs as dynw_bwd_wide_kernel: grad_phi direct with one chunk, else
 // per-chunk partials; workgroup (0, 0) also sums grad_bias and grad_alpha.
 constexpr int kBwdCols = 128;             // columns per workgroup: one 32-column block per wave
-constexpr int kBwdRows = 32;              // rows per staged block
+constexpr int kBwdRows = 64;              // rows per staged block (two 32-row MFMA halves)
 constexpr int kBwdXPitch = kBwdCols + 8;  // bf16 per padded LDS row of the x / grad_x tiles
 constexpr int kBwdGPitch = 40;            // bf16 per LDS row of the split G planes (columns 24..31 zero)
 
@@ -658,7 +659,7 @@ __global__ __launch_bounds__(kThreads) void dynw_bwd_mfma_kernel(const __bf16* _
                                                                  float* __restrict__ gbias,
                                                                  float* __restrict__ galpha, int64_t R, int64_t K,
                                                                  int64_t RC) {
-  constexpr int TR = kBwdRows;
+  constexpr int TR = kBwdRows, NX = TR / 16, NG = TR / 32;
   __shared__ __attribute__((aligned(16))) __bf16 xs[TR * kBwdXPitch];
   __shared__ __attribute__((aligned(16))) __bf16 gxs[TR * kBwdXPitch];
   __shared__ __attribute__((aligned(16))) __bf16 ghi[TR * kBwdGPitch];
@@ -709,18 +710,21 @@ __global__ __launch_bounds__(kThreads) void dynw_bwd_mfma_kernel(const __bf16* _
   const bool xcol_ok = k0 + xc < K;
   const int grow = threadIdx.x >> 3;
   const int gcol = (threadIdx.x & 7) * 4;
-  u32x4 xv[2];
-  f32x4 gv;
+  u32x4 xv[NX];
+  f32x4 gv[NG];
   auto load_block = [&](int64_t r0) {
 #pragma unroll
-    for (int i = 0; i < 2; ++i) {
+    for (int i = 0; i < NX; ++i) {
       const int64_t r = r0 + xr + 16 * i;
       xv[i] = (r < r_end && xcol_ok) ? *reinterpret_cast<const u32x4*>(x + r * K + k0 + xc)
                                      : u32x4{0u, 0u, 0u, 0u};
     }
-    const int64_t r = r0 + grow;
-    gv = (r < r_end && gcol < 28) ? *reinterpret_cast<const f32x4*>(rowbuf + r * kRow + gcol)
-                                  : f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int j = 0; j < NG; ++j) {
+      const int64_t r = r0 + grow + 32 * j;
+      gv[j] = (r < r_end && gcol < 28) ? *reinterpret_cast<const f32x4*>(rowbuf + r * kRow + gcol)
+                                       : f32x4{0.f, 0.f, 0.f, 0.f};
+    }
   };
   // Transpose-read addresses: 16-lane group gi = lane / 16 covers columns 16 (gi & 1) .. +15 of
   // the wave's 32 and rows 8 (gi >> 1) + 0..3 of a 16-row step (+4 for the second read).
@@ -735,36 +739,40 @@ __global__ __launch_bounds__(kThreads) void dynw_bwd_mfma_kernel(const __bf16* _
   for (int64_t r0 = r_beg; r0 < r_end; r0 += TR) {
     // Stage this block: x as loaded, G split into hi + lo planes, coef apart.
 #pragma unroll
-    for (int i = 0; i < 2; ++i) *reinterpret_cast<u32x4*>(&xs[(xr + 16 * i) * kBwdXPitch + xc]) = xv[i];
-    {
+    for (int i = 0; i < NX; ++i) *reinterpret_cast<u32x4*>(&xs[(xr + 16 * i) * kBwdXPitch + xc]) = xv[i];
+#pragma unroll
+    for (int jj = 0; jj < NG; ++jj) {
+      const int gr = grow + 32 * jj;
       bf16x4 h4, l4;
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
-        const float v = gcol < kOut ? gv[e] : 0.f;
+        const float v = gcol < kOut ? gv[jj][e] : 0.f;
         const __bf16 h = (__bf16)v;
         h4[e] = h;
         l4[e] = (__bf16)(v - (float)h);
       }
-      *reinterpret_cast<bf16x4*>(&ghi[grow * kBwdGPitch + gcol]) = h4;
-      *reinterpret_cast<bf16x4*>(&glo[grow * kBwdGPitch + gcol]) = l4;
-      if (gcol == kOut) cf[grow] = gv[0];
+      *reinterpret_cast<bf16x4*>(&ghi[gr * kBwdGPitch + gcol]) = h4;
+      *reinterpret_cast<bf16x4*>(&glo[gr * kBwdGPitch + gcol]) = l4;
+      if (gcol == kOut) cf[gr] = gv[jj][0];
     }
     __syncthreads();
     if (r0 + TR < r_end) load_block(r0 + TR);  // in flight during the compute below
-    // grad_x^T = phi G^T (see above); smallest products first, hi x hi last.
+#pragma unroll
+    for (int hh = 0; hh < NG; ++hh) {
+    // grad_x^T = phi G^T (see above) for each 32-row half; smallest products first, hi x hi last.
     f32x16 d = zero;
 #pragma unroll
     for (int js = 0; js < 2; ++js) {
       const int j0 = 16 * js + 8 * (lane >> 5);
-      const bf16x8 ghv = *reinterpret_cast<const bf16x8*>(&ghi[(lane & 31) * kBwdGPitch + j0]);
-      const bf16x8 glv = *reinterpret_cast<const bf16x8*>(&glo[(lane & 31) * kBwdGPitch + j0]);
+      const bf16x8 ghv = *reinterpret_cast<const bf16x8*>(&ghi[(32 * hh + (lane & 31)) * kBwdGPitch + j0]);
+      const bf16x8 glv = *reinterpret_cast<const bf16x8*>(&glo[(32 * hh + (lane & 31)) * kBwdGPitch + j0]);
       d = __builtin_amdgcn_mfma_f32_32x32x16_bf16(bhi[js], glv, d, 0, 0, 0);
       d = __builtin_amdgcn_mfma_f32_32x32x16_bf16(blo[js], ghv, d, 0, 0, 0);
       d = __builtin_amdgcn_mfma_f32_32x32x16_bf16(bhi[js], ghv, d, 0, 0, 0);
     }
     // Epilogue: lane l holds row l % 32, columns 32 wave + 8 q + 4 (l / 32) + 0..3 in d[4 q ..].
     {
-      const int row = lane & 31;
+      const int row = 32 * hh + (lane & 31);
       const float c = cf[row];
 #pragma unroll
       for (int q = 0; q < 4; ++q) {
@@ -776,10 +784,11 @@ __global__ __launch_bounds__(kThreads) void dynw_bwd_mfma_kernel(const __bf16* _
         *reinterpret_cast<bf16x4*>(&gxs[row * kBwdXPitch + cc]) = o4;
       }
     }
-    // grad_phi += x^T G over the block's two 16-row steps.  A = x^T (lane l: column
+    }
+    // grad_phi += x^T G over the block's 16-row steps.  A = x^T (lane l: column
     // 32 wave + l % 32, rows 16 st + 8 (l / 32) + e), B = G (same rows, j = l % 32).
 #pragma unroll
-    for (int st = 0; st < 2; ++st) {
+    for (int st = 0; st < TR / 16; ++st) {
       const int rb = 16 * st + tr_row;
       const u32x2 x0 = lds_read_tr16(&xs[rb * kBwdXPitch + 32 * wave + tr_col]);
       const u32x2 x1 = lds_read_tr16(&xs[(rb + 4) * kBwdXPitch + 32 * wave + tr_col]);
@@ -797,7 +806,7 @@ __global__ __launch_bounds__(kThreads) void dynw_bwd_mfma_kernel(const __bf16* _
     // grad_x tile out: rows xr + 16 i, 16 bytes at column xc.
     if (gx && xcol_ok) {
 #pragma unroll
-      for (int i = 0; i < 2; ++i) {
+      for (int i = 0; i < NX; ++i) {
         const int64_t r = r0 + xr + 16 * i;
         if (r < r_end)
           *reinterpret_cast<u32x4*>(gx + r * K + k0 + xc) =
