@@ -78,8 +78,9 @@ def _parse():
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--workload", default="config3", choices=sorted(WORKLOADS))
-    ap.add_argument("--cpu-seconds", type=float, default=12.0,
-                    help="target CPU time of the cpu_baseline sample (0 disables it)")
+    ap.add_argument("--cpu-reps", type=int, default=3,
+                    help="timed runs of the cpu_baseline leg at the workload's shape, after one warm-up "
+                         "(0 disables it)")
     ap.add_argument("--ops", action="store_true",
                     help="time the low-level ops one by one (config-2 Sinkhorn, the stream ops and "
                          "expand / collapse at config-3 size, dynamic weights) and exit")
@@ -406,17 +407,20 @@ def _gpu_leg(cfg, steps, warmup):
                 elem=H.element_size(), device=torch.cuda.get_device_name(dev))
 
 
-def _cpu_leg(cfg, target_s):
-    """The reference's pure-PyTorch layer (restated in oracle/torch_path.py),
-    forward + autograd backward on the host cores, fp32-upcast (the reference's
-    own torch path raises on bf16 H with fp32 weights), on a bounded sample of
-    the workload: the same dim, batch rows of a shorter sequence."""
+def _cpu_leg(cfg, reps: int = 3, seq: int | None = None):
+    """The reference's pure-PyTorch layer (restated in oracle/torch_path.py), on the host
+    cores, at the workload's own shape (B, S, D): forward, and forward + autograd backward,
+    fp32-upcast (the reference's own torch path raises on bf16 H with fp32 weights,
+    _torch_baseline.py:136,141).  One warm-up run, then the median of `reps` runs, as the
+    reference's benchmark times its large cases.  `seq` shortens the sequence (tests only)."""
+    import statistics
+
     import torch
 
     from oracle import torch_path
 
     B, D = cfg["B"], cfg["D"]
-    S = 64
+    S = cfg["S"] if seq is None else seq
     g = torch.Generator()
     g.manual_seed(0)
     p = {
@@ -433,29 +437,40 @@ def _cpu_leg(cfg, target_s):
     dHn = torch.randn((B, S, 4, D), generator=g)
     dbi = torch.randn((B, S, D), generator=g)
 
-    def once():
+    def fwd_bwd():
         torch_path.layer_grads(p, H, bo, dHn, dbi, dynamic=cfg["dynamic"], fused=True)
 
-    once()  # warm-up
-    n, t = 0, time.perf_counter()
-    while n < 3 or time.perf_counter() - t < 1.0:
-        once()
-        n += 1
-    one = (time.perf_counter() - t) / n
-    reps = max(1, int(target_s / max(one, 1e-6)))
-    t = time.perf_counter()
-    for _ in range(reps):
-        once()
-    el = time.perf_counter() - t
-    tokens = B * S * reps
+    def fwd():
+        with torch.no_grad():
+            torch_path.layer_forward(p, H, bo, dynamic=cfg["dynamic"], fused=True)
+
+    def median_s(fn, label):
+        t = time.perf_counter()
+        fn()  # warm-up (first touch of the working set)
+        _log(f"bench: cpu {label} warm-up {time.perf_counter() - t:.2f} s")
+        runs = []
+        for i in range(reps):
+            t = time.perf_counter()
+            fn()
+            runs.append(time.perf_counter() - t)
+            _log(f"bench: cpu {label} run {i + 1}/{reps} {runs[-1]:.2f} s")
+        return statistics.median(runs), runs
+
+    t_fb, runs_fb = median_s(fwd_bwd, "fwd+bwd")
+    t_f, _ = median_s(fwd, "fwd")
+    T = B * S
     return {
-        "value": round(tokens / el, 1),
+        "value": round(T / t_fb, 1),
         "unit": "tokens/s",
         "cores": torch.get_num_threads(),
         "kind": "port",
-        "sample": (f"torch CPU fp32 restatement of the reference's pure-PyTorch layer fwd+bwd, "
-                   f"B={B} S={S} D={D} ({'dynamic' if cfg['dynamic'] else 'static'}), "
-                   f"{reps} reps in {el:.1f} s"),
+        "sample": (f"the whole workload: torch CPU fp32 restatement of the reference's pure-PyTorch layer, "
+                   f"B={B} S={S} D={D} ({'dynamic fused' if cfg['dynamic'] else 'static'}), fwd + autograd bwd, "
+                   f"median of {reps} runs after 1 warm-up"),
+        "ms_per_step": round(t_fb * 1e3, 1),
+        "runs_s": [round(r, 3) for r in runs_fb],
+        "fwd_only_tokens_per_s": round(T / t_f, 1),
+        "torch_version": torch.__version__,
         "host_cpus": os.cpu_count(),
         "host_cpu_model": _cpu_model(),
     }
@@ -521,9 +536,9 @@ def main() -> int:
          f"H_new kernel {r['add_ms'] * 1e3:.1f} us")
 
     cpu = None
-    if args.cpu_seconds > 0:
+    if args.cpu_reps > 0:
         _log("bench: cpu baseline ...")
-        cpu = _cpu_leg(cfg, args.cpu_seconds)
+        cpu = _cpu_leg(cfg, args.cpu_reps)
         _log(f"bench: cpu {cpu['value']} tokens/s on {cpu['cores']} threads")
 
     add_gbs = add_bytes / (r["add_ms"] * 1e-3) / 1e9

@@ -6,48 +6,30 @@ The reference composes ``H.mean`` -> ``fused_dynamic_weights`` ->
 that never materialise ``H_residual``:
 
 * node A (``_DynamicLayer`` / ``_StaticLayer`` / ``_GenericLayer``):
-  ``H -> (branch_input, w)`` where ``w`` [B,24] f32 packs H_pre (0:4),
-  H_post (4:8) and H_res (8:24);
-* node B (``_LayerAdd``, the closure): ``(H, branch_output, w) -> H_new``,
+  ``H -> (branch_input, w, link)`` where ``w`` [B,24] f32 packs H_pre (0:4),
+  H_post (4:8) and H_res (8:24), and ``link`` is a view of ``H`` that only the
+  closure consumes;
+* node B (``_LayerAdd``, the closure): ``(link, branch_output, w) -> H_new``,
   recomputing ``H_res @ H`` on the fly.
 
-Node B consumes ``w``, so the autograd engine runs node B's backward before
-node A's.  Node B's backward computes ``d branch_output`` and ``dH_post`` and,
-instead of returning its share of ``dH`` (which the engine would have to add to
-node A's in another full pass), hands ``dH_new`` and ``dH_post`` to node A
-through a shared ``_Stash``; node A then writes the complete ``dH`` once.
-Node B returns no gradient for ``H`` or ``w``.
+Node B consumes ``link`` and ``w``, so the autograd engine runs node B's
+backward before node A's.  Node B's backward computes ``d branch_output`` and
+``dH_post`` and, instead of its true share of ``dH`` (which the engine would have
+to add to node A's in another full pass), returns ``dH_new`` as the link's
+gradient and ``dH_post`` in columns 4:8 of ``w``'s gradient.  Node A's backward
+reads both and writes the complete ``dH`` once.  The engine sums the closure's
+gradients when it is called more than once, and a backward call that reaches
+node B but not node A leaves no state behind.  The traced path (``_library.py``)
+uses the same wiring on the ``torch.ops.mhc`` ops.
 """
 
 from __future__ import annotations
 
-from typing import List, Optional, Tuple
+from typing import Optional
 
 import torch
 
 from . import _lib
-
-
-class _Stash:
-    """Per-forward-call channel from node B's backward to node A's backward."""
-
-    __slots__ = ("items",)
-
-    def __init__(self):
-        self.items: List[Tuple[torch.Tensor, torch.Tensor]] = []
-
-    def put(self, dH_new: torch.Tensor, dH_post: torch.Tensor) -> None:
-        self.items.append((dH_new, dH_post))
-
-    def take(self) -> Tuple[Optional[torch.Tensor], Optional[torch.Tensor]]:
-        items, self.items = self.items, []
-        if not items:
-            return None, None
-        dH_new, dH_post = items[0]
-        for a, b in items[1:]:  # the closure was called more than once
-            dH_new = dH_new + a
-            dH_post = dH_post + b
-        return dH_new, dH_post
 
 
 def _f32(t: torch.Tensor) -> torch.Tensor:
@@ -241,28 +223,31 @@ def add_backward(dH_new, branch_output, w):
     return d_bo, dH_post
 
 
+def _link_dH_post(d_w: Optional[torch.Tensor]) -> Optional[torch.Tensor]:
+    """dH_post, as the closure's backward stores it in w's gradient (columns 4:8)."""
+    return None if d_w is None else d_w[:, 4:8].contiguous()
+
+
 class _DynamicLayer(torch.autograd.Function):
-    """Node A, dynamic fused weights (module.py:119-139 + 177)."""
+    """Node A, dynamic fused weights (module.py:119-139 + 177): H -> (branch_input, w, link)."""
 
     @staticmethod
     def forward(ctx, H, phi, H_pre_base, H_post_base, H_res_base, alpha_pre, alpha_post, alpha_res,
-                stash: _Stash, iters: int, eps: float):
+                iters: int, eps: float):
         params = (phi, H_pre_base, H_post_base, H_res_base, alpha_pre, alpha_post, alpha_res)
         bi, x, w, aux = dynamic_forward(H, *params, iters, eps)
         ctx.save_for_backward(H, x, w, aux, *params)
-        ctx.stash = stash
         ctx.iters = iters
         ctx.eps = eps
         ctx.set_materialize_grads(False)
-        return bi, w
+        return bi, w, H.view_as(H)
 
     @staticmethod
-    def backward(ctx, d_bi, d_w):
+    def backward(ctx, d_bi, d_w, d_link):
         H, x, w, aux, *params = ctx.saved_tensors
-        dH_new, dH_post = ctx.stash.take()
-        dH, gphi, gbias, galpha = dynamic_backward(H, d_bi, dH_new, dH_post, *params, x, w, aux, ctx.iters,
-                                                   ctx.eps, need_dH=ctx.needs_input_grad[0])
-        return (dH, *_dynamic_param_grads(params, gphi, gbias, galpha), None, None, None)
+        dH, gphi, gbias, galpha = dynamic_backward(H, d_bi, d_link, _link_dH_post(d_w), *params, x, w, aux,
+                                                   ctx.iters, ctx.eps, need_dH=ctx.needs_input_grad[0])
+        return (dH, *_dynamic_param_grads(params, gphi, gbias, galpha), None, None)
 
 
 def _dynamic_param_grads(params, gphi, gbias, galpha):
@@ -278,71 +263,62 @@ def _static_param_grads(params, gbias):
 
 
 class _StaticLayer(torch.autograd.Function):
-    """Node A, static weights (module.py:108-117 + 177)."""
+    """Node A, static weights (module.py:108-117 + 177): H -> (branch_input, w, link)."""
 
     @staticmethod
-    def forward(ctx, H, H_pre_base, H_post_base, H_res_base, stash: _Stash, iters: int):
+    def forward(ctx, H, H_pre_base, H_post_base, H_res_base, iters: int):
         params = (H_pre_base, H_post_base, H_res_base)
         bi, w = static_forward(H, *params, iters)
         ctx.save_for_backward(H, w, *params)
-        ctx.stash = stash
         ctx.iters = iters
         ctx.set_materialize_grads(False)
-        return bi, w
+        return bi, w, H.view_as(H)
 
     @staticmethod
-    def backward(ctx, d_bi, d_w):
+    def backward(ctx, d_bi, d_w, d_link):
         H, w, *params = ctx.saved_tensors
-        dH_new, dH_post = ctx.stash.take()
-        dH, gbias = static_backward(H, d_bi, dH_new, dH_post, *params, w, ctx.iters,
+        dH, gbias = static_backward(H, d_bi, d_link, _link_dH_post(d_w), *params, w, ctx.iters,
                                     need_dH=ctx.needs_input_grad[0])
-        return (dH, *_static_param_grads(params, gbias), None, None)
-
-
-def _generic_w_grad(dpre, dres, dH_post, d_w, B, dev):
-    gw = torch.zeros(B, 24, device=dev, dtype=torch.float32)
-    gw[:, 0:4] = dpre
-    gw[:, 8:24] = dres
-    if dH_post is not None:
-        gw[:, 4:8] = dH_post
-    if d_w is not None:
-        gw = gw + d_w
-    return gw
+        return (dH, *_static_param_grads(params, gbias), None)
 
 
 class _GenericLayer(torch.autograd.Function):
     """Node A for weights produced by torch ops (the unfused dynamic path,
-    module.py:141-163): (H, w) -> (branch_input, w), differentiable in w."""
+    module.py:141-163): (H, w) -> (branch_input, w, link), differentiable in w."""
 
     @staticmethod
-    def forward(ctx, H, w_in, stash: _Stash):
+    def forward(ctx, H, w_in):
         w = _f32(w_in)
         bi = branch_input(H, w)
         ctx.save_for_backward(H, w)
-        ctx.stash = stash
         ctx.w_dtype = w_in.dtype
         ctx.set_materialize_grads(False)
-        return bi, w
+        return bi, w.clone() if w is w_in else w, H.view_as(H)
 
     @staticmethod
-    def backward(ctx, d_bi, d_w):
+    def backward(ctx, d_bi, d_w, d_link):
         H, w = ctx.saved_tensors
-        dH_new, dH_post = ctx.stash.take()
-        dH, dpre, dres = mix_backward(H, d_bi, dH_new, w, need_dH=ctx.needs_input_grad[0])
-        gw = _generic_w_grad(dpre, dres, dH_post, d_w, H.shape[0], H.device)
-        return dH, gw.to(ctx.w_dtype), None
+        dH, dpre, dres = mix_backward(H, d_bi, d_link, w, need_dH=ctx.needs_input_grad[0])
+        gw = torch.cat([dpre, torch.zeros_like(dpre), dres], dim=1)
+        if d_w is not None:
+            gw = gw + d_w  # columns 4:8 carry the closure's dH_post
+        return dH, gw.to(ctx.w_dtype)
 
 
 class _LayerAdd(torch.autograd.Function):
-    """Node B, the closure: H_new = H_res @ H + H_post * branch_output
-    (module.py:179-180 with H_residual recomputed from H)."""
+    """Node B, the closure: (link, branch_output, w) -> H_new = H_res @ H + H_post * branch_output
+    (module.py:179-180 with H_residual recomputed from H).
+
+    Its backward returns dH_new as the link's gradient and dH_post in columns 4:8 of w's
+    gradient.  Neither is the true gradient of that input: both only reach node A, which
+    folds dH_new into dH (one pass) and dH_post into the H_post weight gradients.  A backward
+    call that reaches node B but not node A leaves nothing behind."""
 
     @staticmethod
-    def forward(ctx, H, branch_output, w, stash: _Stash):
-        H_new = add_forward(H, branch_output, w)
+    def forward(ctx, link, branch_output, w):
+        H_new = add_forward(link, branch_output, w)
         ctx.save_for_backward(branch_output, w)
-        ctx.stash = stash
-        ctx.h_dtype = H.dtype
+        ctx.h_dtype = link.dtype
         return H_new
 
     @staticmethod
@@ -350,6 +326,7 @@ class _LayerAdd(torch.autograd.Function):
         bo, w = ctx.saved_tensors
         dH_new = dH_new.contiguous().to(ctx.h_dtype)
         d_bo, dH_post = add_backward(dH_new, bo, w)
+        d_w = None
         if ctx.needs_input_grad[2]:
-            ctx.stash.put(dH_new, dH_post)
-        return None, d_bo, None, None
+            d_w = torch.nn.functional.pad(dH_post, (4, 16))
+        return (dH_new if ctx.needs_input_grad[0] else None), d_bo, d_w

@@ -8,13 +8,11 @@ nodes and compiles the whole graph around them without a graph break.
 * The four public ops (reference src/mhc/ops.py:231-323) and the mean-pool
   carry their backward as ``torch.library.register_autograd`` formulas that call
   the backward ops.
-* The layer (reference src/mhc/module.py:103-182) uses two autograd nodes, as
-  in eager mode, but passes the closure's gradients to node A functionally:
-  node A returns a view of ``H`` (the *link*) that only the closure consumes;
-  the closure's backward returns ``dH_new`` as the link's gradient and
-  ``dH_post`` inside ``w``'s gradient, and node A writes the complete ``dH``
-  in one pass.  The eager path hands the same two tensors over through a
-  Python side channel (``_layer._Stash``), which traced code cannot express.
+* The layer (reference src/mhc/module.py:103-182) uses the same two autograd
+  nodes as eager mode (``_layer.py``), on the custom ops: node A returns a view
+  of ``H`` (the *link*) that only the closure consumes; the closure's backward
+  returns ``dH_new`` as the link's gradient and ``dH_post`` inside ``w``'s
+  gradient, and node A writes the complete ``dH`` in one pass.
 
 Eager calls keep going through the launchers directly: a custom-op dispatch
 costs about 13 us of host time, more than some of the kernels it would wrap.

@@ -148,23 +148,35 @@ class HyperConnection(nn.Module):
         return w[:, 4:8].contiguous(), w[:, 0:4].contiguous(), w[:, 8:].reshape(B, n, n).contiguous()
 
     def forward(self, H: torch.Tensor) -> Tuple[torch.Tensor, Callable[[torch.Tensor], torch.Tensor]]:
-        """H (batch, seq, 4, dim) -> (branch_input (batch, seq, dim), add_residual)."""
+        """H (batch, seq, 4, dim) -> (branch_input (batch, seq, dim), add_residual).
+
+        ``add_residual`` recomputes ``H_res @ H`` from ``H`` instead of keeping ``H_residual``
+        (the reference's closure captures it, module.py:177-180).  It therefore raises if ``H``
+        was modified in place between ``forward`` and the call, where the reference would still
+        see the old values.  A strided ``H`` is made contiguous once, here, and that copy serves
+        the forward, the closure and the backward.
+        """
         self._check_input(H)
         if torch.compiler.is_compiling():
             return self._forward_traced(H)
-        stash = _layer._Stash()
+        H = H.contiguous()
+        version = H._version
         if not self.dynamic:
-            bi, w = _layer._StaticLayer.apply(H, self.H_pre_base, self.H_post_base, self.H_res_base, stash,
-                                              self.sinkhorn_iters)
+            bi, w, link = _layer._StaticLayer.apply(H, self.H_pre_base, self.H_post_base, self.H_res_base,
+                                                    self.sinkhorn_iters)
         elif self.use_fused_weights:
-            bi, w = _layer._DynamicLayer.apply(H, self.phi, self.H_pre_base, self.H_post_base, self.H_res_base,
-                                               self.alpha_pre, self.alpha_post, self.alpha_res, stash,
-                                               self.sinkhorn_iters, self.eps)
+            bi, w, link = _layer._DynamicLayer.apply(H, self.phi, self.H_pre_base, self.H_post_base,
+                                                     self.H_res_base, self.alpha_pre, self.alpha_post,
+                                                     self.alpha_res, self.sinkhorn_iters, self.eps)
         else:
-            bi, w = _layer._GenericLayer.apply(H, self._unfused_weights(H), stash)
+            bi, w, link = _layer._GenericLayer.apply(H, self._unfused_weights(H))
 
         def add_residual(branch_output: torch.Tensor) -> torch.Tensor:
-            return _layer._LayerAdd.apply(H, branch_output, w, stash)
+            if H._version != version:
+                raise RuntimeError(
+                    "HyperConnection: H was modified in place after forward(H); add_residual recomputes "
+                    "H_res @ H from H and would mix the modified values. Clone H before modifying it.")
+            return _layer._LayerAdd.apply(link, branch_output, w)
 
         return bi, add_residual
 

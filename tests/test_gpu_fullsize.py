@@ -10,7 +10,11 @@ What is checked, per config:
   bf16/fp16 output tolerance);
 * every parameter gradient: the oracle's weight backward fed torch fp32
   reductions of the upstream gradients (dH_pre = sum d_bi * H[n],
-  dH_res = sum dH_new[n] * H[m], dH_post = sum dH_new[n] * bo), <= 1e-3.
+  dH_res = sum dH_new[n] * H[m], dH_post = sum dH_new[n] * bo), <= 1e-3;
+* branch_input, H_new, d branch_output and dH once more, against the float64
+  value of each expression from the layer's own fp32 weights, rounded once to
+  the bf16 / fp16 output: within one unit in the last place, and bit-identical
+  but for a small fraction (test_gpu_rounding.check_layer_rounding).
 These exercise the kernels' index arithmetic at the real shapes (up to 2^28
 elements per tensor) and the split-S / split-K reduction plans.
 """
@@ -21,6 +25,7 @@ import torch
 
 from helpers import rel_err, to_np
 from oracle import mhc_oracle as O
+from test_gpu_rounding import check_layer_rounding
 
 pytestmark = pytest.mark.gpu
 
@@ -110,3 +115,6 @@ def test_full_size_layer(name):
     del dH_ref
     dbo_ref = (wq[:, None, :, None] * dnf).sum(dim=2)
     assert rel_err(to_np(bol.grad), to_np(dbo_ref)) < 2e-2
+    del dbo_ref, Hl, bol, bi, H_new, dbf, dnf, Hf
+    torch.cuda.empty_cache()
+    check_layer_rounding("dynamic" if c["dynamic"] else "static", hc, H, bo, dHn, dbi)

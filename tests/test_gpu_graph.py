@@ -6,16 +6,37 @@ with kernels, never hipMemsetAsync, so a whole training step of the layer can
 be captured with torch.cuda.graph and replayed.  Each replay must reproduce
 the eager step bit for bit (every kernel is deterministic): checked on several
 replays in a row, with eager work and synchronisations between them, and after
-new values are copied into the captured input tensors.
+new values are copied into the captured input tensors.  The replayed outputs and
+gradients are also checked against the float64 oracle layer on the same inputs
+(fp32: 1e-5 forward, 1e-4 gradients; bf16: 2e-2).
 """
 
+import numpy as np
 import pytest
 import torch
+
+from helpers import rel_err, to_np
+from oracle import mhc_oracle as O
 
 pytestmark = pytest.mark.gpu
 
 
-def _setup(dynamic, fused=True, seed=0):
+def _check_oracle(hc, H, bo, dHn, dbi, got, dtype):
+    """Replayed outputs and gradients against the float64 oracle layer."""
+    p = {n.replace(".weight", ""): to_np(v) for n, v in hc.named_parameters()}
+    fused = hc.use_fused_weights or not hc.dynamic
+    obi, oHn, cache = O.layer_forward(p, to_np(H), to_np(bo), hc.dynamic, fused, hc.sinkhorn_iters, hc.eps)
+    og = O.layer_backward(p, cache, to_np(dHn), to_np(dbi))
+    ftol, gtol = (1e-5, 1e-4) if dtype == torch.float32 else (2e-2, 2e-2)
+    assert rel_err(to_np(got["bi"]), obi) < ftol and rel_err(to_np(got["H_new"]), oHn) < ftol
+    assert rel_err(to_np(got["dH"]), og["H"]) < gtol and rel_err(to_np(got["dbo"]), og["bo"]) < gtol
+    for n, _ in hc.named_parameters():
+        want = og[n]
+        ptol = 1e-4 if dtype == torch.float32 else 1e-3
+        assert rel_err(to_np(got["d" + n]).reshape(np.shape(want)), want) < ptol, n
+
+
+def _setup(dynamic, fused=True, seed=0, dtype=torch.bfloat16):
     import mhc
 
     B, S, D = 2, 64, 256
@@ -27,7 +48,7 @@ def _setup(dynamic, fused=True, seed=0):
             hc.phi.copy_(torch.randn(hc.phi.shape, generator=g, device="cuda") * 0.02)
         if not dynamic:
             hc.H_res_base.copy_(torch.randn((4, 4), generator=g, device="cuda"))
-    mk = lambda *shape: torch.randn(shape, generator=g, device="cuda").bfloat16()  # noqa: E731
+    mk = lambda *shape: torch.randn(shape, generator=g, device="cuda").to(dtype)  # noqa: E731
     H = mk(B, S, 4, D).requires_grad_(True)
     bo = mk(B, S, D).requires_grad_(True)
     return hc, H, bo, mk(B, S, 4, D), mk(B, S, D), mk
@@ -50,9 +71,10 @@ def _snapshot(hc, H, bo, bi, H_new):
     return out
 
 
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
 @pytest.mark.parametrize("dynamic,fused", [(True, True), (False, True), (True, False)])
-def test_layer_step_graph_replays_match_eager(dynamic, fused):
-    hc, H, bo, dHn, dbi, mk = _setup(dynamic, fused)
+def test_layer_step_graph_replays_match_eager(dynamic, fused, dtype):
+    hc, H, bo, dHn, dbi, mk = _setup(dynamic, fused, dtype=dtype)
     ref = _snapshot(hc, H, bo, *_step(hc, H, bo, dHn, dbi))
 
     side = torch.cuda.Stream()
@@ -77,6 +99,8 @@ def test_layer_step_graph_replays_match_eager(dynamic, fused):
         got = _snapshot(hc, H, bo, bi_g, H_new_g)
         for k, v in ref.items():
             assert torch.equal(got[k], v), (i, k)
+        if i == 0:
+            _check_oracle(hc, H, bo, dHn, dbi, got, dtype)
         # unrelated eager work between replays
         x = mk(1024, 1024).float()
         (x @ x).sum().item()
@@ -92,3 +116,4 @@ def test_layer_step_graph_replays_match_eager(dynamic, fused):
     want = _snapshot(hc, H, bo, *_step(hc, H, bo, dHn, dbi))
     for k, v in want.items():
         assert torch.equal(got[k], v), ("new inputs", k)
+    _check_oracle(hc, H, bo, dHn, dbi, got, dtype)

@@ -211,6 +211,45 @@ def test_closure_never_called_and_bi_only():
     assert rel_err(to_np(hc.H_post_base.grad), g["H_post_base"]) < 1e-4
 
 
+@pytest.mark.parametrize("dynamic,fused", [(True, True), (False, True), (True, False)])
+def test_partial_backward_then_branch_input_backward(dynamic, fused):
+    """autograd.grad(H_new, branch_output) runs the closure's backward without node A's.  A later
+    bi.backward() must then give the branch_input-only gradients: nothing of H_new's cotangent may
+    reach dH or the parameter gradients."""
+    hc, H, bo, dHn, dbi = make_case(2, 16, 64, torch.float32, dynamic=dynamic, fused=fused, phi_std=0.05,
+                                    res_std=0.5)
+    Hl = H.clone().requires_grad_(True)
+    bol = bo.clone().requires_grad_(True)
+    bi, add = hc(Hl)
+    Hn = add(bol)
+    (d_bo,) = torch.autograd.grad(Hn, bol, dHn, retain_graph=True)
+    p = params_np(hc)
+    _, _, cache = O.layer_forward(p, to_np(H), to_np(bo), dynamic, fused or not dynamic, hc.sinkhorn_iters, hc.eps)
+    full = O.layer_backward(p, cache, to_np(dHn), to_np(dbi))
+    assert rel_err(to_np(d_bo), full["bo"]) < 1e-4
+    bi.backward(dbi)
+    g = {k.replace(".weight", ""): v for k, v in O.layer_backward(p, cache, np.zeros(H.shape), to_np(dbi)).items()}
+    assert rel_err(to_np(Hl.grad), g["H"]) < 1e-4
+    for n, prm in hc.named_parameters():
+        n = n.replace(".weight", "")
+        assert rel_err(to_np(prm.grad).reshape(np.shape(g[n])), g[n]) < 1e-4, n
+
+
+def test_closure_rejects_in_place_change_of_H():
+    """add_residual recomputes H_res @ H from H, so an in-place change of H between forward and
+    the call raises instead of mixing the new values (the reference's closure holds H_residual)."""
+    hc, H, bo, _, _ = make_case(2, 16, 64, torch.float32, phi_std=0.05)
+    Hc = H.clone()
+    bi, add = hc(Hc)
+    with torch.no_grad():
+        Hc.add_(1.0)
+    with pytest.raises(RuntimeError, match="modified in place"):
+        add(bo)
+    bi, add = hc(H)
+    _, oHn, _ = O.layer_forward(params_np(hc), to_np(H), to_np(bo))
+    assert rel_err(to_np(add(bo)), oHn) < 1e-5
+
+
 def test_h_new_only_and_h_without_grad():
     hc, H, bo, dHn, dbi = make_case(2, 16, 64, torch.float32, phi_std=0.05)
     bol = bo.clone().requires_grad_(True)

@@ -1,12 +1,15 @@
 """Host logic that needs no GPU: module construction / parameters / init
 (reference src/mhc/module.py:37-101,191-224), the public API surface, the
-pure-PyTorch baselines on CPU, and the node-B -> node-A gradient stash."""
+pure-PyTorch baselines on CPU, and the layer's node-B -> node-A gradient wiring
+(run on float64 oracle stand-ins for the HIP launchers)."""
 
 import numpy as np
+import pytest
 import torch
 
 import mhc
 from mhc import _layer
+from oracle import mhc_oracle as O
 
 
 def test_public_api_surface():
@@ -58,20 +61,124 @@ def test_torch_baselines_run_on_cpu_with_autograd():
     assert H.grad.shape == H.shape and hc.phi.grad is not None
 
 
-def test_stash_sums_repeated_closure_gradients():
-    s = _layer._Stash()
-    assert s.take() == (None, None)
-    a, b = torch.ones(2, 3), torch.full((2, 4), 2.0)
-    s.put(a, b)
-    s.put(a * 3, b * 5)
-    dh, dp = s.take()
-    assert torch.equal(dh, torch.full((2, 3), 4.0)) and torch.equal(dp, torch.full((2, 4), 12.0))
-    assert s.take() == (None, None)
+class _OracleLaunchers:
+    """float64 oracle stand-ins for the static layer's launchers, so the autograd wiring of
+    _layer's two nodes (node B's gradients reaching node A through the link and w) can run
+    on the CPU.  Only this test installs them."""
+
+    @staticmethod
+    def static_forward(H, pre, post, res, iters):
+        B = H.shape[0]
+        Hp, Hq, Hr = O.static_weights(pre.detach().numpy(), post.detach().numpy(), res.detach().numpy(), B, iters)
+        bi, _ = O.stream_mix(H.detach().numpy(), Hq, Hr)
+        w = np.concatenate([Hq, Hp, Hr.reshape(B, 16)], axis=1)
+        return torch.tensor(bi), torch.tensor(w)
+
+    @staticmethod
+    def static_backward(H, d_bi, dH_new, dH_post, pre, post, res, w, iters, need_dH=True):
+        B, S, _, D = H.shape
+        wn = w.detach().numpy()
+        d_bi = np.zeros((B, S, D)) if d_bi is None else d_bi.numpy()
+        dHn = np.zeros((B, S, 4, D)) if dH_new is None else dH_new.numpy()
+        dpost = np.zeros((B, 4)) if dH_post is None else dH_post.numpy()
+        dH, dpre, dres = O.stream_mix_backward(d_bi, dHn, H.detach().numpy(), wn[:, 0:4], wn[:, 8:].reshape(B, 4, 4))
+        gq, gp, gr = O.static_weights_backward(pre.detach().numpy(), post.detach().numpy(), res.detach().numpy(),
+                                               dpost, dpre, dres, iters)
+        return (torch.tensor(dH) if need_dH else None), torch.tensor(np.concatenate([gq, gp, gr.reshape(16)]))
+
+    @staticmethod
+    def add_forward(H, bo, w):
+        B = H.shape[0]
+        wn = w.detach().numpy()
+        _, hr = O.stream_mix(H.detach().numpy(), wn[:, 0:4], wn[:, 8:].reshape(B, 4, 4))
+        return torch.tensor(O.add_residual(hr, bo.detach().numpy(), wn[:, 4:8]))
+
+    @staticmethod
+    def add_backward(dH_new, bo, w):
+        _, d_bo, dpost = O.add_residual_backward(dH_new.numpy(), bo.detach().numpy(), w.detach().numpy()[:, 4:8])
+        return torch.tensor(d_bo), torch.tensor(dpost)
+
+
+def _static_case(monkeypatch):
+    for name in ("static_forward", "static_backward", "add_forward", "add_backward"):
+        monkeypatch.setattr(_layer, name, getattr(_OracleLaunchers, name))
+    g = np.random.default_rng(3)
+    B, S, D = 2, 3, 4
+    hc = mhc.HyperConnection(D, dynamic=False).double()
+    p = {"H_pre_base": g.standard_normal(4), "H_post_base": g.standard_normal(4),
+         "H_res_base": g.standard_normal((4, 4))}
+    with torch.no_grad():
+        for n, prm in hc.named_parameters():
+            prm.copy_(torch.tensor(p[n]))
+    arrays = [g.standard_normal(s) for s in ((B, S, 4, D), (B, S, D), (B, S, 4, D), (B, S, D))]
+    return hc, p, arrays
+
+
+def _grads_close(hc, H, g, keys=("H_pre_base", "H_post_base", "H_res_base")):
+    assert np.abs(H.grad.numpy() - g["H"]).max() < 1e-12
+    for n, prm in hc.named_parameters():
+        assert np.abs(prm.grad.numpy() - g[n].reshape(prm.shape)).max() < 1e-12, n
+
+
+def test_partial_backward_leaves_no_closure_gradient_behind(monkeypatch):
+    """A backward call that reaches the closure but not node A (here autograd.grad w.r.t.
+    branch_output only) must not leak into a later backward: H.grad and the parameter grads
+    of bi.backward() afterwards are the branch_input-only gradients."""
+    hc, p, (H_np, bo_np, dHn_np, dbi_np) = _static_case(monkeypatch)
+    H = torch.tensor(H_np, requires_grad=True)
+    bo = torch.tensor(bo_np, requires_grad=True)
+    bi, add = hc(H)
+    Hn = add(bo)
+    (d_bo,) = torch.autograd.grad(Hn, bo, torch.tensor(dHn_np), retain_graph=True)
+    _, _, cache = O.layer_forward(p, H_np, bo_np, dynamic=False)
+    full = O.layer_backward(p, cache, dHn_np, dbi_np)
+    assert np.abs(d_bo.numpy() - full["bo"]).max() < 1e-12
+    bi.backward(torch.tensor(dbi_np))
+    _grads_close(hc, H, O.layer_backward(p, cache, np.zeros_like(dHn_np), dbi_np))
+
+
+def test_closure_gradients_reach_node_a_and_sum_over_calls(monkeypatch):
+    """Full backward through bi and two closure calls: the engine sums the two link / w
+    gradients, and node A sees their sum (the closure is linear in dH_new)."""
+    hc, p, (H_np, bo_np, dHn_np, dbi_np) = _static_case(monkeypatch)
+    H = torch.tensor(H_np, requires_grad=True)
+    bi, add = hc(H)
+    Hn1 = add(torch.tensor(bo_np))
+    Hn2 = add(torch.tensor(2 * bo_np))
+    torch.autograd.backward([Hn1, Hn2, bi], [torch.tensor(dHn_np), torch.tensor(0.5 * dHn_np), torch.tensor(dbi_np)])
+    _, _, c1 = O.layer_forward(p, H_np, bo_np, dynamic=False)
+    _, _, c2 = O.layer_forward(p, H_np, 2 * bo_np, dynamic=False)
+    g1 = O.layer_backward(p, c1, dHn_np, dbi_np)
+    g2 = O.layer_backward(p, c2, 0.5 * dHn_np, np.zeros_like(dbi_np))
+    _grads_close(hc, H, {k: g1[k] + g2[k] for k in g1})
+
+
+def test_closure_rejects_in_place_change_of_H(monkeypatch):
+    """The closure recomputes H_res @ H from H; an in-place change of H after forward would
+    silently change H_new (the reference's closure holds H_residual), so it raises."""
+    hc, p, (H_np, bo_np, _, _) = _static_case(monkeypatch)
+    H = torch.tensor(H_np)
+    bi, add = hc(H)
+    with torch.no_grad():
+        H.mul_(2.0)
+    with pytest.raises(RuntimeError, match="modified in place"):
+        add(torch.tensor(bo_np))
+    bi, add = hc(H)
+    _, want, _ = O.layer_forward(p, 2 * H_np, bo_np, dynamic=False)
+    assert np.abs(add(torch.tensor(bo_np)).detach().numpy() - want).max() < 1e-12
+    # a strided H is copied once in forward: changing the original afterwards is harmless
+    Hs = torch.tensor(H_np).transpose(1, 3).contiguous().transpose(1, 3)
+    assert not Hs.is_contiguous()
+    bi, add = hc(Hs)
+    with torch.no_grad():
+        Hs.zero_()
+    _, want, _ = O.layer_forward(p, H_np, bo_np, dynamic=False)
+    assert np.abs(add(torch.tensor(bo_np)).detach().numpy() - want).max() < 1e-12
 
 
 def test_bench_cpu_baseline_fields():
     """bench.py's cpu_baseline leg (the reference's torch layer restated, on the host cores) reports
-    the contract's fields plus the host it ran on, on a short sample."""
+    the contract's fields plus the host and torch version it ran on (here on a short sequence)."""
     import importlib.util
     import os
 
@@ -79,7 +186,10 @@ def test_bench_cpu_baseline_fields():
     spec = importlib.util.spec_from_file_location("mhc_bench", path)
     bench = importlib.util.module_from_spec(spec)
     spec.loader.exec_module(bench)
-    r = bench._cpu_leg(dict(bench.WORKLOADS["config5"]), 0.2)
-    assert set(r) >= {"value", "unit", "cores", "kind", "sample", "host_cpus", "host_cpu_model"}
-    assert r["value"] > 0 and r["unit"] == "tokens/s" and r["kind"] == "port"
-    assert r["cores"] == torch.get_num_threads() and r["host_cpus"] == os.cpu_count()
+    for w in ("config3", "config5"):
+        r = bench._cpu_leg(dict(bench.WORKLOADS[w]), reps=1, seq=8)
+        assert set(r) >= {"value", "unit", "cores", "kind", "sample", "host_cpus", "host_cpu_model",
+                          "torch_version", "fwd_only_tokens_per_s", "runs_s"}
+        assert r["value"] > 0 and r["unit"] == "tokens/s" and r["kind"] == "port"
+        assert r["cores"] == torch.get_num_threads() and r["host_cpus"] == os.cpu_count()
+        assert r["torch_version"] == torch.__version__ and "S=8 " in r["sample"]

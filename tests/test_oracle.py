@@ -469,3 +469,251 @@ def test_product_torch_baselines_match_oracle():
         obi, oHn, _ = O.layer_forward(p, H, bo, dynamic, fused)
         assert rel_err(bi.detach().numpy(), obi) < 1e-12
         assert rel_err(Hn.detach().numpy(), oHn) < 1e-12
+
+
+# --------------------------------------------------------------------------- closed-form layer pins
+#
+# Structured inputs for which every weight has a closed form computed here from scalars, with no
+# call into the oracle's own weight functions:
+#
+# * H[b, s, n, d] = c_b + delta_b * (-1)^s with S even, so the mean over the sequence is exactly c_b
+#   and x = c_b * ones(4D);
+# * every projection column (phi[:, j], or a Linear row) is v_j / (4D) * ones, so x . column = c_b v_j;
+# * H_res logits of the form a * C + b * (J - C), where C is the cyclic shift C[n, (n+1) % 4] = 1
+#   and J the all-ones matrix.  Every row and column of |a| C + |b| (J - C) + eps sums to the same r,
+#   so each Sinkhorn normalisation only rescales the matrix: t -> t / (t r + eps).  C is not
+#   symmetric, so a transposed H_res or a column-major flatten fails.
+#
+# RMS with the mean over K and eps inside the sqrt (module.py:145, _torch_baseline.py:78-80) is
+# separated from a sum over K or eps outside the sqrt by c = 1e-3, where c^2 equals eps = 1e-6.
+
+_C = np.roll(np.eye(4), 1, axis=1)
+_J = np.ones((4, 4))
+
+
+def _sk_closed(a, b, iters, eps):
+    """Sinkhorn of a C + b (J - C), in closed form."""
+    A, Bv = abs(a) + eps, abs(b) + eps
+    r = A + 3 * Bv
+    t = 1.0
+    for _ in range(2 * iters):
+        t = t / (t * r + eps)
+    return t * (A * _C + Bv * (_J - _C))
+
+
+def _sig1(z):
+    return 1.0 / (1.0 + np.exp(-np.asarray(z, dtype=np.float64)))
+
+
+def test_sinkhorn_cyclic_closed_form():
+    """The helper itself against the oracle's Sinkhorn: a pin both ways, on a matrix whose
+    answer is also known without iteration (a C + b (J - C) is doubly stochastic up to scale)."""
+    a, b = 2.0, 0.5
+    for iters, eps in [(1, 0.0), (20, 1e-8), (7, 1e-6)]:
+        got = O.sinkhorn((a * _C + b * (_J - _C))[None], iters, eps)[0]
+        assert np.abs(got - _sk_closed(a, b, iters, eps)).max() < 1e-15
+    assert np.abs(_sk_closed(a, b, 20, 0.0) - (a * _C + b * (_J - _C)) / (a + 3 * b)).max() < 1e-15
+
+
+def _structured_H(c, S, D, rng):
+    B = len(c)
+    sign = np.where(np.arange(S) % 2 == 0, 1.0, -1.0)[None, :, None, None]
+    delta = rng.uniform(0.5, 2.0, size=(B, 1, 4, D))
+    return np.asarray(c, dtype=np.float64)[:, None, None, None] + delta * sign
+
+
+def _mix_and_add(H, bo, hpre, hpost, hres):
+    """bi[b,s,d] = sum_n hpre[b,n] H[b,s,n,d];  H_new[b,s,n,d] = sum_m hres[b,n,m] H[b,s,m,d]
+    + hpost[b,n] bo[b,s,d]  (_torch_baseline.py:136,141,164), written as explicit loops."""
+    B, S, n, D = H.shape
+    bi = np.zeros((B, S, D))
+    Hn = np.zeros_like(H)
+    for b in range(B):
+        for i in range(4):
+            bi[b] += hpre[b][i] * H[b, :, i]
+            Hn[b, :, i] = hpost[b][i] * bo[b]
+            for m in range(4):
+                Hn[b, :, i] += hres[b][i][m] * H[b, :, m]
+    return bi, Hn
+
+
+@pytest.mark.parametrize("layer_idx", [0, 2])
+def test_layer_static_known_answer(layer_idx):
+    """Static layer (module.py:108-117, 170-180): H_post = sigmoid(b_post) with no x2, H_pre =
+    sigmoid(b_pre) / (sum + 1e-8), H_res = Sinkhorn(b_res, eps 1e-8); bi uses H_pre, the closure
+    uses H_res on H and H_post on branch_output."""
+    rng = np.random.default_rng(7 + layer_idx)
+    B, S, D = 2, 4, 3
+    bq = np.array([0.3, -0.7, 1.2, 0.1])
+    bq[layer_idx] += 1.0
+    bp = np.array([-0.4, 0.9, 0.2, 1.5])
+    a, b = 2.0, -0.5
+    p = {"H_pre_base": bq, "H_post_base": bp, "H_res_base": a * _C + b * (_J - _C)}
+    H = rng.standard_normal((B, S, 4, D))
+    bo = rng.standard_normal((B, S, D))
+    bi, Hn, _ = O.layer_forward(p, H, bo, dynamic=False, iters=20)
+    sq = _sig1(bq)
+    hpre = np.tile(sq / (sq.sum() + 1e-8), (B, 1))
+    hpost = np.tile(_sig1(bp), (B, 1))
+    hres = np.tile(_sk_closed(a, b, 20, 1e-8), (B, 1, 1))
+    want_bi, want_Hn = _mix_and_add(H, bo, hpre, hpost, hres)
+    assert np.abs(bi - want_bi).max() < 1e-13
+    assert np.abs(Hn - want_Hn).max() < 1e-13
+
+
+def test_layer_dynamic_default_init_known_answer():
+    """Fused dynamic layer at phi = 0 (the default init): s = bias = [b_pre, b_post, b_res]
+    (module.py:127-131), H_pre = sigmoid(b_pre) / (sum + 1e-6), H_post = 2 sigmoid(b_post),
+    H_res = Sinkhorn(|b_res| + 1e-6, eps 1e-6).  A pre/post bias swap, a missing x2, the weights
+    returned as (H_pre, H_post) instead of (H_post, H_pre), or a transposed H_res fail."""
+    rng = np.random.default_rng(11)
+    B, S, D = 2, 4, 3
+    bq, bp = np.array([1.0, 0.0, -0.3, 0.6]), np.array([1.0, -1.2, 0.4, 0.8])
+    a, b = 1.5, 0.25
+    p = {"H_pre_base": bq, "H_post_base": bp, "H_res_base": a * _C + b * (_J - _C),
+         "phi": np.zeros((4 * D, 24)), "alpha_pre": np.array([0.3]), "alpha_post": np.array([0.2]),
+         "alpha_res": np.array([0.1])}
+    H = rng.standard_normal((B, S, 4, D))
+    bo = rng.standard_normal((B, S, D))
+    bi, Hn, _ = O.layer_forward(p, H, bo, dynamic=True, fused=True, iters=20, eps=1e-6)
+    sq = _sig1(bq)
+    hpre = np.tile(sq / (sq.sum() + 1e-6), (B, 1))
+    hpost = np.tile(2.0 * _sig1(bp), (B, 1))
+    hres = np.tile(_sk_closed(a, b, 20, 1e-6), (B, 1, 1))
+    want_bi, want_Hn = _mix_and_add(H, bo, hpre, hpost, hres)
+    assert np.abs(bi - want_bi).max() < 1e-13
+    assert np.abs(Hn - want_Hn).max() < 1e-13
+
+
+def _group_cols(v_pre, v_post, res_ab, K):
+    """phi [K, 24] whose column j is v_j / K * ones; the H_res group is a C + b (J - C), row-major."""
+    v = np.concatenate([v_pre, v_post, (res_ab[0] * _C + res_ab[1] * (_J - _C)).reshape(16)])
+    return np.tile(v / K, (K, 1))
+
+
+def test_layer_dynamic_structured_phi_known_answer():
+    """Fused dynamic layer with phi != 0 on the structured inputs.  x = c_b ones (the sequence
+    mean), raw_j = c_b v_j, inv_rms = 1 / sqrt(c_b^2 + eps), s_j = alpha_g inv_rms raw_j + bias_j with
+    alpha_pre on columns 0:4, alpha_post on 4:8 and alpha_res on 8:24 (_torch_baseline.py:73-111).
+    c = 1e-3 sits where eps inside / outside the sqrt differ; c = 0.5 where mean / sum over K and
+    over S differ."""
+    rng = np.random.default_rng(5)
+    S, D = 6, 2
+    K = 4 * D
+    c = np.array([1e-3, 0.5])
+    B = len(c)
+    eps, iters = 1e-6, 20
+    vq, vp = np.array([0.5, -1.0, 2.0, 0.3]), np.array([-0.6, 1.1, 0.0, 0.9])
+    res_ab = (3.0, -1.0)
+    bq, bp = np.array([0.2, -0.1, 0.4, 0.0]), np.array([0.7, -0.3, 0.1, 0.5])
+    base_ab = (1.0, 0.2)
+    ap, aq, ar = 0.7, 0.4, 0.25
+    p = {"H_pre_base": bq, "H_post_base": bp, "H_res_base": base_ab[0] * _C + base_ab[1] * (_J - _C),
+         "phi": _group_cols(vq, vp, res_ab, K), "alpha_pre": np.array([ap]), "alpha_post": np.array([aq]),
+         "alpha_res": np.array([ar])}
+    H = _structured_H(c, S, D, rng)
+    bo = rng.standard_normal((B, S, D))
+    bi, Hn, cache = O.layer_forward(p, H, bo, dynamic=True, fused=True, iters=iters, eps=eps)
+    assert np.abs(cache["x"] - c[:, None]).max() < 1e-15
+    hpre, hpost, hres = [], [], []
+    for cb in c:
+        k = cb / np.sqrt(cb * cb + eps)
+        sq = _sig1(ap * k * vq + bq)
+        hpre.append(sq / (sq.sum() + eps))
+        hpost.append(2.0 * _sig1(aq * k * vp + bp))
+        hres.append(_sk_closed(base_ab[0] + ar * k * res_ab[0], base_ab[1] + ar * k * res_ab[1], iters, eps))
+    want_bi, want_Hn = _mix_and_add(H, bo, hpre, hpost, hres)
+    assert rel_err(bi, want_bi) < 1e-13
+    assert rel_err(Hn, want_Hn) < 1e-13
+    # the chosen inputs do separate the slips named above
+    k_sum = c[0] / np.sqrt(K * c[0] ** 2 + eps)
+    k_out = c[0] / (abs(c[0]) + eps)
+    k_in = c[0] / np.sqrt(c[0] ** 2 + eps)
+    assert abs(k_sum - k_in) > 0.1 and abs(k_out - k_in) > 0.2
+
+
+def test_unfused_weights_structured_known_answer():
+    """Unfused path (module.py:143-163): rms = sqrt(mean(x^2) + eps), x_n = x / rms, each logit is
+    base + scale * (W x_n), H_post = sigmoid (no x2), 1e-8 in the H_pre normalisation and in the
+    Sinkhorn.  Linears whose rows are w_i / K * ones give W x_n = w_i c / sqrt(c^2 + eps) for
+    x = c ones.  A sum-RMS, eps outside the sqrt, or the scale applied before the normalisation
+    (where the RMS would cancel it) fail at c = 1e-3 or c = 0.5."""
+    K, eps, iters = 8, 1e-6, 20
+    wq, wp = np.array([0.5, -1.0, 2.0, 0.3]), np.array([-0.6, 1.1, 0.0, 0.9])
+    res_ab = (3.0, -1.0)
+    Wq, Wp = np.tile(wq[:, None] / K, (1, K)), np.tile(wp[:, None] / K, (1, K))
+    Wr = np.tile((res_ab[0] * _C + res_ab[1] * (_J - _C)).reshape(16, 1) / K, (1, K))
+    sq_, sp_, sr_ = 0.4, 0.7, 0.25
+    bq, bp = np.array([0.2, -0.1, 0.4, 0.0]), np.array([0.7, -0.3, 0.1, 0.5])
+    base_ab = (1.0, 0.2)
+    br = base_ab[0] * _C + base_ab[1] * (_J - _C)
+    c = np.array([1e-3, 0.5])
+    x = np.tile(c[:, None], (1, K))
+    H_post, H_pre, H_res = O.unfused_weights(x, Wq, Wp, Wr, sq_, sp_, sr_, bq, bp, br, iters, eps)
+    for i, cb in enumerate(c):
+        k = cb / np.sqrt(cb * cb + eps)
+        assert np.abs(H_post[i] - _sig1(bp + sp_ * k * wp)).max() < 1e-15
+        sq = _sig1(bq + sq_ * k * wq)
+        assert np.abs(H_pre[i] - sq / (sq.sum() + 1e-8)).max() < 1e-15
+        want = _sk_closed(base_ab[0] + sr_ * k * res_ab[0], base_ab[1] + sr_ * k * res_ab[1], iters, 1e-8)
+        assert np.abs(H_res[i] - want).max() < 1e-14
+
+
+def test_layer_unfused_structured_known_answer():
+    """The unfused layer end to end on the structured H: the sequence mean feeds the RMS, bi uses
+    H_pre and the closure H_res and H_post (module.py:165-180)."""
+    rng = np.random.default_rng(9)
+    S, D = 4, 2
+    K = 4 * D
+    c = np.array([1e-3, 0.5])
+    B = len(c)
+    eps, iters = 1e-6, 20
+    wq, wp = np.array([0.5, -1.0, 2.0, 0.3]), np.array([-0.6, 1.1, 0.0, 0.9])
+    res_ab, base_ab = (3.0, -1.0), (1.0, 0.2)
+    p = {"H_pre_base": np.array([0.2, -0.1, 0.4, 0.0]), "H_post_base": np.array([0.7, -0.3, 0.1, 0.5]),
+         "H_res_base": base_ab[0] * _C + base_ab[1] * (_J - _C),
+         "W_pre": np.tile(wq[:, None] / K, (1, K)), "W_post": np.tile(wp[:, None] / K, (1, K)),
+         "W_res": np.tile((res_ab[0] * _C + res_ab[1] * (_J - _C)).reshape(16, 1) / K, (1, K)),
+         "scale_pre": np.array([0.4]), "scale_post": np.array([0.7]), "scale_res": np.array([0.25])}
+    H = _structured_H(c, S, D, rng)
+    bo = rng.standard_normal((B, S, D))
+    bi, Hn, _ = O.layer_forward(p, H, bo, dynamic=True, fused=False, iters=iters, eps=eps)
+    hpre, hpost, hres = [], [], []
+    for cb in c:
+        k = cb / np.sqrt(cb * cb + eps)
+        sq = _sig1(p["H_pre_base"] + 0.4 * k * wq)
+        hpre.append(sq / (sq.sum() + 1e-8))
+        hpost.append(_sig1(p["H_post_base"] + 0.7 * k * wp))
+        hres.append(_sk_closed(base_ab[0] + 0.25 * k * res_ab[0], base_ab[1] + 0.25 * k * res_ab[1], iters, 1e-8))
+    want_bi, want_Hn = _mix_and_add(H, bo, hpre, hpost, hres)
+    assert rel_err(bi, want_bi) < 1e-13
+    assert rel_err(Hn, want_Hn) < 1e-13
+
+
+@pytest.mark.parametrize("dynamic,fused", [(True, False), (False, True)])
+def test_layer_backward_finite_differences_static_and_unfused(dynamic, fused):
+    """The whole layer's gradients against central differences of its forward, for the paths
+    the dynamic-fused FD test does not cover."""
+    rng = np.random.default_rng(21)
+    B, S, D = 2, 3, 2
+    p = _layer_params(dynamic, fused, D, rng)
+    H = rng.standard_normal((B, S, 4, D))
+    bo = rng.standard_normal((B, S, D))
+    dHn = rng.standard_normal((B, S, 4, D))
+    dbi = rng.standard_normal((B, S, D))
+
+    def loss(pp, HH, bb):
+        bi, Hn, _ = O.layer_forward(pp, HH, bb, dynamic, fused, iters=4, eps=1e-6)
+        return float((bi * dbi).sum() + (Hn * dHn).sum())
+
+    _, _, cache = O.layer_forward(p, H, bo, dynamic, fused, iters=4, eps=1e-6)
+    g = O.layer_backward(p, cache, dHn, dbi)
+    assert rel_err(g["H"], _fd(lambda v: loss(p, v, bo), H.copy())) < 1e-6
+    assert rel_err(g["bo"], _fd(lambda v: loss(p, H, v), bo.copy())) < 1e-6
+    for k in p:
+        def f(v, k=k):
+            q = dict(p)
+            q[k] = v
+            return loss(q, H, bo)
+        key = k + ".weight" if k.startswith("W_") else k
+        assert rel_err(np.asarray(g[key]).reshape(p[k].shape), _fd(f, p[k].astype(np.float64).copy())) < 1e-6, k
