@@ -201,6 +201,30 @@ int mhc_layer_dynamic_forward(const void* H, int dtype, const float* phi,
                               int64_t B, int64_t S, int64_t D, int iters, float eps,
                               void* workspace, size_t workspace_bytes, mhc_stream_t stream);
 
+/* Size of the static device scratch of mhc_layer_dynamic_forward_noalloc
+ * (16 MiB, held by every GPU the library runs on until the process ends). */
+#define MHC_NOALLOC_SCRATCH_BYTES ((size_t)16 << 20)
+
+/* No counterpart in the reference.  For callers that cannot allocate device
+ * memory (code under HIP graph capture, tight serving loops, harnesses that
+ * forbid hipMalloc): mhc_layer_dynamic_forward with the same arguments, outputs
+ * and bits, but no workspace argument.  Its scratch (the mean-pool column
+ * partials and the projection partials) is a static device array of
+ * MHC_NOALLOC_SCRATCH_BYTES; the call allocates nothing.  It returns
+ * MHC_ERR_WORKSPACE, before any device work, when the shape needs more:
+ * about 17.6 * B * D bytes once that exceeds 3 MiB (6 MiB for fp32 H), so
+ * B * D up to about 950k fits (B = 232 at D = 4096, any S).  The scratch
+ * starts from nothing it has to find zeroed: each call overwrites every entry
+ * it reads.  All calls on one GPU share that GPU's array, so calls that overlap
+ * on one GPU (on different streams) race; serialise them. */
+int mhc_layer_dynamic_forward_noalloc(const void* H, int dtype, const float* phi,
+                                      const float* H_pre_base, const float* H_post_base,
+                                      const float* H_res_base, const float* alpha_pre,
+                                      const float* alpha_post, const float* alpha_res,
+                                      void* branch_input, float* x, float* w, float* aux,
+                                      int64_t B, int64_t S, int64_t D, int iters, float eps,
+                                      mhc_stream_t stream);
+
 /* Static layer forward (module.py:108-117 + 177): w from the base
  * parameters (H_post = sigmoid, H_pre = sigmoid/(sum+1e-8), H_res = Sinkhorn
  * with eps 1e-8), then branch_input. */

@@ -37,6 +37,6 @@ int num_cus() {
 
 }  // namespace mhc
 
-extern "C" int mhc_abi_version(void) { return 2; }
+extern "C" int mhc_abi_version(void) { return 3; }
 
 extern "C" const char* mhc_last_error(void) { return mhc::g_err; }

@@ -12,6 +12,8 @@
 // Per token that is 18 D e bytes forward and 24 D e backward (e = element
 // size), against 22 + ~39 for the reference's op-by-op composition.
 // Static layers skip the mean-pool and fold pass B into pass C.
+#include <mutex>
+
 #include "dynw_kernels.hpp"
 #include "stream_kernels.hpp"
 
@@ -243,23 +245,33 @@ extern "C" size_t mhc_layer_workspace_bytes(int64_t B, int64_t S, int64_t D, int
   if (int rc_ = check_workspace(who, workspace, workspace_bytes, L.total)) return rc_;      \
   char* wsb = (char*)workspace;
 
-extern "C" int mhc_layer_dynamic_forward(const void* H, int dtype, const float* phi, const float* H_pre_base,
-                                         const float* H_post_base, const float* H_res_base,
-                                         const float* alpha_pre, const float* alpha_post, const float* alpha_res,
-                                         void* branch_input, float* x, float* w, float* aux, int64_t B, int64_t S,
-                                         int64_t D, int iters, float eps, void* workspace, size_t workspace_bytes,
-                                         mhc_stream_t stream) {
-  if (int rc = check_bsd("layer_dynamic_forward", B, S, D)) return rc;
-  if (iters < 0) { set_error("layer_dynamic_forward: negative iters"); return MHC_ERR_ARG; }
+// Argument checks shared by the two dynamic-forward entry points; 0 when the call may proceed
+// (also for B == 0, which the callers then return early on).
+static int layer_dynamic_forward_args(const char* who, const void* H, const float* phi, const float* H_pre_base,
+                                      const float* H_post_base, const float* H_res_base, const float* alpha_pre,
+                                      const float* alpha_post, const float* alpha_res, const void* branch_input,
+                                      const float* x, const float* w, const float* aux, int64_t B, int64_t S,
+                                      int64_t D, int iters) {
+  if (int rc = check_bsd(who, B, S, D)) return rc;
+  if (iters < 0) { set_error("%s: negative iters", who); return MHC_ERR_ARG; }
   if (B == 0) return MHC_OK;
   const bool nz = S * D != 0;  // bulk tensors may be empty (null) when S * D == 0
   if ((nz && (!H || !branch_input)) || !phi || !H_pre_base || !H_post_base || !H_res_base || !alpha_pre ||
       !alpha_post || !alpha_res || !x || !w || !aux) {
-    set_error("layer_dynamic_forward: null pointer");
+    set_error("%s: null pointer", who);
     return MHC_ERR_ARG;
   }
-  LAYER_WS_CHECK("layer_dynamic_forward");
-  hipStream_t st = (hipStream_t)stream;
+  return MHC_OK;
+}
+
+// The dynamic layer forward proper: mean-pool with the projection partials, the Eq. 14-19
+// epilogue, branch_input.  It uses the column partials (L.colpart) and the projection
+// partials (L.pool_part) of the workspace at wsb, and overwrites every entry it reads.
+static int layer_dynamic_forward_run(const void* H, int dtype, const float* phi, const float* H_pre_base,
+                                     const float* H_post_base, const float* H_res_base, const float* alpha_pre,
+                                     const float* alpha_post, const float* alpha_res, void* branch_input, float* x,
+                                     float* w, float* aux, int64_t B, int64_t S, int64_t D, int iters, float eps,
+                                     const LayerWs& L, char* wsb, hipStream_t st) {
   float* part = (float*)(wsb + L.pool_part);
   int nK = 0;
   if (int rc = mean_pool_any(H, dtype, x, phi, part, (float*)(wsb + L.colpart), B, S, D, &nK, st)) return rc;
@@ -268,6 +280,89 @@ extern "C" int mhc_layer_dynamic_forward(const void* H, int dtype, const float* 
       part, nK, B, 4 * D, P, OutRow{w, kOut}, OutRow{w + 4, kOut}, OutRow{w + 8, kOut}, aux, iters, eps);
   if (int rc = hip_status(hipGetLastError(), "layer finalize launch")) return rc;
   return branch_input_any(H, dtype, w, branch_input, B, S, D, st);
+}
+
+extern "C" int mhc_layer_dynamic_forward(const void* H, int dtype, const float* phi, const float* H_pre_base,
+                                         const float* H_post_base, const float* H_res_base,
+                                         const float* alpha_pre, const float* alpha_post, const float* alpha_res,
+                                         void* branch_input, float* x, float* w, float* aux, int64_t B, int64_t S,
+                                         int64_t D, int iters, float eps, void* workspace, size_t workspace_bytes,
+                                         mhc_stream_t stream) {
+  if (int rc = layer_dynamic_forward_args("layer_dynamic_forward", H, phi, H_pre_base, H_post_base, H_res_base,
+                                          alpha_pre, alpha_post, alpha_res, branch_input, x, w, aux, B, S, D,
+                                          iters))
+    return rc;
+  if (B == 0) return MHC_OK;
+  LAYER_WS_CHECK("layer_dynamic_forward");
+  return layer_dynamic_forward_run(H, dtype, phi, H_pre_base, H_post_base, H_res_base, alpha_pre, alpha_post,
+                                   alpha_res, branch_input, x, w, aux, B, S, D, iters, eps, L, wsb,
+                                   (hipStream_t)stream);
+}
+
+// ---------------------------------------------------------------------------
+// Allocation-free dynamic layer forward.  Its scratch is the static device
+// array below: every GPU the library runs on holds its own copy, for the life
+// of the process.  In host code `scratch` only names the symbol; the device
+// address of each GPU's copy comes from hipGetSymbolAddress, taken once per
+// device with that device current, and kept in g_scratch_dev.  Calls that
+// overlap on one GPU (different streams) share the array and race.
+// ---------------------------------------------------------------------------
+constexpr size_t kScratchBytes = MHC_NOALLOC_SCRATCH_BYTES;
+static __device__ __align__(256) unsigned char scratch[kScratchBytes];
+
+constexpr int kMaxDevices = 64;
+static std::mutex g_scratch_mu;
+static void* g_scratch_dev[kMaxDevices];
+
+// Device address of the current device's scratch array.
+static int scratch_on_current_device(char** out) {
+  int dev = -1;
+  if (int rc = hip_status(hipGetDevice(&dev), "layer_dynamic_forward_noalloc: hipGetDevice")) return rc;
+  if (dev < 0 || dev >= kMaxDevices) {
+    set_error("layer_dynamic_forward_noalloc: device %d beyond the %d the library tracks", dev, kMaxDevices);
+    return MHC_ERR_ARG;
+  }
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch_dev[dev]) {
+    void* p = nullptr;
+    if (int rc = hip_status(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)),
+                            "layer_dynamic_forward_noalloc: hipGetSymbolAddress"))
+      return rc;
+    if (!p || ((uintptr_t)p & 255) != 0) {
+      set_error("layer_dynamic_forward_noalloc: scratch address %p is not 256-byte aligned", p);
+      return MHC_ERR_HIP;
+    }
+    g_scratch_dev[dev] = p;
+  }
+  *out = (char*)g_scratch_dev[dev];
+  return MHC_OK;
+}
+
+extern "C" int mhc_layer_dynamic_forward_noalloc(const void* H, int dtype, const float* phi,
+                                                 const float* H_pre_base, const float* H_post_base,
+                                                 const float* H_res_base, const float* alpha_pre,
+                                                 const float* alpha_post, const float* alpha_res,
+                                                 void* branch_input, float* x, float* w, float* aux, int64_t B,
+                                                 int64_t S, int64_t D, int iters, float eps, mhc_stream_t stream) {
+  const char* who = "layer_dynamic_forward_noalloc";
+  if (int rc = layer_dynamic_forward_args(who, H, phi, H_pre_base, H_post_base, H_res_base, alpha_pre, alpha_post,
+                                          alpha_res, branch_input, x, w, aux, B, S, D, iters))
+    return rc;
+  if (B == 0) return MHC_OK;
+  // The forward reads and writes only the column and projection partials, which
+  // lead the layer workspace: its first L.red_part bytes.
+  const LayerWs L = layer_ws(B, S, D, dtype);
+  if (L.red_part > kScratchBytes) {
+    set_error("%s: B=%lld S=%lld D=%lld needs %zu bytes of scratch, more than the %zu the static array holds; "
+              "call mhc_layer_dynamic_forward with a workspace instead",
+              who, (long long)B, (long long)S, (long long)D, L.red_part, kScratchBytes);
+    return MHC_ERR_WORKSPACE;
+  }
+  char* wsb = nullptr;
+  if (int rc = scratch_on_current_device(&wsb)) return rc;
+  return layer_dynamic_forward_run(H, dtype, phi, H_pre_base, H_post_base, H_res_base, alpha_pre, alpha_post,
+                                   alpha_res, branch_input, x, w, aux, B, S, D, iters, eps, L, wsb,
+                                   (hipStream_t)stream);
 }
 
 extern "C" int mhc_layer_static_forward(const void* H, int dtype, const float* H_pre_base, const float* H_post_base,

@@ -51,6 +51,8 @@ _SIGNATURES = {
     "mhc_mean_pool": (_I, [_P, _I, _P, _I64, _I64, _I64, _P, _SZ, _P]),
     "mhc_layer_dynamic_forward": (
         _I, [_P, _I, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I, _F, _P, _SZ, _P]),
+    "mhc_layer_dynamic_forward_noalloc": (
+        _I, [_P, _I, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I, _F, _P]),
     "mhc_layer_static_forward": (_I, [_P, _I, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I, _P]),
     "mhc_layer_branch_input": (_I, [_P, _I, _P, _P, _I64, _I64, _I64, _P]),
     "mhc_layer_mix_backward": (_I, [_P, _I, _P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _P, _SZ, _P]),
@@ -63,7 +65,7 @@ _SIGNATURES = {
         _I, [_P, _I, _P, _P, _P, _P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I, _P, _SZ, _P]),
 }
 
-ABI_VERSION = 2
+ABI_VERSION = 3
 
 _lib = None
 _lock = threading.Lock()

@@ -94,6 +94,11 @@ def test_host_side_validation_without_gpu(lib):
     assert lib.mhc_stream_mix_forward(16, 16, 16, 16, 16, 1, (1 << 32) - 1, 1, 0, None) == 1
     assert b"2^32 - 2^16" in lib.mhc_last_error()
     assert lib.mhc_layer_dynamic_forward(None, 0, *([None] * 11), 1, 1, 1, -1, 1e-6, None, 0, None) == 1
+    # the allocation-free forward: a shape whose scratch exceeds the static array is refused
+    # with MHC_ERR_WORKSPACE before any HIP call (B = 512 at D = 4096 needs ~37 MB)
+    assert lib.mhc_layer_dynamic_forward_noalloc(16, 1, *([16] * 11), 512, 1, 4096, 20, 1e-6, None) == 3
+    assert b"static array holds" in lib.mhc_last_error()
+    assert lib.mhc_layer_dynamic_forward_noalloc(None, 1, *([None] * 11), 2, 3, 4, 20, 1e-6, None) == 1
 
 
 def test_ops_reject_cpu_tensors():
