@@ -63,9 +63,11 @@ ALGO_UNITS = {True: (18, 24), False: (14, 19)}
 # rocprofv3 counter passes over this bench (`--pmc FETCH_SIZE`, then
 # `--pmc WRITE_SIZE`), each scaled by what the counter reads for a 512 MiB
 # device copy (`bench.py --calibrate-copy`: FETCH_SIZE x2.0, WRITE_SIZE x1.0 on
-# MI355X).  Against the 1,207,959,552 algorithmic bytes: +0.018%.  None where
-# not measured.
-MEASURED_TRAFFIC = {"config3": 1208172419}
+# MI355X).  Measured at commit de1782b on the kernel as built there (unchanged
+# since); algorithmic bytes 9 D e T: config3 1,207,959,552 (+0.018%), config4
+# 1,056,964,608 (+0.018%), config5 1,207,959,552 (+0.012%).
+MEASURED_TRAFFIC = {"config3": 1208171969, "config4": 1057150466, "config5": 1208101031}
+TRAFFIC_COMMIT = "de1782b"
 
 
 def _log(msg: str) -> None:
@@ -569,6 +571,7 @@ def main() -> int:
             "unit": "GB/s",
             "frac": round(add_gbs / HBM_PEAK_GBS, 4),
             "traffic": MEASURED_TRAFFIC.get(args.workload),
+            "traffic_measured_at": TRAFFIC_COMMIT,
         },
         "layer_roofline": {
             "algorithmic_bytes_per_step": step_bytes,

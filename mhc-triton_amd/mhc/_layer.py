@@ -6,18 +6,18 @@ The reference composes ``H.mean`` -> ``fused_dynamic_weights`` ->
 that never materialise ``H_residual``:
 
 * node A (``_DynamicLayer`` / ``_StaticLayer`` / ``_GenericLayer``):
-  ``H -> (branch_input, w, link)`` where ``w`` [B,24] f32 packs H_pre (0:4),
-  H_post (4:8) and H_res (8:24), and ``link`` is a view of ``H`` that only the
-  closure consumes;
-* node B (``_LayerAdd``, the closure): ``(link, branch_output, w) -> H_new``,
-  recomputing ``H_res @ H`` on the fly.
+  ``H -> (branch_input, w, link, post_link)`` where ``w`` [B,24] f32 packs
+  H_pre (0:4), H_post (4:8) and H_res (8:24); ``link`` is a view of ``H`` and
+  ``post_link`` an unwritten [B,4] tensor, both consumed only by the closure;
+* node B (``_LayerAdd``, the closure): ``(link, branch_output, w, post_link)
+  -> H_new``, recomputing ``H_res @ H`` on the fly.
 
-Node B consumes ``link`` and ``w``, so the autograd engine runs node B's
-backward before node A's.  Node B's backward computes ``d branch_output`` and
+Node B consumes the links, so the autograd engine runs node B's backward
+before node A's.  Node B's backward computes ``d branch_output`` and
 ``dH_post`` and, instead of its true share of ``dH`` (which the engine would have
 to add to node A's in another full pass), returns ``dH_new`` as the link's
-gradient and ``dH_post`` in columns 4:8 of ``w``'s gradient.  Node A's backward
-reads both and writes the complete ``dH`` once.  The engine sums the closure's
+gradient and ``dH_post`` as post_link's.  Node A's backward reads both and
+writes the complete ``dH`` once.  The engine sums the closure's
 gradients when it is called more than once, and a backward call that reaches
 node B but not node A leaves no state behind.  The traced path (``_library.py``)
 uses the same wiring on the ``torch.ops.mhc`` ops.
@@ -223,13 +223,14 @@ def add_backward(dH_new, branch_output, w):
     return d_bo, dH_post
 
 
-def _link_dH_post(d_w: Optional[torch.Tensor]) -> Optional[torch.Tensor]:
-    """dH_post, as the closure's backward stores it in w's gradient (columns 4:8)."""
-    return None if d_w is None else d_w[:, 4:8].contiguous()
+def _links(H: torch.Tensor, w: torch.Tensor):
+    """The closure's two gradient carriers: a view of H (-> dH_new) and an unwritten [B, 4]
+    tensor in w's dtype (-> dH_post).  The closure reads neither's values."""
+    return H.view_as(H), w.new_empty((w.shape[0], 4))
 
 
 class _DynamicLayer(torch.autograd.Function):
-    """Node A, dynamic fused weights (module.py:119-139 + 177): H -> (branch_input, w, link)."""
+    """Node A, dynamic fused weights (module.py:119-139 + 177): H -> (branch_input, w, link, post_link)."""
 
     @staticmethod
     def forward(ctx, H, phi, H_pre_base, H_post_base, H_res_base, alpha_pre, alpha_post, alpha_res,
@@ -240,12 +241,12 @@ class _DynamicLayer(torch.autograd.Function):
         ctx.iters = iters
         ctx.eps = eps
         ctx.set_materialize_grads(False)
-        return bi, w, H.view_as(H)
+        return (bi, w, *_links(H, w))
 
     @staticmethod
-    def backward(ctx, d_bi, d_w, d_link):
+    def backward(ctx, d_bi, d_w, d_link, d_post):
         H, x, w, aux, *params = ctx.saved_tensors
-        dH, gphi, gbias, galpha = dynamic_backward(H, d_bi, d_link, _link_dH_post(d_w), *params, x, w, aux,
+        dH, gphi, gbias, galpha = dynamic_backward(H, d_bi, d_link, d_post, *params, x, w, aux,
                                                    ctx.iters, ctx.eps, need_dH=ctx.needs_input_grad[0])
         return (dH, *_dynamic_param_grads(params, gphi, gbias, galpha), None, None)
 
@@ -263,7 +264,7 @@ def _static_param_grads(params, gbias):
 
 
 class _StaticLayer(torch.autograd.Function):
-    """Node A, static weights (module.py:108-117 + 177): H -> (branch_input, w, link)."""
+    """Node A, static weights (module.py:108-117 + 177): H -> (branch_input, w, link, post_link)."""
 
     @staticmethod
     def forward(ctx, H, H_pre_base, H_post_base, H_res_base, iters: int):
@@ -272,19 +273,19 @@ class _StaticLayer(torch.autograd.Function):
         ctx.save_for_backward(H, w, *params)
         ctx.iters = iters
         ctx.set_materialize_grads(False)
-        return bi, w, H.view_as(H)
+        return (bi, w, *_links(H, w))
 
     @staticmethod
-    def backward(ctx, d_bi, d_w, d_link):
+    def backward(ctx, d_bi, d_w, d_link, d_post):
         H, w, *params = ctx.saved_tensors
-        dH, gbias = static_backward(H, d_bi, d_link, _link_dH_post(d_w), *params, w, ctx.iters,
+        dH, gbias = static_backward(H, d_bi, d_link, d_post, *params, w, ctx.iters,
                                     need_dH=ctx.needs_input_grad[0])
         return (dH, *_static_param_grads(params, gbias), None)
 
 
 class _GenericLayer(torch.autograd.Function):
     """Node A for weights produced by torch ops (the unfused dynamic path,
-    module.py:141-163): (H, w) -> (branch_input, w, link), differentiable in w."""
+    module.py:141-163): (H, w) -> (branch_input, w, link, post_link), differentiable in w."""
 
     @staticmethod
     def forward(ctx, H, w_in):
@@ -293,29 +294,29 @@ class _GenericLayer(torch.autograd.Function):
         ctx.save_for_backward(H, w)
         ctx.w_dtype = w_in.dtype
         ctx.set_materialize_grads(False)
-        return bi, w.clone() if w is w_in else w, H.view_as(H)
+        return (bi, w.clone() if w is w_in else w, *_links(H, w))
 
     @staticmethod
-    def backward(ctx, d_bi, d_w, d_link):
+    def backward(ctx, d_bi, d_w, d_link, d_post):
         H, w = ctx.saved_tensors
         dH, dpre, dres = mix_backward(H, d_bi, d_link, w, need_dH=ctx.needs_input_grad[0])
-        gw = torch.cat([dpre, torch.zeros_like(dpre), dres], dim=1)
+        gw = torch.cat([dpre, torch.zeros_like(dpre) if d_post is None else d_post, dres], dim=1)
         if d_w is not None:
-            gw = gw + d_w  # columns 4:8 carry the closure's dH_post
+            gw = gw + d_w
         return dH, gw.to(ctx.w_dtype)
 
 
 class _LayerAdd(torch.autograd.Function):
-    """Node B, the closure: (link, branch_output, w) -> H_new = H_res @ H + H_post * branch_output
-    (module.py:179-180 with H_residual recomputed from H).
+    """Node B, the closure: (link, branch_output, w, post_link) -> H_new = H_res @ H +
+    H_post * branch_output (module.py:179-180 with H_residual recomputed from H).
 
-    Its backward returns dH_new as the link's gradient and dH_post in columns 4:8 of w's
-    gradient.  Neither is the true gradient of that input: both only reach node A, which
-    folds dH_new into dH (one pass) and dH_post into the H_post weight gradients.  A backward
-    call that reaches node B but not node A leaves nothing behind."""
+    Its backward returns dH_new as the link's gradient and dH_post [B,4] as post_link's.
+    Neither is the true gradient of that input: both only reach node A, which folds dH_new
+    into dH (one pass) and dH_post into the H_post weight gradients.  It returns no gradient
+    for w.  A backward call that reaches node B but not node A leaves nothing behind."""
 
     @staticmethod
-    def forward(ctx, link, branch_output, w):
+    def forward(ctx, link, branch_output, w, post_link):
         H_new = add_forward(link, branch_output, w)
         ctx.save_for_backward(branch_output, w)
         ctx.h_dtype = link.dtype
@@ -326,7 +327,5 @@ class _LayerAdd(torch.autograd.Function):
         bo, w = ctx.saved_tensors
         dH_new = dH_new.contiguous().to(ctx.h_dtype)
         d_bo, dH_post = add_backward(dH_new, bo, w)
-        d_w = None
-        if ctx.needs_input_grad[2]:
-            d_w = torch.nn.functional.pad(dH_post, (4, 16))
-        return (dH_new if ctx.needs_input_grad[0] else None), d_bo, d_w
+        return ((dH_new if ctx.needs_input_grad[0] else None), d_bo, None,
+                (dH_post if ctx.needs_input_grad[3] else None))

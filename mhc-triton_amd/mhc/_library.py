@@ -10,9 +10,9 @@ nodes and compiles the whole graph around them without a graph break.
   the backward ops.
 * The layer (reference src/mhc/module.py:103-182) uses the same two autograd
   nodes as eager mode (``_layer.py``), on the custom ops: node A returns a view
-  of ``H`` (the *link*) that only the closure consumes; the closure's backward
-  returns ``dH_new`` as the link's gradient and ``dH_post`` inside ``w``'s
-  gradient, and node A writes the complete ``dH`` in one pass.
+  of ``H`` (the *link*) and an unwritten [B,4] tensor (the *post link*) that only
+  the closure consumes; the closure's backward returns ``dH_new`` and ``dH_post``
+  as their gradients, and node A writes the complete ``dH`` in one pass.
 
 Eager calls keep going through the launchers directly: a custom-op dispatch
 costs about 13 us of host time, more than some of the kernels it would wrap.
@@ -23,7 +23,6 @@ from __future__ import annotations
 from typing import Optional, Tuple
 
 import torch
-import torch.nn.functional as F
 from torch import Tensor
 
 from . import _backward as _b
@@ -360,13 +359,8 @@ def _(dH_new, branch_output, w):
     return branch_output.new_empty(branch_output.shape), _f32_like(dH_new, dH_new.shape[0], 4)
 
 
-def _link_grads(d_w: Optional[Tensor]) -> Optional[Tensor]:
-    """dH_post, as the closure stores it in w's gradient (columns 4:8)."""
-    return None if d_w is None else d_w[:, 4:8].contiguous()
-
-
 class DynamicLayer(torch.autograd.Function):
-    """Node A, dynamic fused weights: H -> (branch_input, w, link)."""
+    """Node A, dynamic fused weights: H -> (branch_input, w, link, post_link)."""
 
     @staticmethod
     def forward(ctx, H, phi, H_pre_base, H_post_base, H_res_base, alpha_pre, alpha_post, alpha_res,
@@ -377,18 +371,18 @@ class DynamicLayer(torch.autograd.Function):
         ctx.iters = iters
         ctx.eps = eps
         ctx.set_materialize_grads(False)
-        return bi, w, H.view_as(H)
+        return (bi, w, *_l._links(H, w))
 
     @staticmethod
-    def backward(ctx, d_bi, d_w, d_link):
+    def backward(ctx, d_bi, d_w, d_link, d_post):
         H, x, w, aux, *params = ctx.saved_tensors
         dH, gphi, gbias, galpha = torch.ops.mhc.layer_dynamic_backward(
-            H, d_bi, d_link, _link_grads(d_w), *params, x, w, aux, ctx.iters, ctx.eps)
+            H, d_bi, d_link, d_post, *params, x, w, aux, ctx.iters, ctx.eps)
         return (dH, *_l._dynamic_param_grads(params, gphi, gbias, galpha), None, None)
 
 
 class StaticLayer(torch.autograd.Function):
-    """Node A, static weights: H -> (branch_input, w, link)."""
+    """Node A, static weights: H -> (branch_input, w, link, post_link)."""
 
     @staticmethod
     def forward(ctx, H, H_pre_base, H_post_base, H_res_base, iters: int):
@@ -397,17 +391,18 @@ class StaticLayer(torch.autograd.Function):
         ctx.save_for_backward(H, w, *params)
         ctx.iters = iters
         ctx.set_materialize_grads(False)
-        return bi, w, H.view_as(H)
+        return (bi, w, *_l._links(H, w))
 
     @staticmethod
-    def backward(ctx, d_bi, d_w, d_link):
+    def backward(ctx, d_bi, d_w, d_link, d_post):
         H, w, *params = ctx.saved_tensors
-        dH, gbias = torch.ops.mhc.layer_static_backward(H, d_bi, d_link, _link_grads(d_w), *params, w, ctx.iters)
+        dH, gbias = torch.ops.mhc.layer_static_backward(H, d_bi, d_link, d_post, *params, w, ctx.iters)
         return (dH, *_l._static_param_grads(params, gbias), None)
 
 
 class GenericLayer(torch.autograd.Function):
-    """Node A for weights produced by torch ops (the unfused dynamic path): (H, w) -> (branch_input, w, link)."""
+    """Node A for weights produced by torch ops (the unfused dynamic path):
+    (H, w) -> (branch_input, w, link, post_link)."""
 
     @staticmethod
     def forward(ctx, H, w_in):
@@ -416,25 +411,25 @@ class GenericLayer(torch.autograd.Function):
         ctx.save_for_backward(H, w)
         ctx.w_dtype = w_in.dtype
         ctx.set_materialize_grads(False)
-        return bi, w.clone() if w is w_in else w, H.view_as(H)
+        return (bi, w.clone() if w is w_in else w, *_l._links(H, w))
 
     @staticmethod
-    def backward(ctx, d_bi, d_w, d_link):
+    def backward(ctx, d_bi, d_w, d_link, d_post):
         H, w = ctx.saved_tensors
         dH, dpre, dres = torch.ops.mhc.layer_mix_backward(H, d_bi, d_link, w)
-        gw = torch.cat([dpre, torch.zeros_like(dpre), dres], dim=1)
+        gw = torch.cat([dpre, torch.zeros_like(dpre) if d_post is None else d_post, dres], dim=1)
         if d_w is not None:
-            gw = gw + d_w  # includes the closure's dH_post in columns 4:8
+            gw = gw + d_w
         return dH, gw.to(ctx.w_dtype)
 
 
 class LayerAdd(torch.autograd.Function):
-    """Node B, the closure: (link, branch_output, w) -> H_new.  Its backward returns
-    dH_new as the link's gradient and dH_post in columns 4:8 of w's gradient, for
-    node A to consume (neither is the true gradient of those inputs)."""
+    """Node B, the closure: (link, branch_output, w, post_link) -> H_new.  Its backward returns
+    dH_new as the link's gradient and dH_post [B,4] as post_link's, for node A to consume
+    (neither is the true gradient of those inputs), and no gradient for w."""
 
     @staticmethod
-    def forward(ctx, link, branch_output, w):
+    def forward(ctx, link, branch_output, w, post_link):
         ctx.save_for_backward(branch_output, w)
         ctx.h_dtype = link.dtype
         return torch.ops.mhc.layer_add_forward(link, branch_output, w)
@@ -444,7 +439,7 @@ class LayerAdd(torch.autograd.Function):
         bo, w = ctx.saved_tensors
         dH_new = dH_new.to(ctx.h_dtype)
         d_bo, dH_post = torch.ops.mhc.layer_add_backward(dH_new, bo, w)
-        return dH_new, d_bo, F.pad(dH_post, (4, 16))
+        return dH_new, d_bo, None, dH_post
 
 
 # --------------------------------------------------------------------------

@@ -162,21 +162,21 @@ class HyperConnection(nn.Module):
         H = H.contiguous()
         version = H._version
         if not self.dynamic:
-            bi, w, link = _layer._StaticLayer.apply(H, self.H_pre_base, self.H_post_base, self.H_res_base,
-                                                    self.sinkhorn_iters)
+            bi, w, link, post_link = _layer._StaticLayer.apply(H, self.H_pre_base, self.H_post_base,
+                                                               self.H_res_base, self.sinkhorn_iters)
         elif self.use_fused_weights:
-            bi, w, link = _layer._DynamicLayer.apply(H, self.phi, self.H_pre_base, self.H_post_base,
-                                                     self.H_res_base, self.alpha_pre, self.alpha_post,
-                                                     self.alpha_res, self.sinkhorn_iters, self.eps)
+            bi, w, link, post_link = _layer._DynamicLayer.apply(H, self.phi, self.H_pre_base, self.H_post_base,
+                                                                self.H_res_base, self.alpha_pre, self.alpha_post,
+                                                                self.alpha_res, self.sinkhorn_iters, self.eps)
         else:
-            bi, w, link = _layer._GenericLayer.apply(H, self._unfused_weights(H))
+            bi, w, link, post_link = _layer._GenericLayer.apply(H, self._unfused_weights(H))
 
         def add_residual(branch_output: torch.Tensor) -> torch.Tensor:
             if H._version != version:
                 raise RuntimeError(
                     "HyperConnection: H was modified in place after forward(H); add_residual recomputes "
                     "H_res @ H from H and would mix the modified values. Clone H before modifying it.")
-            return _layer._LayerAdd.apply(link, branch_output, w)
+            return _layer._LayerAdd.apply(link, branch_output, w, post_link)
 
         return bi, add_residual
 
@@ -184,17 +184,17 @@ class HyperConnection(nn.Module):
         """The same two nodes as ``forward``, on the torch.library ops, with the closure's
         gradients passed to node A through a link output instead of a side channel."""
         if not self.dynamic:
-            bi, w, link = _library.StaticLayer.apply(H, self.H_pre_base, self.H_post_base, self.H_res_base,
-                                                     self.sinkhorn_iters)
+            bi, w, link, post_link = _library.StaticLayer.apply(H, self.H_pre_base, self.H_post_base,
+                                                                self.H_res_base, self.sinkhorn_iters)
         elif self.use_fused_weights:
-            bi, w, link = _library.DynamicLayer.apply(H, self.phi, self.H_pre_base, self.H_post_base,
-                                                      self.H_res_base, self.alpha_pre, self.alpha_post,
-                                                      self.alpha_res, self.sinkhorn_iters, self.eps)
+            bi, w, link, post_link = _library.DynamicLayer.apply(H, self.phi, self.H_pre_base, self.H_post_base,
+                                                                 self.H_res_base, self.alpha_pre, self.alpha_post,
+                                                                 self.alpha_res, self.sinkhorn_iters, self.eps)
         else:
-            bi, w, link = _library.GenericLayer.apply(H, self._unfused_weights(H, traced=True))
+            bi, w, link, post_link = _library.GenericLayer.apply(H, self._unfused_weights(H, traced=True))
 
         def add_residual(branch_output: torch.Tensor) -> torch.Tensor:
-            return _library.LayerAdd.apply(link, branch_output, w)
+            return _library.LayerAdd.apply(link, branch_output, w, post_link)
 
         return bi, add_residual
 
