@@ -93,10 +93,86 @@ def _parse():
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="only run 3 plain device copies of 512 MiB (the known-size kernel that scales "
                          "rocprofv3 FETCH_SIZE / WRITE_SIZE readings into bytes) and exit")
+    ap.add_argument("--stream-ceiling", action="store_true",
+                    help="only time the streaming-ceiling probe (libmhc_probe.so): kernels shaped like the "
+                         "layer's streaming kernels that move the same read / write mixes at config-3 "
+                         "size and do nothing else, over occupancy caps and cache policies, and exit")
     return ap.parse_args()
 
 
 COPY_BYTES = 512 << 20
+
+# (mix, input rows per token in three arrays, output rows, layer kernels with that mix)
+PROBE_MIXES = [
+    ("read 1:0", (1, 0, 0), 0, "plain read"),
+    ("write 0:1", (0, 0, 0), 1, "plain write"),
+    ("copy 1:1", (1, 0, 0), 1, "plain copy"),
+    ("4:0", (4, 0, 0), 0, "colsum_kernel (mean-pool)"),
+    ("4:1", (4, 0, 0), 1, "mix_fwd_kernel<BI> (branch_input)"),
+    ("5:4", (4, 1, 0), 4, "mix_fwd_kernel<RES,ADD_BO> (closure forward); dh_kernel (pass C)"),
+    ("5:1", (4, 1, 0), 1, "add_residual_bwd_kernel (closure backward)"),
+    ("9:0", (4, 4, 1), 0, "mix_bwd_kernel<REDUCE> (pass B)"),
+]
+
+
+def _stream_ceiling(tokens: int = 16384, row_bytes: int = 8192, caps=(0, 2, 3, 4, 6, 8), reps: int = 20,
+                    warm: int = 3) -> dict:
+    """Best HBM rate of each read / write mix of the layer's streaming kernels, as moved by a kernel of the
+    same launch shape (one 16-byte vector per lane and row, buffer resources, one tile per workgroup) that
+    computes nothing: the ceiling those kernels are measured against.  Config-3 layout (T = 16384 tokens,
+    8 KiB rows); the one-row mixes run over 4 T tokens, so every array is 512 MiB."""
+    import ctypes
+
+    import torch
+
+    path = os.path.join(ROOT, "mhc-triton_amd", "mhc", "libmhc_probe.so")
+    if not os.path.exists(path):
+        raise RuntimeError(f"{path} is not built (make -C mhc-triton_amd)")
+    lib = ctypes.CDLL(path)
+    fn = lib.mhc_probe_stream
+    fn.restype = ctypes.c_int
+    fn.argtypes = [ctypes.c_int] * 4 + [ctypes.c_void_p] * 4 + [ctypes.c_int64] * 2 + [ctypes.c_int] * 2 + \
+        [ctypes.c_void_p] * 2
+    dev = "cuda:0"
+    sink = torch.zeros(256, dtype=torch.int32, device=dev)
+    out = {}
+    for name, (na, nb, nc), nw, kernels in PROBE_MIXES:
+        toks = tokens * (4 if na + nb + nc + nw <= 2 else 1)
+
+        def arr(rows):
+            return torch.zeros(max(rows, 1) * toks * row_bytes // 4, dtype=torch.int32, device=dev)
+
+        a, b, c, w = arr(na), arr(nb), arr(nc), arr(nw)
+        nbytes = toks * (na + nb + nc + nw) * row_bytes
+        stream = torch.cuda.current_stream().cuda_stream
+
+        def launch(cap, nt):
+            rc = fn(na, nb, nc, nw, a.data_ptr(), b.data_ptr(), c.data_ptr(), w.data_ptr(), toks, row_bytes,
+                    cap, nt, sink.data_ptr(), stream)
+            if rc:
+                raise RuntimeError(f"mhc_probe_stream({name}) returned {rc}")
+
+        runs = {}
+        for nt in (1, 0):
+            for cap in caps:
+                for _ in range(warm):
+                    launch(cap, nt)
+                ev0 = torch.cuda.Event(enable_timing=True)
+                ev1 = torch.cuda.Event(enable_timing=True)
+                ev0.record()
+                for _ in range(reps):
+                    launch(cap, nt)
+                ev1.record()
+                torch.cuda.synchronize()
+                us = ev0.elapsed_time(ev1) * 1e3 / reps
+                runs[f"{'nt' if nt else 'plain'} cap{cap}"] = {
+                    "us": round(us, 1), "frac": round(nbytes / (us * 1e-6) / (HBM_PEAK_GBS * 1e9), 4)}
+        best = max(runs, key=lambda k: runs[k]["frac"])
+        out[name] = {"layer_kernels": kernels, "bytes": nbytes, "best": best, **runs[best], "runs": runs}
+        _log(f"stream ceiling {name}: best {best} {runs[best]['us']} us {runs[best]['frac']:.3f}")
+        del a, b, c, w
+        torch.cuda.empty_cache()
+    return out
 
 
 def _calibrate_copy() -> int:
@@ -508,6 +584,12 @@ def main() -> int:
         return 1
     if args.calibrate_copy:
         return _calibrate_copy()
+    if args.stream_ceiling:
+        print(json.dumps({"stream_ceiling": _stream_ceiling(), "unit": "us per launch", "peak_GBps": HBM_PEAK_GBS,
+                          "layout": "config 3: 16384 tokens x 8 KiB rows per array row",
+                          "caps": "cap0 = no occupancy cap, capN = at most N workgroups per CU",
+                          "device": torch.cuda.get_device_name(0)}), flush=True)
+        return 0
     from mhc import _lib
 
     _lib.load()  # fails loudly when the HIP library is not built

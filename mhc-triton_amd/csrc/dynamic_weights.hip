@@ -32,11 +32,13 @@ static DynPlan dyn_plan(int64_t R, int64_t K) {
 
 static size_t align256(size_t v) { return (v + 255) & ~(size_t)255; }
 
-// MFMA plan for bf16 x with many rows: workgroups of kMfmaRowsWg rows, and the
-// K steps (16 k each) split into nK chunks so that about 2048 workgroups
-// (8 per CU, 4 resident at a time) stream x; at least 16 steps per chunk.  At
-// R = K = 16384 (nK = 16) the kernel runs at 4.2 TB/s; 1024 or 4096
-// workgroups were slower.
+// MFMA plan for bf16 x with many rows: workgroups of kMfmaRowsWg rows
+// (kMfmaWaves waves of 32 rows), and the K steps (16 k each) split into nK
+// chunks so that about 8192 waves stream x (two rounds of one 16-wave
+// workgroup per CU); at least 16 steps per chunk.  At R = K = 16384 (nK = 16):
+// 123.7 us with 4-wave workgroups of 128 rows, 119.6 with 8 waves, 116.0 with
+// 16, since every workgroup stages the same phi fragments once for all its
+// waves (phi L2->LDS traffic per x byte: 75% at 4 waves, 19% at 16).
 constexpr int64_t kMfmaMinRows = 64;
 constexpr int64_t kMfmaWgRows = kMfmaRowsWg;
 
@@ -55,7 +57,8 @@ static MfmaPlan mfma_plan(int64_t R, int64_t K) {
   MfmaPlan p;
   p.nsteps = K / 16;
   const int64_t wg_rows = (R + kMfmaWgRows - 1) / kMfmaWgRows;
-  int64_t nk = (2048 + wg_rows - 1) / wg_rows;
+  const int64_t target_wg = 2048 * 4 / kMfmaWaves;  // 8192 waves
+  int64_t nk = (target_wg + wg_rows - 1) / wg_rows;
   const int64_t max_nk = p.nsteps / 16 > 0 ? p.nsteps / 16 : 1;
   if (nk > max_nk) nk = max_nk;
   if (nk < 1) nk = 1;
@@ -110,7 +113,7 @@ extern "C" int mhc_dynamic_weights_forward(const void* x, int dtype_x, const flo
     dynw_pack_phi_kernel<><<<dim3((unsigned)((m.nsteps * 64 + kThreads - 1) / kThreads)), kThreads, 0, st>>>(
         phi, packed, m.nsteps);
     if (int rc = hip_status(hipGetLastError(), "dynamic_weights_forward pack launch")) return rc;
-    dynw_mfma_kernel<><<<dim3((unsigned)((R + kMfmaWgRows - 1) / kMfmaWgRows), (unsigned)m.nK), kThreads, 0, st>>>(
+    dynw_mfma_kernel<><<<dim3((unsigned)((R + kMfmaWgRows - 1) / kMfmaWgRows), (unsigned)m.nK), 64 * kMfmaWaves, 0, st>>>(
         (const __bf16*)x, packed, part, R, K, m.nK, m.spc);
     if (int rc = hip_status(hipGetLastError(), "dynamic_weights_forward mfma launch")) return rc;
     nK = m.nK;
@@ -160,7 +163,8 @@ extern "C" size_t mhc_dynamic_weights_backward_workspace_bytes(int64_t R, int64_
   if (R <= 0) return 0;
   const WidePlan w = wide_plan(R, K);
   size_t need = align256((size_t)R * kRow * sizeof(float));
-  if (w.nR > 1) need += align256((size_t)w.nR * K * kOut * sizeof(float));
+  // split rows: the grad_phi chunk partials, and the grad_bias / grad_alpha chunk records
+  if (w.nR > 1) need += align256((size_t)w.nR * K * kOut * sizeof(float)) + align256((size_t)w.nR * 27 * sizeof(float));
   return need;
 }
 
@@ -206,14 +210,18 @@ extern "C" int mhc_dynamic_weights_backward(const void* x, int dtype_x, const fl
   if (int rc = hip_status(hipGetLastError(), "dynamic_weights_backward rows launch")) return rc;
   const bool phi_vec = aligned16(phi);
   const WidePlan w = wide_plan(R, K);
-  float* gphi_part =
-      (w.nR > 1 && grad_phi) ? (float*)((char*)workspace + align256((size_t)R * kRow * sizeof(float))) : nullptr;
+  char* split_ws = (char*)workspace + align256((size_t)R * kRow * sizeof(float));
+  float* gphi_part = (w.nR > 1 && grad_phi) ? (float*)split_ws : nullptr;
+  float* bias_part = nullptr;  // MFMA path, split rows: per-chunk grad_bias / grad_alpha records
   int rc;
   if (dtype_x == MHC_DTYPE_BF16 && R >= kMfmaMinRows && K % 8 == 0 && aligned16(x) && (!grad_x || aligned16(grad_x))) {
     // bf16 rows in bulk: grad_x and grad_phi on MFMA.
-    const unsigned ncb = (unsigned)((K + kBwdCols - 1) / kBwdCols);
-    dynw_bwd_mfma_kernel<><<<dim3(ncb, (unsigned)w.nR), kThreads, 0, st>>>(
-        (const __bf16*)x, phi, rowbuf, (__bf16*)grad_x, grad_phi, gphi_part, grad_bias, grad_alpha, R, K, w.RC);
+    if (w.nR > 1 && (grad_bias || grad_alpha))
+      bias_part = (float*)(split_ws + align256((size_t)w.nR * K * kOut * sizeof(float)));
+    const unsigned ncb = (unsigned)((K + 32 * kBwdWaves - 1) / (32 * kBwdWaves));
+    dynw_bwd_mfma_kernel<><<<dim3(ncb, (unsigned)w.nR), 64 * kBwdWaves, 0, st>>>(
+        (const __bf16*)x, phi, rowbuf, (__bf16*)grad_x, grad_phi, gphi_part, bias_part, grad_bias, grad_alpha, R, K,
+        w.RC);
     rc = hip_status(hipGetLastError(), "dynamic_weights_backward mfma launch");
   } else {
     rc = MHC_DISPATCH_DTYPE(dtype_x, [&] {
@@ -222,10 +230,11 @@ extern "C" int mhc_dynamic_weights_backward(const void* x, int dtype_x, const fl
                         "dynamic_weights_backward wide launch");
     });
   }
-  if (rc || !gphi_part) return rc;
-  const int64_t n = K * kOut;
-  dynw_gphi_reduce_kernel<><<<dim3((unsigned)((n + kThreads - 1) / kThreads)), kThreads, 0, st>>>(gphi_part, grad_phi,
-                                                                                                n, w.nR);
+  if (rc || (!gphi_part && !bias_part)) return rc;
+  const int64_t n = gphi_part ? K * kOut : 0;
+  const int64_t nt = n + (bias_part ? 27 : 0);
+  dynw_gphi_reduce_kernel<><<<dim3((unsigned)((nt + kThreads - 1) / kThreads)), kThreads, 0, st>>>(
+      gphi_part, grad_phi, n, w.nR, bias_part, grad_bias, grad_alpha);
   return hip_status(hipGetLastError(), "dynamic_weights_backward grad_phi reduce launch");
 }
 

@@ -132,44 +132,52 @@ __global__ __launch_bounds__(kThreads) void dynw_pack_phi_kernel(const float* __
   packed[(s * 3 + 2) * 64 + lane] = __builtin_bit_cast(u32x4, lo);
 }
 
-// One workgroup per 128-row tile and K chunk (wave w owns rows 32w..32w+31).
-// A group of kMfmaGrpSteps = 4 steps covers 128 bytes of each row.  A wave
-// loads its 32 rows x 128 bytes with fully coalesced 16-byte loads (load j:
-// rows 8j .. 8j+7, lane l at row 8j + l/8, chunk l%8), one group ahead of the
-// MFMAs, and passes them through its own LDS tile into the fragment layout
-// (step j of lane l: row l%32, chunk 2j + l/32; chunk c of row r is stored in
-// slot c ^ (r & 7), so neither side has bank conflicts).  Loading the
-// fragments straight from global memory (32 rows x 32 bytes per load) ran at
-// 158 us against 128 us this way at R = K = 16384, with the same results.
-// The x rows go through one buffer span per workgroup: rows past R read as
-// zeros; chunks of steps past the K chunk are read but never used.  The phi
-// fragments of a group are the same for all four waves, so the workgroup
+// One workgroup per tile of 32 * NW rows and a K chunk (wave w owns rows
+// 32w..32w+31).  A group of kMfmaGrpSteps = 4 steps covers 128 bytes of each
+// row.  A wave loads its 32 rows x 128 bytes with fully coalesced 16-byte
+// loads (load j: rows 8j .. 8j+7, lane l at row 8j + l/8, chunk l%8), one
+// group ahead of the MFMAs, and passes them through its own LDS tile into the
+// fragment layout (step j of lane l: row l%32, chunk 2j + l/32; chunk c of row
+// r is stored in slot c ^ (r & 7), so neither side has bank conflicts).
+// Loading the fragments straight from global memory (32 rows x 32 bytes per
+// load) ran at 158 us against 128 us this way at R = K = 16384, with the same
+// results.  The x rows go through one buffer span per workgroup: rows past R
+// read as zeros; chunks of steps past the K chunk are read but never used.
+// The phi fragments of a group are the same for all waves, so the workgroup
 // stages them once in double-buffered LDS (one barrier per group) instead of
 // every wave loading them from L2 (per-wave phi loads competing with the x
-// stream had cost ~45 us).  Each 16-k step's three MFMAs start from zero and
-// the step result is added into `acc` with fp32 VALU adds (a long MFMA
+// stream had cost ~45 us); the more waves share a stage, the less of that
+// L2 -> LDS traffic per x byte.  Each 16-k step's three MFMAs start from zero
+// and the step result is added into `acc` with fp32 VALU adds (a long MFMA
 // accumulation chain drifts by ~1e-5 relative over 1024 steps; the
-// round-to-nearest adds do not).  Writes the same 25-float partial records as
-// dynw_partial_kernel: part[r][kc][0:24] and the row's sum of squares [24],
-// which the VALU forms from the A fragments alongside the MFMAs.  Requires
-// K % 16 == 0, a 16-byte aligned x and 128 rows of K under 2^31 bytes.
-constexpr int kMfmaRowsWg = 128;
+// round-to-nearest adds do not; a chain over a 4-step group needs 16 more
+// live VGPRs than 4 waves per SIMD leave).  Writes the same 25-float partial
+// records as dynw_partial_kernel: part[r][kc][0:24] and the row's sum of
+// squares [24], which the VALU forms from the A fragments alongside the MFMAs
+// (v_dot2_f32_bf16 would take a quarter of the instructions, but its sums are
+// not fp32-accurate: H_pre moved by 6e-3 relative at K = 4096).  Requires
+// K % 16 == 0, a 16-byte aligned x and 32 * NW rows of K under 2^31 bytes.
+constexpr int kMfmaWaves = 16;                               // waves per workgroup
+constexpr int kMfmaRowsWg = 32 * kMfmaWaves;
 constexpr int kMfmaGrpSteps = 4;                             // 16-k steps per group
 constexpr int kMfmaPhiGrp = kMfmaGrpSteps * 3 * 64;          // 16-byte phi chunks per group
-constexpr int kMfmaPhiPerThread = kMfmaPhiGrp / kThreads;    // 3
-static_assert(kMfmaPhiGrp % kThreads == 0, "phi chunks split evenly over the workgroup");
 
-template <int = 0>
-__global__ __launch_bounds__(kThreads) void dynw_mfma_kernel(const __bf16* __restrict__ x,
-                                                             const u32x4* __restrict__ packed,
-                                                             float* __restrict__ part, int64_t R, int64_t K, int nK,
-                                                             int64_t steps_per_chunk) {
+// Four waves per SIMD (at most 128 VGPRs): the x loads in flight set the pace.
+// With NW = 16 one workgroup fills a CU (LDS: 24 KiB of phi stages + 4 KiB per wave).
+template <int NW = kMfmaWaves>
+__global__ __launch_bounds__(64 * NW, 4) void dynw_mfma_kernel(const __bf16* __restrict__ x,
+                                                            const u32x4* __restrict__ packed,
+                                                            float* __restrict__ part, int64_t R, int64_t K, int nK,
+                                                            int64_t steps_per_chunk) {
   constexpr int G = kMfmaGrpSteps;
+  constexpr int kWgThreads = 64 * NW;
+  constexpr int kRowsWg = 32 * NW;
+  constexpr int kPhiPerThread = (kMfmaPhiGrp + kWgThreads - 1) / kWgThreads;
   __shared__ __attribute__((aligned(16))) u32x4 phs[2][kMfmaPhiGrp];
-  __shared__ __attribute__((aligned(16))) u32x4 ast[4][32 * 8];  // per wave: 32 rows x 8 chunks
+  __shared__ __attribute__((aligned(16))) u32x4 ast[NW][32 * 8];  // per wave: 32 rows x 8 chunks
   const int wave = threadIdx.x >> 6;
   const int lane = threadIdx.x & 63;
-  const int64_t rb0 = (int64_t)blockIdx.x * kMfmaRowsWg + wave * 32;
+  const int64_t rb0 = (int64_t)blockIdx.x * kRowsWg + wave * 32;
   const int kc = blockIdx.y;
   const int64_t nsteps = K / 16;
   const int64_t s_beg = (int64_t)kc * steps_per_chunk;
@@ -178,12 +186,12 @@ __global__ __launch_bounds__(kThreads) void dynw_mfma_kernel(const __bf16* __res
   const int64_t row = rb0 + (lane & 31);
   const bool rok = row < R;
   const int lrow = lane >> 3, lchk = lane & 7;
-  const int64_t rbw = (int64_t)blockIdx.x * kMfmaRowsWg;
-  const int64_t nrow = R - rbw < kMfmaRowsWg ? R - rbw : kMfmaRowsWg;
+  const int64_t rbw = (int64_t)blockIdx.x * kRowsWg;
+  const int64_t nrow = R - rbw < kRowsWg ? R - rbw : kRowsWg;
   const Span<__bf16, true> xs(x + rbw * K, nrow * K);
   const uint32_t lbase = (uint32_t)((wave * 32 + lrow) * K + 8 * lchk);
   u32x4 a[2][G];
-  u32x4 pv[kMfmaPhiPerThread];
+  u32x4 pv[kPhiPerThread];
   auto aload = [&](int64_t g, u32x4 (&d)[G]) {
     const uint32_t kofs = (uint32_t)((s_beg + g * G) * 16);
 #pragma unroll
@@ -206,38 +214,47 @@ __global__ __launch_bounds__(kThreads) void dynw_mfma_kernel(const __bf16* __res
     const int64_t base = (s_beg + g * G) * 3 * 64;
     const int64_t lim = nsteps * 3 * 64;
 #pragma unroll
-    for (int i = 0; i < kMfmaPhiPerThread; ++i) {
-      const int64_t c = base + threadIdx.x + kThreads * i;
-      pv[i] = c < lim ? packed[c] : u32x4{0u, 0u, 0u, 0u};
+    for (int i = 0; i < kPhiPerThread; ++i) {
+      const int slot = threadIdx.x + kWgThreads * i;
+      const int64_t c = base + slot;
+      if (kMfmaPhiGrp % kWgThreads == 0 || slot < kMfmaPhiGrp)
+        pv[i] = c < lim ? packed[c] : u32x4{0u, 0u, 0u, 0u};
     }
   };
   auto pstore = [&](int buf) {
 #pragma unroll
-    for (int i = 0; i < kMfmaPhiPerThread; ++i) phs[buf][threadIdx.x + kThreads * i] = pv[i];
+    for (int i = 0; i < kPhiPerThread; ++i) {
+      const int slot = threadIdx.x + kWgThreads * i;
+      if (kMfmaPhiGrp % kWgThreads == 0 || slot < kMfmaPhiGrp) phs[buf][slot] = pv[i];
+    }
   };
   f32x16 acc, zero;
 #pragma unroll
   for (int i = 0; i < 16; ++i) acc[i] = zero[i] = 0.f;
-  float ss = 0.f;
+  float ss = 0.f, ss_hi = 0.f;
   auto compute = [&](int64_t g, const u32x4 (&d)[G], int buf) {
 #pragma unroll
     for (int j = 0; j < G; ++j) {
       if (s_beg + g * G + j < s_end) {
+        f32x16 st = zero;
         const u32x4 b0 = phs[buf][(j * 3 + 0) * 64 + lane];
         const u32x4 b1 = phs[buf][(j * 3 + 1) * 64 + lane];
         const u32x4 b2 = phs[buf][(j * 3 + 2) * 64 + lane];
         const bf16x8 av = __builtin_bit_cast(bf16x8, d[j]);
         // smallest part first: the step sum sees the corrections before the bulk
-        f32x16 st = __builtin_amdgcn_mfma_f32_32x32x16_bf16(av, __builtin_bit_cast(bf16x8, b2), zero, 0, 0, 0);
+        st = __builtin_amdgcn_mfma_f32_32x32x16_bf16(av, __builtin_bit_cast(bf16x8, b2), st, 0, 0, 0);
         st = __builtin_amdgcn_mfma_f32_32x32x16_bf16(av, __builtin_bit_cast(bf16x8, b1), st, 0, 0, 0);
         st = __builtin_amdgcn_mfma_f32_32x32x16_bf16(av, __builtin_bit_cast(bf16x8, b0), st, 0, 0, 0);
-        acc += st;
+        // x^2 of the lane's 8 values: the low and high halves of each dword
+        // accumulate separately (two VALU ops per value)
 #pragma unroll
         for (int c = 0; c < 4; ++c) {
           const float lo_ = __uint_as_float(d[j][c] << 16);
           const float hi_ = __uint_as_float(d[j][c] & 0xffff0000u);
-          ss += lo_ * lo_ + hi_ * hi_;
+          ss = fmaf(lo_, lo_, ss);
+          ss_hi = fmaf(hi_, hi_, ss_hi);
         }
+        acc += st;
       }
     }
   };
@@ -275,6 +292,7 @@ __global__ __launch_bounds__(kThreads) void dynw_mfma_kernel(const __bf16* __res
       if (r < R) part[(r * nK + kc) * kPart + col] = acc[i];
     }
   }
+  ss += ss_hi;
   const float sst = ss + __shfl_xor(ss, 32, 64);  // the two k halves of one row
   if (lane < 32 && rok) part[(row * nK + kc) * kPart + kOut] = sst;
 }
@@ -613,14 +631,17 @@ inline hipError_t launch_dynw_bwd_wide(const TX* x, const float* phi, const floa
 //   grad_x [R, K]  = G [R, 24] phi^T [24, K] + coef [R] x      (bf16 out)
 //   grad_phi [K, 24] = x^T [K, R] G [R, 24]                      (f32, per chunk)
 // with G = grad_raw = rowbuf[r][0:24] and coef = rowbuf[r][24].  A workgroup
-// owns 128 columns (wave w: the 32-column block at 32 w) and a chunk of RC
-// rows, walked in 64-row blocks (two barriers each; with 32-row blocks the
-// kernel took 234.9 us against 224.3 us at R = K = 16384, same results).  Per
-// block the x tile (bf16) and the G rows are staged in LDS with 16-byte loads,
-// the next block's loads being in flight meanwhile.  G is split into bf16 hi + lo planes once, as it is staged (fp32
-// products then take hi*hi + hi*lo + lo*hi, relative error ~2^-16):
+// of kBwdWaves waves owns kBwdCols = 32 * kBwdWaves columns (wave w: the
+// 32-column block at 32 w) and a chunk of RC rows, walked in 64-row blocks.
+// The x strip a workgroup reads and the grad_x strip it writes are 512 bytes
+// of each row: as a plain copy, 256-byte strips (128 columns, four waves)
+// peak at 67% of 8 TB/s and 512-byte strips at 79%, at the same grid size.
+// Per block the x tile (bf16) and the G rows are staged in LDS, with the next
+// two blocks' loads in flight (streaming loads and stores: x is read and
+// grad_x written once).  G is split into bf16 hi + lo planes once, as it is
+// staged (fp32 products then take hi*hi + hi*lo + lo*hi, relative error ~2^-16):
 //   grad_x: computed transposed, grad_x^T = phi G^T, so that the A operand is
-//           the workgroup's phi fragments (registers for the whole kernel) and
+//           the wave's phi fragments (registers for the whole kernel) and
 //           the B operand 16-byte reads of the G planes.  Each lane then holds
 //           one row and four runs of four consecutive columns: the epilogue
 //           adds coef * x with 8-byte LDS reads and writes bf16 to an LDS tile
@@ -630,14 +651,19 @@ inline hipError_t launch_dynw_bwd_wide(const TX* x, const float* phi, const floa
 //           (ds_read_b64_tr_b16: within each 16-lane group, lane i receives
 //           element i % 4 of the 8 bytes lane 4 j + i / 4 addresses, j = 0..3),
 //           accumulated in the MFMA registers over the chunk.
-// Against per-wave splits, 2-byte LDS gathers and a column-per-lane epilogue
-// the kernel is 10% faster with bit-identical results.  Requires K % 8 == 0
-// and 16-byte aligned x and grad_x.  Grid (K / 128 column blocks, row chunks);
-// outputs as dynw_bwd_wide_kernel: grad_phi direct with one chunk, else
-// per-chunk partials; workgroup (0, 0) also sums grad_bias and grad_alpha.
-constexpr int kBwdCols = 128;             // columns per workgroup: one 32-column block per wave
+// The LDS padding leaves 2-way bank conflicts on the transpose and epilogue
+// reads; making those reads conflict-free (wrong results, timing only) saved
+// 1%, and without any x / grad_x traffic the kernel runs in under half its
+// time: it is bound by the x read and grad_x write.  Requires K % 8 == 0 and
+// 16-byte aligned x and grad_x.  Grid (K / kBwdCols column blocks, row
+// chunks); outputs as dynw_bwd_wide_kernel: grad_phi direct with one chunk,
+// else per-chunk partials.  Column block 0 of each row chunk also sums the
+// chunk's grad_bias / grad_alpha records after its main loop: into gbias /
+// galpha with one chunk, else into bias_part[chunk][27], which
+// dynw_gphi_reduce_kernel adds in chunk order.
+constexpr int kBwdWaves = 8;              // waves per workgroup (32 columns each)
+constexpr int kBwdMinWaves = 2;           // waves per SIMD the register allocation must allow
 constexpr int kBwdRows = 64;              // rows per staged block (two 32-row MFMA halves)
-constexpr int kBwdXPitch = kBwdCols + 8;  // bf16 per padded LDS row of the x / grad_x tiles
 constexpr int kBwdGPitch = 40;            // bf16 per LDS row of the split G planes (columns 24..31 zero)
 
 typedef short s16x4 __attribute__((ext_vector_type(4)));
@@ -650,44 +676,41 @@ __device__ __forceinline__ u32x2 lds_read_tr16(const __bf16* p) {
   return __builtin_bit_cast(u32x2, __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(p)));
 }
 
-template <int = 0>
-__global__ __launch_bounds__(kThreads) void dynw_bwd_mfma_kernel(const __bf16* __restrict__ x,
-                                                                 const float* __restrict__ phi,
-                                                                 const float* __restrict__ rowbuf,
-                                                                 __bf16* __restrict__ gx, float* __restrict__ gphi,
-                                                                 float* __restrict__ gphi_part,
-                                                                 float* __restrict__ gbias,
-                                                                 float* __restrict__ galpha, int64_t R, int64_t K,
-                                                                 int64_t RC) {
-  constexpr int TR = kBwdRows, NX = TR / 16, NG = TR / 32;
+template <int NW = kBwdWaves, int MINW = kBwdMinWaves>
+__global__ __launch_bounds__(64 * NW, MINW) void dynw_bwd_mfma_kernel(const __bf16* __restrict__ x,
+                                                                    const float* __restrict__ phi,
+                                                                    const float* __restrict__ rowbuf,
+                                                                    __bf16* __restrict__ gx, float* __restrict__ gphi,
+                                                                    float* __restrict__ gphi_part,
+                                                                    float* __restrict__ bias_part,
+                                                                    float* __restrict__ gbias,
+                                                                    float* __restrict__ galpha, int64_t R, int64_t K,
+                                                                    int64_t RC) {
+  constexpr int kBwdThreads = 64 * NW;
+  constexpr int kBwdCols = 32 * NW;            // columns per workgroup
+  constexpr int kBwdXPitch = kBwdCols + 8;     // bf16 per padded LDS row of the x / grad_x tiles
+  constexpr int TR = kBwdRows;
+  constexpr int XLPR = kBwdCols / 8;           // lanes per x row (16 bytes each)
+  constexpr int XRPP = kBwdThreads / XLPR;     // x rows per pass of the workgroup
+  constexpr int NX = TR / XRPP;                // 16-byte x vectors per lane per block
+  constexpr int GRPP = kBwdThreads / 8;        // G rows per pass (8 lanes per 32-float row)
+  constexpr int NG = TR / GRPP > 0 ? TR / GRPP : 1;
+  static_assert(TR % XRPP == 0 && (TR % GRPP == 0 || GRPP >= TR), "block shape");
   __shared__ __attribute__((aligned(16))) __bf16 xs[TR * kBwdXPitch];
   __shared__ __attribute__((aligned(16))) __bf16 gxs[TR * kBwdXPitch];
   __shared__ __attribute__((aligned(16))) __bf16 ghi[TR * kBwdGPitch];
   __shared__ __attribute__((aligned(16))) __bf16 glo[TR * kBwdGPitch];
   __shared__ float cf[TR];
-  if (blockIdx.x == 0 && blockIdx.y == 0 && (gbias || galpha)) {
-    __shared__ float lds[4 * 27];
-    float acc[27];
-#pragma unroll
-    for (int i = 0; i < 27; ++i) acc[i] = 0.f;
-    for (int64_t r = threadIdx.x; r < R; r += kThreads) {
-      const float* rb = rowbuf + r * kRow;
-#pragma unroll
-      for (int i = 0; i < 27; ++i) acc[i] += rb[25 + i];
-    }
-    block_sum<27>(acc, lds);
-    if (threadIdx.x == 0) {
-#pragma unroll
-      for (int j = 0; j < kOut; ++j) if (gbias) gbias[j] = acc[j];
-#pragma unroll
-      for (int g = 0; g < 3; ++g) if (galpha) galpha[g] = acc[24 + g];
-    }
-  }
+  const int64_t r_beg = (int64_t)blockIdx.y * RC;
+  const int64_t r_end = r_beg + RC < R ? r_beg + RC : R;
+  // grad_bias and grad_alpha: the rows' records 25..51 summed over the rows.  Column block 0
+  // sums its row chunk after its main loop (below): with one chunk into gbias / galpha, else
+  // into bias_part[chunk] for dynw_gphi_reduce_kernel.  (One workgroup summing all 16384 rows
+  // of R = K = 16384 before its main loop finished ~70 us after the others.)
+  const bool do_bias = blockIdx.x == 0 && (bias_part || gbias || galpha);
   const int wave = threadIdx.x >> 6;
   const int lane = threadIdx.x & 63;
   const int64_t k0 = (int64_t)blockIdx.x * kBwdCols;
-  const int64_t r_beg = (int64_t)blockIdx.y * RC;
-  const int64_t r_end = r_beg + RC < R ? r_beg + RC : R;
   // phi fragments: lane l, element e -> phi[k0 + 32 wave + l % 32][16 js + 8 (l / 32) + e].
   bf16x8 bhi[2], blo[2];
   {
@@ -704,26 +727,27 @@ __global__ __launch_bounds__(kThreads) void dynw_bwd_mfma_kernel(const __bf16* _
       }
     }
   }
-  // Tile loads: x rows t/16 + 16 i (16 bytes at column 8 (t % 16)); record row t/8, floats 4 (t % 8)..+3.
-  const int xr = threadIdx.x >> 4;
-  const int xc = (threadIdx.x & 15) * 8;
+  // Tile loads: x rows t / XLPR + XRPP i (16 bytes at column 8 (t % XLPR)); G record row
+  // t / 8 + GRPP j, floats 4 (t % 8)..+3.
+  const int xr = threadIdx.x / XLPR;
+  const int xc = (threadIdx.x % XLPR) * 8;
   const bool xcol_ok = k0 + xc < K;
   const int grow = threadIdx.x >> 3;
   const int gcol = (threadIdx.x & 7) * 4;
-  u32x4 xv[NX];
-  f32x4 gv[NG];
-  auto load_block = [&](int64_t r0) {
+  const bool g_ok = grow < TR;
+  auto load_block = [&](int64_t r0, u32x4 (&xv)[NX], f32x4 (&gv)[NG]) {
 #pragma unroll
     for (int i = 0; i < NX; ++i) {
-      const int64_t r = r0 + xr + 16 * i;
-      xv[i] = (r < r_end && xcol_ok) ? *reinterpret_cast<const u32x4*>(x + r * K + k0 + xc)
-                                     : u32x4{0u, 0u, 0u, 0u};
+      const int64_t r = r0 + xr + XRPP * i;
+      xv[i] = (r < r_end && xcol_ok)
+                  ? __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(x + r * K + k0 + xc))
+                  : u32x4{0u, 0u, 0u, 0u};
     }
 #pragma unroll
     for (int j = 0; j < NG; ++j) {
-      const int64_t r = r0 + grow + 32 * j;
-      gv[j] = (r < r_end && gcol < 28) ? *reinterpret_cast<const f32x4*>(rowbuf + r * kRow + gcol)
-                                       : f32x4{0.f, 0.f, 0.f, 0.f};
+      const int64_t r = r0 + grow + GRPP * j;
+      gv[j] = (g_ok && r < r_end && gcol < 28) ? *reinterpret_cast<const f32x4*>(rowbuf + r * kRow + gcol)
+                                               : f32x4{0.f, 0.f, 0.f, 0.f};
     }
   };
   // Transpose-read addresses: 16-lane group gi = lane / 16 covers columns 16 (gi & 1) .. +15 of
@@ -735,43 +759,45 @@ __global__ __launch_bounds__(kThreads) void dynw_bwd_mfma_kernel(const __bf16* _
 #pragma unroll
   for (int i = 0; i < 16; ++i) zero[i] = 0.f;
   dphi = zero;
-  if (r_beg < r_end) load_block(r_beg);
-  for (int64_t r0 = r_beg; r0 < r_end; r0 += TR) {
+  // One 64-row block: stage the registers loaded for it, refill them with the block two ahead,
+  // compute, write its grad_x tile.
+  auto block = [&](int64_t r0, u32x4 (&xv)[NX], f32x4 (&gv)[NG]) {
     // Stage this block: x as loaded, G split into hi + lo planes, coef apart.
 #pragma unroll
-    for (int i = 0; i < NX; ++i) *reinterpret_cast<u32x4*>(&xs[(xr + 16 * i) * kBwdXPitch + xc]) = xv[i];
+    for (int i = 0; i < NX; ++i) *reinterpret_cast<u32x4*>(&xs[(xr + XRPP * i) * kBwdXPitch + xc]) = xv[i];
+    if (g_ok) {
 #pragma unroll
-    for (int jj = 0; jj < NG; ++jj) {
-      const int gr = grow + 32 * jj;
-      bf16x4 h4, l4;
+      for (int jj = 0; jj < NG; ++jj) {
+        const int gr = grow + GRPP * jj;
+        bf16x4 h4, l4;
 #pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const float v = gcol < kOut ? gv[jj][e] : 0.f;
-        const __bf16 h = (__bf16)v;
-        h4[e] = h;
-        l4[e] = (__bf16)(v - (float)h);
+        for (int e = 0; e < 4; ++e) {
+          const float v = gcol < kOut ? gv[jj][e] : 0.f;
+          const __bf16 h = (__bf16)v;
+          h4[e] = h;
+          l4[e] = (__bf16)(v - (float)h);
+        }
+        *reinterpret_cast<bf16x4*>(&ghi[gr * kBwdGPitch + gcol]) = h4;
+        *reinterpret_cast<bf16x4*>(&glo[gr * kBwdGPitch + gcol]) = l4;
+        if (gcol == kOut) cf[gr] = gv[jj][0];
       }
-      *reinterpret_cast<bf16x4*>(&ghi[gr * kBwdGPitch + gcol]) = h4;
-      *reinterpret_cast<bf16x4*>(&glo[gr * kBwdGPitch + gcol]) = l4;
-      if (gcol == kOut) cf[gr] = gv[jj][0];
     }
     __syncthreads();
-    if (r0 + TR < r_end) load_block(r0 + TR);  // in flight during the compute below
+    if (r0 + 2 * TR < r_end) load_block(r0 + 2 * TR, xv, gv);  // in flight during the compute below
 #pragma unroll
-    for (int hh = 0; hh < NG; ++hh) {
-    // grad_x^T = phi G^T (see above) for each 32-row half; smallest products first, hi x hi last.
-    f32x16 d = zero;
+    for (int hh = 0; hh < TR / 32; ++hh) {
+      // grad_x^T = phi G^T (see above) for each 32-row half; smallest products first, hi x hi last.
+      f32x16 d = zero;
 #pragma unroll
-    for (int js = 0; js < 2; ++js) {
-      const int j0 = 16 * js + 8 * (lane >> 5);
-      const bf16x8 ghv = *reinterpret_cast<const bf16x8*>(&ghi[(32 * hh + (lane & 31)) * kBwdGPitch + j0]);
-      const bf16x8 glv = *reinterpret_cast<const bf16x8*>(&glo[(32 * hh + (lane & 31)) * kBwdGPitch + j0]);
-      d = __builtin_amdgcn_mfma_f32_32x32x16_bf16(bhi[js], glv, d, 0, 0, 0);
-      d = __builtin_amdgcn_mfma_f32_32x32x16_bf16(blo[js], ghv, d, 0, 0, 0);
-      d = __builtin_amdgcn_mfma_f32_32x32x16_bf16(bhi[js], ghv, d, 0, 0, 0);
-    }
-    // Epilogue: lane l holds row l % 32, columns 32 wave + 8 q + 4 (l / 32) + 0..3 in d[4 q ..].
-    {
+      for (int js = 0; js < 2; ++js) {
+        const int j0 = 16 * js + 8 * (lane >> 5);
+        const bf16x8 ghv = *reinterpret_cast<const bf16x8*>(&ghi[(32 * hh + (lane & 31)) * kBwdGPitch + j0]);
+        const bf16x8 glv = *reinterpret_cast<const bf16x8*>(&glo[(32 * hh + (lane & 31)) * kBwdGPitch + j0]);
+        d = __builtin_amdgcn_mfma_f32_32x32x16_bf16(bhi[js], glv, d, 0, 0, 0);
+        d = __builtin_amdgcn_mfma_f32_32x32x16_bf16(blo[js], ghv, d, 0, 0, 0);
+        d = __builtin_amdgcn_mfma_f32_32x32x16_bf16(bhi[js], ghv, d, 0, 0, 0);
+      }
+      // Epilogue: lane l holds row l % 32, columns 32 wave + 8 q + 4 (l / 32) + 0..3 in d[4 q ..].
       const int row = 32 * hh + (lane & 31);
       const float c = cf[row];
 #pragma unroll
@@ -783,7 +809,6 @@ __global__ __launch_bounds__(kThreads) void dynw_bwd_mfma_kernel(const __bf16* _
         for (int r = 0; r < 4; ++r) o4[r] = (__bf16)(d[4 * q + r] + c * (float)x4[r]);
         *reinterpret_cast<bf16x4*>(&gxs[row * kBwdXPitch + cc]) = o4;
       }
-    }
     }
     // grad_phi += x^T G over the block's 16-row steps.  A = x^T (lane l: column
     // 32 wave + l % 32, rows 16 st + 8 (l / 32) + e), B = G (same rows, j = l % 32).
@@ -803,19 +828,55 @@ __global__ __launch_bounds__(kThreads) void dynw_bwd_mfma_kernel(const __bf16* _
       dphi = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a2, b2hi, dphi, 0, 0, 0);
     }
     __syncthreads();
-    // grad_x tile out: rows xr + 16 i, 16 bytes at column xc.
+    // grad_x tile out: rows xr + XRPP i, 16 bytes at column xc.
     if (gx && xcol_ok) {
 #pragma unroll
       for (int i = 0; i < NX; ++i) {
-        const int64_t r = r0 + xr + 16 * i;
+        const int64_t r = r0 + xr + XRPP * i;
         if (r < r_end)
-          *reinterpret_cast<u32x4*>(gx + r * K + k0 + xc) =
-              *reinterpret_cast<const u32x4*>(&gxs[(xr + 16 * i) * kBwdXPitch + xc]);
+          __builtin_nontemporal_store(*reinterpret_cast<const u32x4*>(&gxs[(xr + XRPP * i) * kBwdXPitch + xc]),
+                                      reinterpret_cast<u32x4*>(gx + r * K + k0 + xc));
       }
     }
     // No barrier here: every read of xs / ghi / glo / cf in this block came
     // before the barrier above, and gxs is next written after the next
     // block's first barrier, which waits for these reads.
+  };
+  // Blocks alternate between two register sets, each refilled with the block two ahead.
+  u32x4 xva[NX], xvb[NX];
+  f32x4 gva[NG], gvb[NG];
+  if (r_beg < r_end) load_block(r_beg, xva, gva);
+  if (r_beg + TR < r_end) load_block(r_beg + TR, xvb, gvb);
+  for (int64_t r0 = r_beg; r0 < r_end; r0 += 2 * TR) {
+    block(r0, xva, gva);
+    if (r0 + TR < r_end) block(r0 + TR, xvb, gvb);
+  }
+  if (do_bias) {
+    // this chunk's rows strided over the workgroup's threads, then the wave sums in wave order
+    __shared__ float lds[NW * 27];
+    float acc[27];
+#pragma unroll
+    for (int i = 0; i < 27; ++i) acc[i] = 0.f;
+    for (int64_t r = r_beg + threadIdx.x; r < r_end; r += kBwdThreads) {
+      const float* rb = rowbuf + r * kRow;
+#pragma unroll
+      for (int i = 0; i < 27; ++i) acc[i] += rb[25 + i];
+    }
+#pragma unroll
+    for (int i = 0; i < 27; ++i) acc[i] = wave_sum(acc[i]);
+    if (lane == 0) {
+#pragma unroll
+      for (int i = 0; i < 27; ++i) lds[wave * 27 + i] = acc[i];
+    }
+    __syncthreads();
+    if (threadIdx.x < 27) {
+      float t = 0.f;
+#pragma unroll
+      for (int w = 0; w < NW; ++w) t += lds[w * 27 + threadIdx.x];
+      if (bias_part) bias_part[(int64_t)blockIdx.y * 27 + threadIdx.x] = t;
+      else if (threadIdx.x < kOut) { if (gbias) gbias[threadIdx.x] = t; }
+      else if (galpha) galpha[threadIdx.x - kOut] = t;
+    }
   }
   // grad_phi: lane l, element i -> k = k0 + 32 wave + 8 (i / 4) + 4 (l / 32) + i % 4, j = l % 32.
   const int j = lane & 31;
@@ -828,16 +889,28 @@ __global__ __launch_bounds__(kThreads) void dynw_bwd_mfma_kernel(const __bf16* _
   }
 }
 
-// grad_phi[i] = sum over row chunks c (in order) of gphi_part[c][i], i < K * 24.
+// grad_phi[i] = sum over row chunks c (in order) of gphi_part[c][i], i < n = K * 24
+// (n = 0: no grad_phi), and, with bias_part given, grad_bias / grad_alpha from
+// the chunks' 27-float records, in threads n .. n + 26.
 template <int = 0>
 __global__ __launch_bounds__(kThreads) void dynw_gphi_reduce_kernel(const float* __restrict__ part,
-                                                                    float* __restrict__ gphi, int64_t n, int nc) {
+                                                                    float* __restrict__ gphi, int64_t n, int nc,
+                                                                    const float* __restrict__ bias_part,
+                                                                    float* __restrict__ gbias,
+                                                                    float* __restrict__ galpha) {
   const int64_t i = (int64_t)blockIdx.x * kThreads + threadIdx.x;
-  if (i >= n) return;
-  float v = 0.f;
+  if (i < n) {
+    float v = 0.f;
 #pragma unroll 4
-  for (int c = 0; c < nc; ++c) v += part[(int64_t)c * n + i];
-  gphi[i] = v;
+    for (int c = 0; c < nc; ++c) v += part[(int64_t)c * n + i];
+    gphi[i] = v;
+  } else if (bias_part && i < n + 27) {
+    const int j = (int)(i - n);
+    float v = 0.f;
+    for (int c = 0; c < nc; ++c) v += bias_part[c * 27 + j];
+    if (j < kOut) { if (gbias) gbias[j] = v; }
+    else if (galpha) galpha[j - kOut] = v;
+  }
 }
 
 // ---------------------------------------------------------------------------

@@ -1,0 +1,117 @@
+// Streaming-ceiling probe: how fast can a kernel shaped like the layer's
+// streaming kernels move a given mix of reads and writes on this GPU?  Not part
+// of the C ABI of the mHC path (libmhc_hip.so); built into libmhc_probe.so and
+// loaded only by `bench.py --stream-ceiling`.
+//
+// The tensors are laid out like the layer's: per token, an input array holds
+// NA (resp. NB, NC) rows of `row_bytes` and the output array NW rows, token
+// after token ([T, rows, D] row-major).  One workgroup of 256 lanes owns one
+// tile = (token, 4 KiB column block); each lane moves one 16-byte vector per
+// row through a buffer resource, as the layer kernels do, with every load of
+// the tile issued before the first use.  Output row w is the 32-bit sum of
+// all input rows plus one of them; with no output the sum is kept live by a
+// store that never fires.
+// The occupancy cap (workgroups per CU) is set with a dynamic-LDS reservation,
+// as in the layer kernels.
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "../stream_kernels.hpp"
+
+namespace {
+
+using mhc::Span;
+using mhc::u32x4;
+
+constexpr int kLanes = 256;
+constexpr int kTileBytes = kLanes * 16;
+
+template <int NA, int NB, int NC, int NW, bool NT>
+__global__ __launch_bounds__(kLanes) void stream_probe_kernel(const char* __restrict__ a, const char* __restrict__ b,
+                                                              const char* __restrict__ c, char* __restrict__ w,
+                                                              int64_t row_bytes, uint32_t tiles_per_token,
+                                                              unsigned* __restrict__ sink) {
+  constexpr int NR = NA + NB + NC;
+  extern __shared__ char occupancy_reserve[];
+  (void)occupancy_reserve;
+  const int64_t tok = blockIdx.x / tiles_per_token;
+  const uint32_t col = (blockIdx.x % tiles_per_token) * kTileBytes + threadIdx.x * 16;
+  // one span per array covering this token's rows
+  const Span<char, true> sa(a + tok * NA * row_bytes, NA * row_bytes);
+  const Span<char, true> sb(b + tok * NB * row_bytes, NB * row_bytes);
+  const Span<char, true> sc(c + tok * NC * row_bytes, NC * row_bytes);
+  const Span<char, true> sw(w + tok * NW * row_bytes, NW * row_bytes);
+  u32x4 v[NR > 0 ? NR : 1];
+#pragma unroll
+  for (int i = 0; i < NA; ++i) v[i] = sa.load16<NT>((uint32_t)(i * row_bytes) + col);
+#pragma unroll
+  for (int i = 0; i < NB; ++i) v[NA + i] = sb.load16<NT>((uint32_t)(i * row_bytes) + col);
+#pragma unroll
+  for (int i = 0; i < NC; ++i) v[NA + NB + i] = sc.load16<NT>((uint32_t)(i * row_bytes) + col);
+  __builtin_amdgcn_sched_barrier(0);
+  // every input row feeds every output row, so no load can be dropped
+  u32x4 tot = u32x4{0u, 0u, 0u, 0u};
+#pragma unroll
+  for (int i = 0; i < NR; ++i) tot += v[i];
+  if constexpr (NW > 0) {
+#pragma unroll
+    for (int o = 0; o < NW; ++o) {
+      u32x4 s = tot + u32x4{(uint32_t)o, 0u, 0u, 0u};
+      if constexpr (NR > 0) s += v[o % NR];
+      sw.store16<NT>((uint32_t)(o * row_bytes) + col, s);
+    }
+  } else {
+    if (tot.x == 0x9e3779b9u && tot.y == 0x7f4a7c15u && tot.z == tot.w) sink[threadIdx.x] = tot.x;
+  }
+}
+
+template <int NA, int NB, int NC, int NW>
+hipError_t launch(const void* a, const void* b, const void* c, void* w, int64_t tokens, int64_t row_bytes,
+                  size_t lds, bool nt, unsigned* sink, hipStream_t st) {
+  const uint32_t tpt = (uint32_t)(row_bytes / kTileBytes);
+  const dim3 grid((unsigned)(tokens * tpt));
+  if (nt)
+    stream_probe_kernel<NA, NB, NC, NW, true><<<grid, kLanes, lds, st>>>(
+        (const char*)a, (const char*)b, (const char*)c, (char*)w, row_bytes, tpt, sink);
+  else
+    stream_probe_kernel<NA, NB, NC, NW, false><<<grid, kLanes, lds, st>>>(
+        (const char*)a, (const char*)b, (const char*)c, (char*)w, row_bytes, tpt, sink);
+  return hipGetLastError();
+}
+
+}  // namespace
+
+// Moves tokens x (na + nb + nc) input rows and tokens x nw output rows of
+// row_bytes each (a multiple of 4096).  Supported (na, nb, nc, nw): the read /
+// write mixes of the layer's streaming kernels and the plain references
+// (4,0,0,0) (4,0,0,1) (4,1,0,4) (4,1,0,1) (4,4,1,0) (1,0,0,1) (1,0,0,0)
+// (0,0,0,1).  wg_per_cu > 0 caps resident workgroups per CU (0: no cap).
+// `sink` is 1 KiB of device memory that a read-only mix keeps live.  Returns
+// 0, 1 for an unsupported mix or shape, 2 for a launch error.
+extern "C" int mhc_probe_stream(int na, int nb, int nc, int nw, const void* a, const void* b, const void* c, void* w,
+                                int64_t tokens, int64_t row_bytes, int wg_per_cu, int nt, void* sink,
+                                void* stream) {
+  if (tokens <= 0 || row_bytes <= 0 || row_bytes % kTileBytes != 0) return 1;
+  int rows = na > nb ? na : nb;
+  rows = rows > nc ? rows : nc;
+  rows = rows > nw ? rows : nw;
+  if ((int64_t)rows * row_bytes >= ((int64_t)1 << 31)) return 1;  // one token's span of an array
+  if (tokens * (row_bytes / kTileBytes) >= ((int64_t)1 << 31)) return 1;
+  const size_t lds = mhc::occupancy_lds(wg_per_cu);
+  hipStream_t st = (hipStream_t)stream;
+  unsigned* s = (unsigned*)sink;
+  const int key = na * 1000 + nb * 100 + nc * 10 + nw;
+  hipError_t e;
+  switch (key) {
+    case 4000: e = launch<4, 0, 0, 0>(a, b, c, w, tokens, row_bytes, lds, nt, s, st); break;
+    case 4001: e = launch<4, 0, 0, 1>(a, b, c, w, tokens, row_bytes, lds, nt, s, st); break;
+    case 4104: e = launch<4, 1, 0, 4>(a, b, c, w, tokens, row_bytes, lds, nt, s, st); break;
+    case 4101: e = launch<4, 1, 0, 1>(a, b, c, w, tokens, row_bytes, lds, nt, s, st); break;
+    case 4410: e = launch<4, 4, 1, 0>(a, b, c, w, tokens, row_bytes, lds, nt, s, st); break;
+    case 1001: e = launch<1, 0, 0, 1>(a, b, c, w, tokens, row_bytes, lds, nt, s, st); break;
+    case 1000: e = launch<1, 0, 0, 0>(a, b, c, w, tokens, row_bytes, lds, nt, s, st); break;
+    case 1: e = launch<0, 0, 0, 1>(a, b, c, w, tokens, row_bytes, lds, nt, s, st); break;
+    default: return 1;
+  }
+  return e == hipSuccess ? 0 : 2;
+}

@@ -127,3 +127,26 @@ def test_shape_errors_are_assertion_compatible():
         mhc.HyperConnection(8, num_streams=3)
     with pytest.raises(ValueError):
         mhc.HyperConnection(8)(torch.zeros(1, 2, 4, 9))
+
+
+def test_stream_ceiling_probe_rejects_bad_shapes_without_gpu(lib):
+    """libmhc_probe.so (bench.py --stream-ceiling) is separate from the mHC C ABI: it exports only
+    its probe, and refuses unsupported mixes and shapes before any device work."""
+    import ctypes
+
+    path = os.path.join(ROOT, "mhc-triton_amd", "mhc", "libmhc_probe.so")
+    if not os.path.exists(path):
+        import __graft_entry__
+
+        __graft_entry__.build()
+    probe = ctypes.CDLL(path)
+    fn = probe.mhc_probe_stream
+    fn.restype = ctypes.c_int
+    fn.argtypes = [ctypes.c_int] * 4 + [ctypes.c_void_p] * 4 + [ctypes.c_int64] * 2 + [ctypes.c_int] * 2 + \
+        [ctypes.c_void_p] * 2
+    null = None
+    assert fn(1, 0, 0, 1, null, null, null, null, 0, 8192, 0, 1, null, null) == 1  # no tokens
+    assert fn(1, 0, 0, 1, null, null, null, null, 16, 1000, 0, 1, null, null) == 1  # row not 4 KiB tiles
+    assert fn(2, 0, 0, 0, null, null, null, null, 16, 8192, 0, 1, null, null) == 1  # unsupported mix
+    assert fn(4, 0, 0, 0, null, null, null, null, 16, 1 << 30, 0, 1, null, null) == 1  # span >= 2^31
+    assert not hasattr(lib, "mhc_probe_stream")
