@@ -112,6 +112,9 @@ PROBE_MIXES = [
     ("5:4", (4, 1, 0), 4, "mix_fwd_kernel<RES,ADD_BO> (closure forward); dh_kernel (pass C)"),
     ("5:1", (4, 1, 0), 1, "add_residual_bwd_kernel (closure backward)"),
     ("9:0", (4, 4, 1), 0, "mix_bwd_kernel<REDUCE> (pass B)"),
+    ("4:5", (4, 0, 0), 5, "fused_stream_mix forward (H_residual and branch_input)"),
+    ("1:4", (1, 0, 0), 4, "expand_streams"),
+    ("9:4", (4, 4, 1), 4, "fused_stream_mix backward (dH with the dH_pre / dH_res partials)"),
 ]
 
 

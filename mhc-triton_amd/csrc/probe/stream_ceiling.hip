@@ -85,7 +85,7 @@ hipError_t launch(const void* a, const void* b, const void* c, void* w, int64_t 
 // row_bytes each (a multiple of 4096).  Supported (na, nb, nc, nw): the read /
 // write mixes of the layer's streaming kernels and the plain references
 // (4,0,0,0) (4,0,0,1) (4,1,0,4) (4,1,0,1) (4,4,1,0) (1,0,0,1) (1,0,0,0)
-// (0,0,0,1).  wg_per_cu > 0 caps resident workgroups per CU (0: no cap).
+// (0,0,0,1), and those of the standalone ops (4,0,0,5) (1,0,0,4) (4,4,1,4).  wg_per_cu > 0 caps resident workgroups per CU (0: no cap).
 // `sink` is 1 KiB of device memory that a read-only mix keeps live.  Returns
 // 0, 1 for an unsupported mix or shape, 2 for a launch error.
 extern "C" int mhc_probe_stream(int na, int nb, int nc, int nw, const void* a, const void* b, const void* c, void* w,
@@ -111,6 +111,9 @@ extern "C" int mhc_probe_stream(int na, int nb, int nc, int nw, const void* a, c
     case 1001: e = launch<1, 0, 0, 1>(a, b, c, w, tokens, row_bytes, lds, nt, s, st); break;
     case 1000: e = launch<1, 0, 0, 0>(a, b, c, w, tokens, row_bytes, lds, nt, s, st); break;
     case 1: e = launch<0, 0, 0, 1>(a, b, c, w, tokens, row_bytes, lds, nt, s, st); break;
+    case 4005: e = launch<4, 0, 0, 5>(a, b, c, w, tokens, row_bytes, lds, nt, s, st); break;
+    case 1004: e = launch<1, 0, 0, 4>(a, b, c, w, tokens, row_bytes, lds, nt, s, st); break;
+    case 4414: e = launch<4, 4, 1, 4>(a, b, c, w, tokens, row_bytes, lds, nt, s, st); break;
     default: return 1;
   }
   return e == hipSuccess ? 0 : 2;
