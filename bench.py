@@ -69,6 +69,13 @@ ALGO_UNITS = {True: (18, 24), False: (14, 19)}
 MEASURED_TRAFFIC = {"config3": 1208171969, "config4": 1057150466, "config5": 1208101031}
 TRAFFIC_COMMIT = "de1782b"
 
+# Best fraction of 8 TB/s that a kernel of the closure forward's launch shape
+# reaches when it only moves the same 5:4 read / write mix (4 H rows + bo read,
+# 4 H_new rows written per token) at the config-3 layout: `bench.py
+# --stream-ceiling` (profiles/stream_ceiling.md).  Row layouts that are not a
+# whole number of 4 KiB tiles (config 4) are not measured.
+STREAM_CEILING_5_4 = {"config3": 0.814, "config5": None, "config4": None}
+
 
 def _log(msg: str) -> None:
     print(msg, file=sys.stderr, flush=True)
@@ -657,6 +664,9 @@ def main() -> int:
             "frac": round(add_gbs / HBM_PEAK_GBS, 4),
             "traffic": MEASURED_TRAFFIC.get(args.workload),
             "traffic_measured_at": TRAFFIC_COMMIT,
+            "mix_ceiling_frac": STREAM_CEILING_5_4.get(args.workload),
+            "frac_of_mix_ceiling": (round(add_gbs / HBM_PEAK_GBS / STREAM_CEILING_5_4[args.workload], 4)
+                                    if STREAM_CEILING_5_4.get(args.workload) else None),
         },
         "layer_roofline": {
             "algorithmic_bytes_per_step": step_bytes,
