@@ -637,7 +637,7 @@ inline hipError_t launch_dynw_bwd_wide(const TX* x, const float* phi, const floa
 // of each row: as a plain copy, 256-byte strips (128 columns, four waves)
 // peak at 67% of 8 TB/s and 512-byte strips at 79%, at the same grid size.
 // Per block the x tile (bf16) and the G rows are staged in LDS, with the next
-// two blocks' loads in flight (streaming loads and stores: x is read and
+// kBwdAhead = 3 blocks' loads in flight (streaming loads and stores: x is read and
 // grad_x written once).  G is split into bf16 hi + lo planes once, as it is
 // staged (fp32 products then take hi*hi + hi*lo + lo*hi, relative error ~2^-16):
 //   grad_x: computed transposed, grad_x^T = phi G^T, so that the A operand is
@@ -664,6 +664,7 @@ inline hipError_t launch_dynw_bwd_wide(const TX* x, const float* phi, const floa
 constexpr int kBwdWaves = 8;              // waves per workgroup (32 columns each)
 constexpr int kBwdMinWaves = 2;           // waves per SIMD the register allocation must allow
 constexpr int kBwdRows = 64;              // rows per staged block (two 32-row MFMA halves)
+constexpr int kBwdAhead = 3;              // blocks of loads in flight: register sets (2 or 3)
 constexpr int kBwdGPitch = 40;            // bf16 per LDS row of the split G planes (columns 24..31 zero)
 
 typedef short s16x4 __attribute__((ext_vector_type(4)));
@@ -783,7 +784,7 @@ __global__ __launch_bounds__(64 * NW, MINW) void dynw_bwd_mfma_kernel(const __bf
       }
     }
     __syncthreads();
-    if (r0 + 2 * TR < r_end) load_block(r0 + 2 * TR, xv, gv);  // in flight during the compute below
+    if (r0 + kBwdAhead * TR < r_end) load_block(r0 + kBwdAhead * TR, xv, gv);  // in flight during the compute below
 #pragma unroll
     for (int hh = 0; hh < TR / 32; ++hh) {
       // grad_x^T = phi G^T (see above) for each 32-row half; smallest products first, hi x hi last.
@@ -842,14 +843,17 @@ __global__ __launch_bounds__(64 * NW, MINW) void dynw_bwd_mfma_kernel(const __bf
     // before the barrier above, and gxs is next written after the next
     // block's first barrier, which waits for these reads.
   };
-  // Blocks alternate between two register sets, each refilled with the block two ahead.
-  u32x4 xva[NX], xvb[NX];
-  f32x4 gva[NG], gvb[NG];
+  // Blocks rotate through kBwdAhead register sets, each refilled with the block kBwdAhead ahead.
+  static_assert(kBwdAhead == 2 || kBwdAhead == 3, "register sets");
+  u32x4 xva[NX], xvb[NX], xvc[NX];
+  f32x4 gva[NG], gvb[NG], gvc[NG];
   if (r_beg < r_end) load_block(r_beg, xva, gva);
   if (r_beg + TR < r_end) load_block(r_beg + TR, xvb, gvb);
-  for (int64_t r0 = r_beg; r0 < r_end; r0 += 2 * TR) {
+  if (kBwdAhead == 3 && r_beg + 2 * TR < r_end) load_block(r_beg + 2 * TR, xvc, gvc);
+  for (int64_t r0 = r_beg; r0 < r_end; r0 += kBwdAhead * TR) {
     block(r0, xva, gva);
     if (r0 + TR < r_end) block(r0 + TR, xvb, gvb);
+    if (kBwdAhead == 3 && r0 + 2 * TR < r_end) block(r0 + 2 * TR, xvc, gvc);
   }
   if (do_bias) {
     // this chunk's rows strided over the workgroup's threads, then the wave sums in wave order
