@@ -102,8 +102,8 @@ def _parse():
                          "rocprofv3 FETCH_SIZE / WRITE_SIZE readings into bytes) and exit")
     ap.add_argument("--stream-ceiling", action="store_true",
                     help="only time the streaming-ceiling probe (libmhc_probe.so): kernels shaped like the "
-                         "layer's streaming kernels that move the same read / write mixes at config-3 "
-                         "size and do nothing else, over occupancy caps and cache policies, and exit")
+                         "layer's streaming kernels that move the same read / write mixes at the workload's "
+                         "layout and do nothing else, over occupancy caps and cache policies, and exit")
     return ap.parse_args()
 
 
@@ -127,12 +127,12 @@ PROBE_MIXES = [
 ]
 
 
-def _stream_ceiling(tokens: int = 16384, row_bytes: int = 8192, caps=(0, 2, 3, 4, 6, 8), reps: int = 20,
+def _stream_ceiling(tokens: int, row_bytes: int, caps=(0, 2, 3, 4, 6, 8), reps: int = 20,
                     warm: int = 3) -> dict:
     """Best HBM rate of each read / write mix of the layer's streaming kernels, as moved by a kernel of the
-    same launch shape (one 16-byte vector per lane and row, buffer resources, one tile per workgroup) that
-    computes nothing: the ceiling those kernels are measured against.  Config-3 layout (T = 16384 tokens,
-    8 KiB rows); the one-row mixes run over 4 T tokens, so every array is 512 MiB."""
+    same launch shape (one 16-byte vector per lane and row, buffer resources, one tile or 256 flattened
+    items per workgroup) that computes nothing: the ceiling those kernels are measured against.  The
+    workload's layout: T tokens of D * e byte rows; the one-row mixes run over 4 T tokens."""
     import ctypes
 
     import torch
@@ -602,8 +602,11 @@ def main() -> int:
     if args.calibrate_copy:
         return _calibrate_copy()
     if args.stream_ceiling:
-        print(json.dumps({"stream_ceiling": _stream_ceiling(), "unit": "us per launch", "peak_GBps": HBM_PEAK_GBS,
-                          "layout": "config 3: 16384 tokens x 8 KiB rows per array row",
+        cfg = WORKLOADS[args.workload]
+        tokens, row_bytes = cfg["B"] * cfg["S"], cfg["D"] * (2 if cfg["dtype"] in ("bf16", "fp16") else 4)
+        print(json.dumps({"stream_ceiling": _stream_ceiling(tokens, row_bytes), "unit": "us per launch",
+                          "peak_GBps": HBM_PEAK_GBS, "workload": args.workload,
+                          "layout": f"{tokens} tokens x {row_bytes}-byte rows per array row",
                           "caps": "cap0 = no occupancy cap, capN = at most N workgroups per CU",
                           "device": torch.cuda.get_device_name(0)}), flush=True)
         return 0

@@ -146,7 +146,7 @@ def test_stream_ceiling_probe_rejects_bad_shapes_without_gpu(lib):
         [ctypes.c_void_p] * 2
     null = None
     assert fn(1, 0, 0, 1, null, null, null, null, 0, 8192, 0, 1, null, null) == 1  # no tokens
-    assert fn(1, 0, 0, 1, null, null, null, null, 16, 1000, 0, 1, null, null) == 1  # row not 4 KiB tiles
+    assert fn(1, 0, 0, 1, null, null, null, null, 16, 1000, 0, 1, null, null) == 1  # row not a multiple of 16 bytes
     assert fn(2, 0, 0, 0, null, null, null, null, 16, 8192, 0, 1, null, null) == 1  # unsupported mix
     assert fn(4, 0, 0, 0, null, null, null, null, 16, 1 << 30, 0, 1, null, null) == 1  # span >= 2^31
     assert not hasattr(lib, "mhc_probe_stream")

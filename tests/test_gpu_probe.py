@@ -1,8 +1,9 @@
 """The streaming-ceiling probe (libmhc_probe.so, `bench.py --stream-ceiling`) moves the bytes
 it is credited with: every input row of a mix is read and every output row written, with the
 values its kernel defines (output row o = the 32-bit sum of all input rows, plus o in the first
-word, plus input row o mod n).  A probe that dropped a load would report a ceiling for a
-lighter mix than the layer kernel it is compared with.
+word, plus input row o mod n), on whole 4 KiB tiles and on flattened items.  A probe that
+dropped a load would report a ceiling for a lighter mix than the layer kernel it is compared
+with.
 """
 
 import ctypes
@@ -32,10 +33,11 @@ def probe():
 
 
 @pytest.mark.parametrize("mix", MIXES, ids=lambda m: "".join(map(str, m)))
-@pytest.mark.parametrize("nt,cap", [(1, 2), (0, 0)])
-def test_probe_moves_every_row(probe, mix, nt, cap):
+@pytest.mark.parametrize("nt,cap,row_bytes", [(1, 2, 8192), (0, 0, 8192), (1, 3, 14336), (1, 0, 1040)],
+                         ids=["tiles-nt", "tiles-plain", "flat-14336", "flat-1040"])
+def test_probe_moves_every_row(probe, mix, nt, cap, row_bytes):
     na, nb, nc, nw = mix
-    tokens, row_bytes = 37, 8192
+    tokens = 37
     words = row_bytes // 4
     g = torch.Generator(device="cuda")
     g.manual_seed(sum(mix) * 7 + nt)
