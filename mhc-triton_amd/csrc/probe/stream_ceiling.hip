@@ -153,11 +153,12 @@ hipError_t launch(const void* a, const void* b, const void* c, void* w, int64_t 
 // (4,0,0,0) (4,0,0,1) (4,1,0,4) (4,1,0,1) (4,4,1,0) (1,0,0,1) (1,0,0,0)
 // (0,0,0,1), and those of the standalone ops (4,0,0,5) (1,0,0,4) (4,4,1,4).  wg_per_cu > 0 caps resident workgroups per CU (0: no cap).
 // `sink` is 1 KiB of device memory that a read-only mix keeps live.  Returns
-// 0, 1 for an unsupported mix or shape, 2 for a launch error.
+// 0, 1 for an unsupported mix, shape or a missing array, 2 for a launch error.
 extern "C" int mhc_probe_stream(int na, int nb, int nc, int nw, const void* a, const void* b, const void* c, void* w,
                                 int64_t tokens, int64_t row_bytes, int wg_per_cu, int nt, void* sink,
                                 void* stream) {
   if (tokens <= 0 || row_bytes <= 0 || row_bytes % 16 != 0) return 1;
+  if ((na > 0 && !a) || (nb > 0 && !b) || (nc > 0 && !c) || (nw > 0 && !w) || (nw == 0 && !sink)) return 1;
   int rows = na > nb ? na : nb;
   rows = rows > nc ? rows : nc;
   rows = rows > nw ? rows : nw;

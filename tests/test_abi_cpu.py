@@ -145,8 +145,11 @@ def test_stream_ceiling_probe_rejects_bad_shapes_without_gpu(lib):
     fn.argtypes = [ctypes.c_int] * 4 + [ctypes.c_void_p] * 4 + [ctypes.c_int64] * 2 + [ctypes.c_int] * 2 + \
         [ctypes.c_void_p] * 2
     null = None
-    assert fn(1, 0, 0, 1, null, null, null, null, 0, 8192, 0, 1, null, null) == 1  # no tokens
-    assert fn(1, 0, 0, 1, null, null, null, null, 16, 1000, 0, 1, null, null) == 1  # row not a multiple of 16 bytes
-    assert fn(2, 0, 0, 0, null, null, null, null, 16, 8192, 0, 1, null, null) == 1  # unsupported mix
-    assert fn(4, 0, 0, 0, null, null, null, null, 16, 1 << 30, 0, 1, null, null) == 1  # span >= 2^31
+    fake = 4096  # never dereferenced: every call below is refused on the host
+    assert fn(1, 0, 0, 1, fake, null, null, fake, 0, 8192, 0, 1, null, null) == 1  # no tokens
+    assert fn(1, 0, 0, 1, fake, null, null, fake, 16, 1000, 0, 1, null, null) == 1  # row not a multiple of 16 bytes
+    assert fn(1, 0, 0, 1, null, null, null, fake, 16, 8192, 0, 1, null, null) == 1  # missing input array
+    assert fn(1, 0, 0, 0, fake, null, null, null, 16, 8192, 0, 1, null, null) == 1  # read-only mix without a sink
+    assert fn(2, 0, 0, 0, fake, null, null, null, 16, 8192, 0, 1, fake, null) == 1  # unsupported mix
+    assert fn(4, 0, 0, 0, fake, null, null, null, 16, 1 << 30, 0, 1, fake, null) == 1  # span >= 2^31
     assert not hasattr(lib, "mhc_probe_stream")
