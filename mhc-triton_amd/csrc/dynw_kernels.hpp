@@ -147,11 +147,13 @@ __global__ __launch_bounds__(kThreads) void dynw_pack_phi_kernel(const float* __
 // stages them once in double-buffered LDS (one barrier per group) instead of
 // every wave loading them from L2 (per-wave phi loads competing with the x
 // stream had cost ~45 us); the more waves share a stage, the less of that
-// L2 -> LDS traffic per x byte.  Each 16-k step's three MFMAs start from zero
-// and the step result is added into `acc` with fp32 VALU adds (a long MFMA
-// accumulation chain drifts by ~1e-5 relative over 1024 steps; the
-// round-to-nearest adds do not; a chain over a 4-step group needs 16 more
-// live VGPRs than 4 waves per SIMD leave).  Writes the same 25-float partial
+// L2 -> LDS traffic per x byte.  A group's 12 MFMAs (4 steps x 3 phi parts)
+// accumulate in one chain that starts from zero, and the group result is added
+// into `acc` with fp32 VALU adds: a single MFMA chain over all 1024 steps of
+// K = 16384 drifts by ~1e-5 relative, the round-to-nearest adds do not.  (At
+// 4 waves per workgroup the group chain did not fit 128 VGPRs and each step
+// was added on its own; with 16 waves the phi stage needs fewer registers per
+// lane.)  Writes the same 25-float partial
 // records as dynw_partial_kernel: part[r][kc][0:24] and the row's sum of
 // squares [24], which the VALU forms from the A fragments alongside the MFMAs
 // (v_dot2_f32_bf16 would take a quarter of the instructions, but its sums are
@@ -233,10 +235,10 @@ __global__ __launch_bounds__(64 * NW, 4) void dynw_mfma_kernel(const __bf16* __r
   for (int i = 0; i < 16; ++i) acc[i] = zero[i] = 0.f;
   float ss = 0.f, ss_hi = 0.f;
   auto compute = [&](int64_t g, const u32x4 (&d)[G], int buf) {
+    f32x16 st = zero;
 #pragma unroll
     for (int j = 0; j < G; ++j) {
       if (s_beg + g * G + j < s_end) {
-        f32x16 st = zero;
         const u32x4 b0 = phs[buf][(j * 3 + 0) * 64 + lane];
         const u32x4 b1 = phs[buf][(j * 3 + 1) * 64 + lane];
         const u32x4 b2 = phs[buf][(j * 3 + 2) * 64 + lane];
@@ -254,9 +256,9 @@ __global__ __launch_bounds__(64 * NW, 4) void dynw_mfma_kernel(const __bf16* __r
           ss = fmaf(lo_, lo_, ss);
           ss_hi = fmaf(hi_, hi_, ss_hi);
         }
-        acc += st;
       }
     }
+    acc += st;
   };
   // Group g's loads sit in a[g % 2] and its phi in phs[g % 2]; the loop is
   // unrolled by two so that neither register set is copied.
