@@ -133,7 +133,14 @@ def require_gpu(*tensors) -> torch.device:
     return dev
 
 
+_raw_stream = getattr(torch._C, "_cuda_getCurrentRawStream", None)
+
+
 def stream(dev: torch.device) -> int:
+    """The handle of torch's current stream on `dev` (the stream every launch goes to).  The raw
+    getter skips building a torch.cuda.Stream object (about 5 us of host time per call)."""
+    if _raw_stream is not None:
+        return _raw_stream(dev.index if dev.index is not None else torch.cuda.current_device())
     return torch.cuda.current_stream(dev).cuda_stream
 
 
