@@ -641,7 +641,7 @@ inline hipError_t launch_dynw_bwd_wide(const TX* x, const float* phi, const floa
 // of each row: as a plain copy, 256-byte strips (128 columns, four waves)
 // peak at 67% of 8 TB/s and 512-byte strips at 79%, at the same grid size.
 // Per block the x tile (bf16) and the G rows are staged in LDS, with the next
-// kBwdAhead = 3 blocks' loads in flight (streaming loads and stores: x is read and
+// kBwdAhead = 2 blocks' loads in flight (streaming loads and stores: x is read and
 // grad_x written once).  G is split into bf16 hi + lo planes once, as it is
 // staged (fp32 products then take hi*hi + hi*lo + lo*hi, relative error ~2^-16):
 //   grad_x: computed transposed, grad_x^T = phi G^T, so that the A operand is
@@ -668,7 +668,7 @@ inline hipError_t launch_dynw_bwd_wide(const TX* x, const float* phi, const floa
 constexpr int kBwdWaves = 8;              // waves per workgroup (32 columns each)
 constexpr int kBwdMinWaves = 2;           // waves per SIMD the register allocation must allow
 constexpr int kBwdRows = 64;              // rows per staged block (two 32-row MFMA halves)
-constexpr int kBwdAhead = 3;              // blocks of loads in flight: register sets (2 or 3)
+constexpr int kBwdAhead = 2;              // blocks of loads in flight: register sets (2 or 3)
 constexpr int kBwdGPitch = 40;            // bf16 per LDS row of the split G planes (columns 24..31 zero)
 
 typedef short s16x4 __attribute__((ext_vector_type(4)));

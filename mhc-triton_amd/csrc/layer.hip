@@ -400,8 +400,8 @@ extern "C" int mhc_layer_add_forward(const void* H, int dtype_h, const void* bra
       return for_batch_chunks(B, [&](int64_t b0, int64_t nb) {
         const Geom g = make_geom<W, kLU>(S, D, b0);
         // 3 workgroups per CU: 188.5 us at config-3 size against 194.9 with 2 and 190.4 with 4
-        // when chosen; with the buffer-span loads and nt policy the three caps now time alike
-        // (192.8-194.5 us event-timed in the bench).
+        // when chosen; with the buffer-span loads and nt policy caps 2 and 3 time alike and 4
+        // is about 1 us slower (192.6-195.4 us event-timed in the bench).
         mix_fwd_kernel<TH, TB, W, kLU, false, true, true, kNt>
             <<<dim3(g.ntiles, nb), kThreads, occupancy_lds(3), st>>>(
             (const TH*)H, (const TB*)branch_output, WRow{nullptr, 0}, WRow{w + 8, kOut}, WRow{w + 4, kOut},
