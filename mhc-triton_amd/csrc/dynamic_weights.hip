@@ -32,38 +32,38 @@ static DynPlan dyn_plan(int64_t R, int64_t K) {
 
 static size_t align256(size_t v) { return (v + 255) & ~(size_t)255; }
 
-// MFMA plan for bf16 x with many rows: workgroups of kMfmaRowsWg rows
-// (kMfmaWaves waves of 32 rows), and the K steps (16 k each) split into nK
-// chunks so that about 8192 waves stream x (two rounds of one 16-wave
-// workgroup per CU); at least 16 steps per chunk.  At R = K = 16384 (nK = 16):
-// 123.7 us with 4-wave workgroups of 128 rows, 119.6 with 8 waves, 116.0 with
-// 16, since every workgroup stages the same phi fragments once for all its
-// waves (phi L2->LDS traffic per x byte: 75% at 4 waves, 19% at 16).
+// MFMA plan for bf16 x with many rows (dynw_mfma_kernel): K chunks of
+// kMfmaChunkSteps steps (1024 k), and row ranges of whole 32-row tiles so that
+// about kMfmaTargetWg workgroups run, one per CU (the kernel's LDS allows one).
+// At R = K = 16384: 16 chunks x 16 ranges of 1024 rows.
 constexpr int64_t kMfmaMinRows = 64;
-constexpr int64_t kMfmaWgRows = kMfmaRowsWg;
+constexpr int64_t kMfmaTargetWg = 256;
 
 struct MfmaPlan {
-  int64_t nsteps;  // K / 16
-  int64_t spc;     // steps per chunk
-  int nK;          // chunks
+  int64_t nsteps;       // K / 16
+  int nK;               // chunks
+  int64_t rows_per_wg;  // multiple of 32
+  int ngr;              // row ranges
   size_t part_bytes, packed_bytes;
 };
 
 static bool mfma_shape_ok(int64_t R, int64_t K) {
-  return R >= kMfmaMinRows && K > 0 && K % 16 == 0 && span_ok(kMfmaWgRows * K, 2);
+  return R >= kMfmaMinRows && K > 0 && K % 16 == 0 && span_ok(32 * K, 2);
 }
 
 static MfmaPlan mfma_plan(int64_t R, int64_t K) {
   MfmaPlan p;
   p.nsteps = K / 16;
-  const int64_t wg_rows = (R + kMfmaWgRows - 1) / kMfmaWgRows;
-  const int64_t target_wg = 2048 * 4 / kMfmaWaves;  // 8192 waves
-  int64_t nk = (target_wg + wg_rows - 1) / wg_rows;
-  const int64_t max_nk = p.nsteps / 16 > 0 ? p.nsteps / 16 : 1;
-  if (nk > max_nk) nk = max_nk;
-  if (nk < 1) nk = 1;
-  p.spc = (p.nsteps + nk - 1) / nk;
-  p.nK = (int)((p.nsteps + p.spc - 1) / p.spc);
+  p.nK = (int)((p.nsteps + kMfmaChunkSteps - 1) / kMfmaChunkSteps);
+  if (p.nK < 1) p.nK = 1;
+  const int64_t tiles = (R + 31) / 32;
+  int64_t ngr = (kMfmaTargetWg + p.nK - 1) / p.nK;
+  if (ngr > tiles) ngr = tiles;
+  if (ngr < 1) ngr = 1;
+  int64_t tpw = (tiles + ngr - 1) / ngr;
+  while (tpw > 1 && !span_ok(32 * tpw * K, 2)) tpw = (tpw + 1) / 2;
+  p.rows_per_wg = 32 * tpw;
+  p.ngr = (int)((R + p.rows_per_wg - 1) / p.rows_per_wg);
   p.part_bytes = align256((size_t)R * p.nK * kPart * sizeof(float));
   p.packed_bytes = (size_t)p.nsteps * 3 * 64 * 16;
   return p;
@@ -113,8 +113,8 @@ extern "C" int mhc_dynamic_weights_forward(const void* x, int dtype_x, const flo
     dynw_pack_phi_kernel<><<<dim3((unsigned)((m.nsteps * 64 + kThreads - 1) / kThreads)), kThreads, 0, st>>>(
         phi, packed, m.nsteps);
     if (int rc = hip_status(hipGetLastError(), "dynamic_weights_forward pack launch")) return rc;
-    dynw_mfma_kernel<><<<dim3((unsigned)((R + kMfmaWgRows - 1) / kMfmaWgRows), (unsigned)m.nK), 64 * kMfmaWaves, 0, st>>>(
-        (const __bf16*)x, packed, part, R, K, m.nK, m.spc);
+    dynw_mfma_kernel<><<<dim3((unsigned)m.ngr, (unsigned)m.nK), 64 * kMfmaWaves, 0, st>>>(
+        (const __bf16*)x, packed, part, R, K, m.nK, m.rows_per_wg);
     if (int rc = hip_status(hipGetLastError(), "dynamic_weights_forward mfma launch")) return rc;
     nK = m.nK;
   } else {
@@ -214,7 +214,9 @@ extern "C" int mhc_dynamic_weights_backward(const void* x, int dtype_x, const fl
   float* gphi_part = (w.nR > 1 && grad_phi) ? (float*)split_ws : nullptr;
   float* bias_part = nullptr;  // MFMA path, split rows: per-chunk grad_bias / grad_alpha records
   int rc;
-  if (dtype_x == MHC_DTYPE_BF16 && R >= kMfmaMinRows && K % 8 == 0 && aligned16(x) && (!grad_x || aligned16(grad_x))) {
+  // (the kernel's buffer spans reach up to four blocks past a chunk's rows)
+  if (dtype_x == MHC_DTYPE_BF16 && R >= kMfmaMinRows && K % 8 == 0 && aligned16(x) && (!grad_x || aligned16(grad_x)) &&
+      span_ok((w.RC + 4 * kBwdRows) * K, 2) && span_ok((w.RC + 4 * kBwdRows) * kRow, 4)) {
     // bf16 rows in bulk: grad_x and grad_phi on MFMA.
     if (w.nR > 1 && (grad_bias || grad_alpha))
       bias_part = (float*)(split_ws + align256((size_t)w.nR * K * kOut * sizeof(float)));

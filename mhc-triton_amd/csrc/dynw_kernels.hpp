@@ -132,173 +132,158 @@ __global__ __launch_bounds__(kThreads) void dynw_pack_phi_kernel(const float* __
   packed[(s * 3 + 2) * 64 + lane] = __builtin_bit_cast(u32x4, lo);
 }
 
-// One workgroup per tile of 32 * NW rows and a K chunk (wave w owns rows
-// 32w..32w+31).  A group of kMfmaGrpSteps = 4 steps covers 128 bytes of each
-// row.  A wave loads its 32 rows x 128 bytes with fully coalesced 16-byte
-// loads (load j: rows 8j .. 8j+7, lane l at row 8j + l/8, chunk l%8), one
-// group ahead of the MFMAs, and passes them through its own LDS tile into the
-// fragment layout (step j of lane l: row l%32, chunk 2j + l/32; chunk c of row
-// r is stored in slot c ^ (r & 7), so neither side has bank conflicts).
-// Loading the fragments straight from global memory (32 rows x 32 bytes per
-// load) ran at 158 us against 128 us this way at R = K = 16384, with the same
-// results.  The x rows go through one buffer span per workgroup: rows past R
-// read as zeros; chunks of steps past the K chunk are read but never used.
-// x is read once, with the streaming (nt) policy: launched back to back the
-// kernel took 99-101 us with it against 112-113 us without.
-// The phi fragments of a group are the same for all waves, so the workgroup
-// stages them once in double-buffered LDS (one barrier per group) instead of
-// every wave loading them from L2 (per-wave phi loads competing with the x
-// stream had cost ~45 us); the more waves share a stage, the less of that
-// L2 -> LDS traffic per x byte.  A group's 12 MFMAs (4 steps x 3 phi parts)
-// accumulate in one chain that starts from zero, and the group result is added
-// into `acc` with fp32 VALU adds: a single MFMA chain over all 1024 steps of
-// K = 16384 drifts by ~1e-5 relative, the round-to-nearest adds do not.  (At
-// 4 waves per workgroup the group chain did not fit 128 VGPRs and each step
-// was added on its own; with 16 waves the phi stage needs fewer registers per
-// lane.)  Writes the same 25-float partial
-// records as dynw_partial_kernel: part[r][kc][0:24] and the row's sum of
+// Forward projection on MFMA, K-slice form.  A workgroup of NW waves owns a
+// K chunk of NW * S steps and a range of rows; wave w owns the chunk's steps
+// w S .. w S + S - 1 (S * 32 bytes of each row) and keeps that slice's phi
+// fragments (3 parts per step) in registers for the whole kernel, so phi costs
+// no LDS or L2 traffic per x byte.  The workgroup walks its rows in 32-row
+// tiles; per tile each wave loads its 32 rows x S * 32 bytes with 16-byte loads
+// (S * 2 lanes per row), two tiles ahead, and passes them through its own LDS
+// tile into the fragment layout (chunk c of row r in slot c ^ (r % (2 S))).
+// At any time a workgroup streams NW * S * 32 = 2 KiB of each of 32 rows.  The
+// row-owning form this replaces (waves owning 32 rows each, phi staged in LDS
+// per 4-step group for a 512-row workgroup) streamed 128 bytes of each of 512
+// rows: as a plain read, that pattern took 86 us at R = K = 16384 against 76
+// for 512-byte runs, and the kernel took 108 us against 97 for this one.  The
+// S * 3 MFMAs of a tile accumulate in one chain from zero (smallest part
+// first); the NW waves' tile results and sums of squares meet in a
+// double-buffered LDS area (one barrier per tile) and are added in wave order
+// into 25-float partial records: part[r][kc][0:24] and the row's sum of
 // squares [24], which the VALU forms from the A fragments alongside the MFMAs
 // (v_dot2_f32_bf16 would take a quarter of the instructions, but its sums are
 // not fp32-accurate: H_pre moved by 6e-3 relative at K = 4096).  Requires
-// K % 16 == 0, a 16-byte aligned x and 32 * NW rows of K under 2^31 bytes.
-constexpr int kMfmaWaves = 16;                               // waves per workgroup
-constexpr int kMfmaRowsWg = 32 * kMfmaWaves;
-constexpr int kMfmaGrpSteps = 4;                             // 16-k steps per group
-constexpr int kMfmaPhiGrp = kMfmaGrpSteps * 3 * 64;          // 16-byte phi chunks per group
+// K % 16 == 0, a 16-byte aligned x and rows_per_wg * K * 2 bytes under 2^31.
+constexpr int kMfmaWaves = 8;                             // waves per workgroup (2 per SIMD)
+constexpr int kMfmaSteps = 8;                             // 16-k steps per wave slice
+constexpr int kMfmaChunkSteps = kMfmaWaves * kMfmaSteps;  // steps per K chunk
+constexpr int kMfmaRedCols = kPart;                       // 24 dot products and the sum of squares
+constexpr int kMfmaRedPitch = 36;                         // floats per (wave, column): 32 rows + pad
 
-// Four waves per SIMD (at most 128 VGPRs): the x loads in flight set the pace.
-// With NW = 16 one workgroup fills a CU (LDS: 24 KiB of phi stages + 4 KiB per wave).
-template <int NW = kMfmaWaves>
-__global__ __launch_bounds__(64 * NW, 4) void dynw_mfma_kernel(const __bf16* __restrict__ x,
-                                                            const u32x4* __restrict__ packed,
-                                                            float* __restrict__ part, int64_t R, int64_t K, int nK,
-                                                            int64_t steps_per_chunk) {
-  constexpr int G = kMfmaGrpSteps;
-  constexpr int kWgThreads = 64 * NW;
-  constexpr int kRowsWg = 32 * NW;
-  constexpr int kPhiPerThread = (kMfmaPhiGrp + kWgThreads - 1) / kWgThreads;
-  __shared__ __attribute__((aligned(16))) u32x4 phs[2][kMfmaPhiGrp];
-  __shared__ __attribute__((aligned(16))) u32x4 ast[NW][32 * 8];  // per wave: 32 rows x 8 chunks
+template <int NW = kMfmaWaves, int S = kMfmaSteps>
+__global__ __launch_bounds__(64 * NW, 2) void dynw_mfma_kernel(const __bf16* __restrict__ x,
+                                                             const u32x4* __restrict__ packed,
+                                                             float* __restrict__ part, int64_t R, int64_t K, int nK,
+                                                             int64_t rows_per_wg) {
+  constexpr int kThr = 64 * NW;
+  constexpr int L = 2 * S;      // 16-byte chunks of a row in the wave's slice
+  constexpr int RPL = 64 / L;   // rows per load instruction
+  constexpr int NL = 32 / RPL;  // loads per lane per tile
+  static_assert(64 % L == 0 && 32 % RPL == 0, "slice shape");
+  constexpr int kRedWave = kMfmaRedCols * kMfmaRedPitch;
+  __shared__ __attribute__((aligned(16))) u32x4 xt[NW][32 * L];
+  __shared__ __attribute__((aligned(16))) float red[2][NW * kRedWave];
   const int wave = threadIdx.x >> 6;
   const int lane = threadIdx.x & 63;
-  const int64_t rb0 = (int64_t)blockIdx.x * kRowsWg + wave * 32;
   const int kc = blockIdx.y;
   const int64_t nsteps = K / 16;
-  const int64_t s_beg = (int64_t)kc * steps_per_chunk;
-  const int64_t s_end = s_beg + steps_per_chunk < nsteps ? s_beg + steps_per_chunk : nsteps;
-  const int64_t ngrp = (s_end - s_beg + G - 1) / G;
-  const int64_t row = rb0 + (lane & 31);
-  const bool rok = row < R;
-  const int lrow = lane >> 3, lchk = lane & 7;
-  const int64_t rbw = (int64_t)blockIdx.x * kRowsWg;
-  const int64_t nrow = R - rbw < kRowsWg ? R - rbw : kRowsWg;
-  const Span<__bf16, true> xs(x + rbw * K, nrow * K);
-  const uint32_t lbase = (uint32_t)((wave * 32 + lrow) * K + 8 * lchk);
-  u32x4 a[2][G];
-  u32x4 pv[kPhiPerThread];
-  auto aload = [&](int64_t g, u32x4 (&d)[G]) {
-    const uint32_t kofs = (uint32_t)((s_beg + g * G) * 16);
+  const int64_t s0 = (int64_t)kc * (NW * S) + (int64_t)wave * S;  // the slice's first step
+  int nvalid = (int)(nsteps - s0 < S ? nsteps - s0 : S);         // its steps inside K
+  if (nvalid < 0) nvalid = 0;
+  u32x4 bf[S][3];
 #pragma unroll
-    for (int j = 0; j < G; ++j) d[j] = xs.load16<true>(lbase + (uint32_t)(8 * j) * (uint32_t)K + kofs);
+  for (int i = 0; i < S; ++i)
+#pragma unroll
+    for (int h = 0; h < 3; ++h) bf[i][h] = i < nvalid ? packed[((s0 + i) * 3 + h) * 64 + lane] : u32x4{0u, 0u, 0u, 0u};
+  const int64_t rbeg = (int64_t)blockIdx.x * rows_per_wg;
+  const int64_t rend = rbeg + rows_per_wg < R ? rbeg + rows_per_wg : R;
+  if (rbeg >= rend) return;  // the whole workgroup
+  const int64_t ntile = (rend - rbeg + 31) / 32;
+  const Span<__bf16, true> xs(x + rbeg * K, (rend - rbeg) * K);
+  const int lr = lane / L, lc = lane % L;
+  // element offset of load j of tile t: (32 t + RPL j + lr) K + 16 s0 + 8 lc (past K: never used)
+  const uint32_t lbase = (uint32_t)(lr * K + 16 * s0 + 8 * lc);
+  u32x4* tile = xt[wave];
+  u32x4 a[2][NL];
+  auto aload = [&](int64_t t, u32x4 (&d)[NL]) {
+#pragma unroll
+    for (int j = 0; j < NL; ++j) d[j] = xs.load16<true>(lbase + (uint32_t)((32 * t + RPL * j) * K));
   };
-  u32x4* tile = ast[wave];
-  auto astage = [&](const u32x4 (&raw)[G], u32x4 (&d)[G]) {
+  auto astage = [&](const u32x4 (&d)[NL]) {
 #pragma unroll
-    for (int j = 0; j < G; ++j) tile[(8 * j + lrow) * 8 + (lchk ^ (lrow & 7))] = raw[j];
+    for (int j = 0; j < NL; ++j) {
+      const int r = RPL * j + lr;
+      tile[r * L + (lc ^ (r & (L - 1)))] = d[j];
+    }
     // Lanes read what other lanes of the wave wrote: keep the order.
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
     __builtin_amdgcn_wave_barrier();
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-    const int fr = lane & 31;
-#pragma unroll
-    for (int j = 0; j < G; ++j) d[j] = tile[fr * 8 + ((2 * j + (lane >> 5)) ^ (fr & 7))];
   };
-  // Group g's phi chunks are packed[(s_beg + g G) * 192 + c], c < kMfmaPhiGrp (0 past the end).
-  auto pload = [&](int64_t g) {
-    const int64_t base = (s_beg + g * G) * 3 * 64;
-    const int64_t lim = nsteps * 3 * 64;
+  const int fr = lane & 31, half = lane >> 5;
+  // Tile t: its fragments from the wave's LDS tile, the chain, and the wave's
+  // results into red[buf]; then the workgroup adds the NW records of each output.
+  auto tile_compute = [&](int64_t t, int buf) {
+    f32x16 st;
 #pragma unroll
-    for (int i = 0; i < kPhiPerThread; ++i) {
-      const int slot = threadIdx.x + kWgThreads * i;
-      const int64_t c = base + slot;
-      if (kMfmaPhiGrp % kWgThreads == 0 || slot < kMfmaPhiGrp)
-        pv[i] = c < lim ? packed[c] : u32x4{0u, 0u, 0u, 0u};
-    }
-  };
-  auto pstore = [&](int buf) {
+    for (int i = 0; i < 16; ++i) st[i] = 0.f;
+    float ss = 0.f, ss_hi = 0.f;
 #pragma unroll
-    for (int i = 0; i < kPhiPerThread; ++i) {
-      const int slot = threadIdx.x + kWgThreads * i;
-      if (kMfmaPhiGrp % kWgThreads == 0 || slot < kMfmaPhiGrp) phs[buf][slot] = pv[i];
-    }
-  };
-  f32x16 acc, zero;
-#pragma unroll
-  for (int i = 0; i < 16; ++i) acc[i] = zero[i] = 0.f;
-  float ss = 0.f, ss_hi = 0.f;
-  auto compute = [&](int64_t g, const u32x4 (&d)[G], int buf) {
-    f32x16 st = zero;
-#pragma unroll
-    for (int j = 0; j < G; ++j) {
-      if (s_beg + g * G + j < s_end) {
-        const u32x4 b0 = phs[buf][(j * 3 + 0) * 64 + lane];
-        const u32x4 b1 = phs[buf][(j * 3 + 1) * 64 + lane];
-        const u32x4 b2 = phs[buf][(j * 3 + 2) * 64 + lane];
-        const bf16x8 av = __builtin_bit_cast(bf16x8, d[j]);
+    for (int i = 0; i < S; ++i) {
+      if (i < nvalid) {
+        const u32x4 d = tile[fr * L + ((2 * i + half) ^ (fr & (L - 1)))];
+        const bf16x8 av = __builtin_bit_cast(bf16x8, d);
         // smallest part first: the step sum sees the corrections before the bulk
-        st = __builtin_amdgcn_mfma_f32_32x32x16_bf16(av, __builtin_bit_cast(bf16x8, b2), st, 0, 0, 0);
-        st = __builtin_amdgcn_mfma_f32_32x32x16_bf16(av, __builtin_bit_cast(bf16x8, b1), st, 0, 0, 0);
-        st = __builtin_amdgcn_mfma_f32_32x32x16_bf16(av, __builtin_bit_cast(bf16x8, b0), st, 0, 0, 0);
-        // x^2 of the lane's 8 values: the low and high halves of each dword
-        // accumulate separately (two VALU ops per value)
+        st = __builtin_amdgcn_mfma_f32_32x32x16_bf16(av, __builtin_bit_cast(bf16x8, bf[i][2]), st, 0, 0, 0);
+        st = __builtin_amdgcn_mfma_f32_32x32x16_bf16(av, __builtin_bit_cast(bf16x8, bf[i][1]), st, 0, 0, 0);
+        st = __builtin_amdgcn_mfma_f32_32x32x16_bf16(av, __builtin_bit_cast(bf16x8, bf[i][0]), st, 0, 0, 0);
 #pragma unroll
         for (int c = 0; c < 4; ++c) {
-          const float lo_ = __uint_as_float(d[j][c] << 16);
-          const float hi_ = __uint_as_float(d[j][c] & 0xffff0000u);
+          const float lo_ = __uint_as_float(d[c] << 16);
+          const float hi_ = __uint_as_float(d[c] & 0xffff0000u);
           ss = fmaf(lo_, lo_, ss);
           ss_hi = fmaf(hi_, hi_, ss_hi);
         }
       }
     }
-    acc += st;
-  };
-  // Group g's loads sit in a[g % 2] and its phi in phs[g % 2]; the loop is
-  // unrolled by two so that neither register set is copied.
-  if (ngrp > 0) {
-    aload(0, a[0]);
-    pload(0);
-    pstore(0);
-  }
-  if (ngrp > 1) pload(1);
-  __syncthreads();
-  for (int64_t g = 0; g < ngrp; g += 2) {
-    if (g + 1 < ngrp) aload(g + 1, a[1]);
-    u32x4 f0[G];
-    astage(a[0], f0);
-    compute(g, f0, 0);
-    if (g + 1 < ngrp) pstore(1);
-    if (g + 2 < ngrp) pload(g + 2);
-    __syncthreads();
-    if (g + 1 >= ngrp) break;  // uniform
-    if (g + 2 < ngrp) aload(g + 2, a[0]);
-    u32x4 f1[G];
-    astage(a[1], f1);
-    compute(g + 1, f1, 1);
-    if (g + 2 < ngrp) pstore(0);
-    if (g + 3 < ngrp) pload(g + 3);
-    __syncthreads();
-  }
-  const int col = lane & 31;
-  if (col < kOut) {
+    float* rw = red[buf] + wave * kRedWave;
+    // lane l holds column l % 32, rows 8 q + 4 (l / 32) + 0..3 in st[4 q .. 4 q + 3]
+    if (fr < kOut) {
 #pragma unroll
-    for (int i = 0; i < 16; ++i) {
-      const int64_t r = rb0 + (i >> 2) * 8 + (lane >> 5) * 4 + (i & 3);
-      if (r < R) part[(r * nK + kc) * kPart + col] = acc[i];
+      for (int q = 0; q < 4; ++q)
+        *reinterpret_cast<f32x4*>(rw + fr * kMfmaRedPitch + 8 * q + 4 * half) =
+            f32x4{st[4 * q], st[4 * q + 1], st[4 * q + 2], st[4 * q + 3]};
     }
+    // the two k halves of a row's sum of squares sit in lanes l and l + 32
+    const float sq = ss + ss_hi;
+    const float sq2 = sq + __shfl_xor(sq, 32, 64);
+    if (half == 0) rw[kOut * kMfmaRedPitch + fr] = sq2;
+    __syncthreads();
+    // output o of the tile: row o / 25, record entry o % 25 (consecutive threads
+    // write one row's record); no branch between the NW reads
+    const float* rb = red[buf];
+#pragma unroll
+    for (int q = 0; q < (32 * kPart + kThr - 1) / kThr; ++q) {
+      const int o = threadIdx.x + q * kThr;
+      if (o < 32 * kPart) {
+        const int row = o / kPart, c = o - row * kPart;
+        const int64_t r = rbeg + 32 * t + row;
+        float v = 0.f;
+#pragma unroll
+        for (int w = 0; w < NW; ++w) v += rb[w * kRedWave + c * kMfmaRedPitch + row];
+        if (r < rend) part[(r * nK + kc) * kPart + c] = v;
+      }
+    }
+  };
+  // Tile t's loads sit in a[t % 2]; the loop is unrolled by two so that
+  // neither register set is copied, and runs an even number of tiles.  Every
+  // path issues the same loads: a tile past the end lies past the span and
+  // reads zeros without touching memory, and writes no records.  (With the
+  // next tile's loads behind a branch, or a mid-loop exit, the compiler's wait
+  // before a tile's staging has to hold for a path that skipped them, and
+  // waits for the loads in flight as well: 23 us more at R = K = 16384.)  The
+  // other waves read red[buf] of tile t until they reach the barrier of tile
+  // t + 1, so tile t + 2 may write it.
+  aload(0, a[0]);
+  __builtin_amdgcn_sched_barrier(0);  // tile 0's loads first: the first wait is for them alone
+  aload(1, a[1]);
+  for (int64_t t = 0; t < ntile; t += 2) {
+    astage(a[0]);
+    aload(t + 2, a[0]);
+    tile_compute(t, 0);
+    astage(a[1]);
+    aload(t + 3, a[1]);
+    tile_compute(t + 1, 1);
   }
-  ss += ss_hi;
-  const float sst = ss + __shfl_xor(ss, 32, 64);  // the two k halves of one row
-  if (lane < 32 && rok) part[(row * nK + kc) * kPart + kOut] = sst;
 }
 
 struct DynParams {
@@ -668,7 +653,7 @@ inline hipError_t launch_dynw_bwd_wide(const TX* x, const float* phi, const floa
 constexpr int kBwdWaves = 8;              // waves per workgroup (32 columns each)
 constexpr int kBwdMinWaves = 2;           // waves per SIMD the register allocation must allow
 constexpr int kBwdRows = 64;              // rows per staged block (two 32-row MFMA halves)
-constexpr int kBwdAhead = 2;              // blocks of loads in flight: register sets (2 or 3)
+constexpr int kBwdAhead = 2;              // blocks of loads in flight: register sets
 constexpr int kBwdGPitch = 40;            // bf16 per LDS row of the split G planes (columns 24..31 zero)
 
 typedef short s16x4 __attribute__((ext_vector_type(4)));
@@ -733,27 +718,35 @@ __global__ __launch_bounds__(64 * NW, MINW) void dynw_bwd_mfma_kernel(const __bf
     }
   }
   // Tile loads: x rows t / XLPR + XRPP i (16 bytes at column 8 (t % XLPR)); G record row
-  // t / 8 + GRPP j, floats 4 (t % 8)..+3.
+  // t / 8 + GRPP j, floats 4 (t % 8)..+3.  x, grad_x and the G records go through buffer
+  // spans of the chunk's rows, so that every load and store is issued on every path: rows
+  // past the chunk read zeros and drop their stores, and lanes without a column use an
+  // offset past any span.  (Loads and stores behind branches made the compiler's wait
+  // before each block's staging hold for a path without them, so it waited for the next
+  // block's loads as well.)
+  const int64_t nrows = r_end - r_beg;
+  const Span<__bf16, true> xsp(x + r_beg * K, nrows * K);
+  const Span<__bf16, true> gxsp(gx ? gx + r_beg * K : x, gx ? nrows * K : 0);
+  const Span<float, true> gsp(rowbuf + r_beg * kRow, nrows * kRow);
+  constexpr uint32_t kOobBf16 = 0x40000000u, kOobF32 = 0x20000000u;  // 2^31 bytes
   const int xr = threadIdx.x / XLPR;
   const int xc = (threadIdx.x % XLPR) * 8;
   const bool xcol_ok = k0 + xc < K;
   const int grow = threadIdx.x >> 3;
   const int gcol = (threadIdx.x & 7) * 4;
   const bool g_ok = grow < TR;
-  auto load_block = [&](int64_t r0, u32x4 (&xv)[NX], f32x4 (&gv)[NG]) {
+  const bool gld_ok = g_ok && gcol < 28;
+  // element offsets in the spans of row i of this lane in block b
+  auto xoff = [&](int64_t b, int i) -> uint32_t {
+    return xcol_ok ? (uint32_t)((TR * b + xr + XRPP * i) * K + k0 + xc) : kOobBf16;
+  };
+  auto load_block = [&](int64_t b, u32x4 (&xv)[NX], f32x4 (&gv)[NG]) {
 #pragma unroll
-    for (int i = 0; i < NX; ++i) {
-      const int64_t r = r0 + xr + XRPP * i;
-      xv[i] = (r < r_end && xcol_ok)
-                  ? __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(x + r * K + k0 + xc))
-                  : u32x4{0u, 0u, 0u, 0u};
-    }
+    for (int i = 0; i < NX; ++i) xv[i] = xsp.load16<true>(xoff(b, i));
 #pragma unroll
-    for (int j = 0; j < NG; ++j) {
-      const int64_t r = r0 + grow + GRPP * j;
-      gv[j] = (g_ok && r < r_end && gcol < 28) ? *reinterpret_cast<const f32x4*>(rowbuf + r * kRow + gcol)
-                                               : f32x4{0.f, 0.f, 0.f, 0.f};
-    }
+    for (int j = 0; j < NG; ++j)
+      gv[j] = __builtin_bit_cast(
+          f32x4, gsp.load16<false>(gld_ok ? (uint32_t)((TR * b + grow + GRPP * j) * kRow + gcol) : kOobF32));
   };
   // Transpose-read addresses: 16-lane group gi = lane / 16 covers columns 16 (gi & 1) .. +15 of
   // the wave's 32 and rows 8 (gi >> 1) + 0..3 of a 16-row step (+4 for the second read).
@@ -764,9 +757,9 @@ __global__ __launch_bounds__(64 * NW, MINW) void dynw_bwd_mfma_kernel(const __bf
 #pragma unroll
   for (int i = 0; i < 16; ++i) zero[i] = 0.f;
   dphi = zero;
-  // One 64-row block: stage the registers loaded for it, refill them with the block two ahead,
-  // compute, write its grad_x tile.
-  auto block = [&](int64_t r0, u32x4 (&xv)[NX], f32x4 (&gv)[NG]) {
+  // One 64-row block b of the chunk: stage the registers loaded for it, refill them with the
+  // block two ahead, compute, write its grad_x tile.
+  auto block = [&](int64_t b, u32x4 (&xv)[NX], f32x4 (&gv)[NG]) {
     // Stage this block: x as loaded, G split into hi + lo planes, coef apart.
 #pragma unroll
     for (int i = 0; i < NX; ++i) *reinterpret_cast<u32x4*>(&xs[(xr + XRPP * i) * kBwdXPitch + xc]) = xv[i];
@@ -788,7 +781,7 @@ __global__ __launch_bounds__(64 * NW, MINW) void dynw_bwd_mfma_kernel(const __bf
       }
     }
     __syncthreads();
-    if (r0 + kBwdAhead * TR < r_end) load_block(r0 + kBwdAhead * TR, xv, gv);  // in flight during the compute below
+    load_block(b + kBwdAhead, xv, gv);  // in flight during the compute below
 #pragma unroll
     for (int hh = 0; hh < TR / 32; ++hh) {
       // grad_x^T = phi G^T (see above) for each 32-row half; smallest products first, hi x hi last.
@@ -833,31 +826,26 @@ __global__ __launch_bounds__(64 * NW, MINW) void dynw_bwd_mfma_kernel(const __bf
       dphi = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a2, b2hi, dphi, 0, 0, 0);
     }
     __syncthreads();
-    // grad_x tile out: rows xr + XRPP i, 16 bytes at column xc.
-    if (gx && xcol_ok) {
+    // grad_x tile out: rows xr + XRPP i, 16 bytes at column xc (no grad_x: an empty span).
 #pragma unroll
-      for (int i = 0; i < NX; ++i) {
-        const int64_t r = r0 + xr + XRPP * i;
-        if (r < r_end)
-          __builtin_nontemporal_store(*reinterpret_cast<const u32x4*>(&gxs[(xr + XRPP * i) * kBwdXPitch + xc]),
-                                      reinterpret_cast<u32x4*>(gx + r * K + k0 + xc));
-      }
-    }
+    for (int i = 0; i < NX; ++i)
+      gxsp.store16<true>(xoff(b, i), *reinterpret_cast<const u32x4*>(&gxs[(xr + XRPP * i) * kBwdXPitch + xc]));
     // No barrier here: every read of xs / ghi / glo / cf in this block came
     // before the barrier above, and gxs is next written after the next
     // block's first barrier, which waits for these reads.
   };
-  // Blocks rotate through kBwdAhead register sets, each refilled with the block kBwdAhead ahead.
-  static_assert(kBwdAhead == 2 || kBwdAhead == 3, "register sets");
-  u32x4 xva[NX], xvb[NX], xvc[NX];
-  f32x4 gva[NG], gvb[NG], gvc[NG];
-  if (r_beg < r_end) load_block(r_beg, xva, gva);
-  if (r_beg + TR < r_end) load_block(r_beg + TR, xvb, gvb);
-  if (kBwdAhead == 3 && r_beg + 2 * TR < r_end) load_block(r_beg + 2 * TR, xvc, gvc);
-  for (int64_t r0 = r_beg; r0 < r_end; r0 += kBwdAhead * TR) {
-    block(r0, xva, gva);
-    if (r0 + TR < r_end) block(r0 + TR, xvb, gvb);
-    if (kBwdAhead == 3 && r0 + 2 * TR < r_end) block(r0 + 2 * TR, xvc, gvc);
+  // Blocks alternate between two register sets, each refilled with the block two ahead; the
+  // loop runs an even number of blocks (one past the chunk reads zeros and stores nothing).
+  static_assert(kBwdAhead == 2, "register sets");
+  u32x4 xva[NX], xvb[NX];
+  f32x4 gva[NG], gvb[NG];
+  const int64_t nblk = (nrows + TR - 1) / TR;
+  load_block(0, xva, gva);
+  __builtin_amdgcn_sched_barrier(0);  // block 0's loads first: the first wait is for them alone
+  load_block(1, xvb, gvb);
+  for (int64_t b = 0; b < nblk; b += 2) {
+    block(b, xva, gva);
+    block(b + 1, xvb, gvb);
   }
   if (do_bias) {
     // this chunk's rows strided over the workgroup's threads, then the wave sums in wave order
