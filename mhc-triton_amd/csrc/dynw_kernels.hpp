@@ -653,7 +653,7 @@ inline hipError_t launch_dynw_bwd_wide(const TX* x, const float* phi, const floa
 constexpr int kBwdWaves = 8;              // waves per workgroup (32 columns each)
 constexpr int kBwdMinWaves = 2;           // waves per SIMD the register allocation must allow
 constexpr int kBwdRows = 64;              // rows per staged block (two 32-row MFMA halves)
-constexpr int kBwdAhead = 2;              // blocks of loads in flight: register sets
+constexpr int kBwdAhead = 2;              // blocks of loads in flight: register sets (three: slower)
 constexpr int kBwdGPitch = 40;            // bf16 per LDS row of the split G planes (columns 24..31 zero)
 
 typedef short s16x4 __attribute__((ext_vector_type(4)));
@@ -834,18 +834,21 @@ __global__ __launch_bounds__(64 * NW, MINW) void dynw_bwd_mfma_kernel(const __bf
     // before the barrier above, and gxs is next written after the next
     // block's first barrier, which waits for these reads.
   };
-  // Blocks alternate between two register sets, each refilled with the block two ahead; the
-  // loop runs an even number of blocks (one past the chunk reads zeros and stores nothing).
-  static_assert(kBwdAhead == 2, "register sets");
-  u32x4 xva[NX], xvb[NX];
-  f32x4 gva[NG], gvb[NG];
+  // Blocks rotate through kBwdAhead register sets, each refilled with the block kBwdAhead
+  // ahead; the loop runs a multiple of kBwdAhead blocks (those past the chunk read zeros and
+  // store nothing).
+  constexpr int A = kBwdAhead;
+  u32x4 xv[A][NX];
+  f32x4 gv[A][NG];
   const int64_t nblk = (nrows + TR - 1) / TR;
-  load_block(0, xva, gva);
-  __builtin_amdgcn_sched_barrier(0);  // block 0's loads first: the first wait is for them alone
-  load_block(1, xvb, gvb);
-  for (int64_t b = 0; b < nblk; b += 2) {
-    block(b, xva, gva);
-    block(b + 1, xvb, gvb);
+#pragma unroll
+  for (int u = 0; u < A; ++u) {
+    load_block(u, xv[u], gv[u]);
+    __builtin_amdgcn_sched_barrier(0);  // in block order: each wait is for the oldest loads alone
+  }
+  for (int64_t b = 0; b < nblk; b += A) {
+#pragma unroll
+    for (int u = 0; u < A; ++u) block(b + u, xv[u], gv[u]);
   }
   if (do_bias) {
     // this chunk's rows strided over the workgroup's threads, then the wave sums in wave order
