@@ -782,20 +782,58 @@ __global__ __launch_bounds__(64 * NW, MINW) void dynw_bwd_mfma_kernel(const __bf
     }
     __syncthreads();
     load_block(b + kBwdAhead, xv, gv);  // in flight during the compute below
+    // grad_phi operands for the block's 16-row steps, read before the grad_x work so that their
+    // LDS latency overlaps it.  A = x^T (lane l: column 32 wave + l % 32, rows
+    // 16 st + 8 (l / 32) + e), B = G (same rows, j = l % 32).
+    constexpr int NST = TR / 16;
+    bf16x8 pa[NST], pbh[NST], pbl[NST];
 #pragma unroll
-    for (int hh = 0; hh < TR / 32; ++hh) {
-      // grad_x^T = phi G^T (see above) for each 32-row half; smallest products first, hi x hi last.
-      f32x16 d = zero;
+    for (int st = 0; st < NST; ++st) {
+      const int rb = 16 * st + tr_row;
+      const u32x2 x0 = lds_read_tr16(&xs[rb * kBwdXPitch + 32 * wave + tr_col]);
+      const u32x2 x1 = lds_read_tr16(&xs[(rb + 4) * kBwdXPitch + 32 * wave + tr_col]);
+      const u32x2 h0 = lds_read_tr16(&ghi[rb * kBwdGPitch + tr_col]);
+      const u32x2 h1 = lds_read_tr16(&ghi[(rb + 4) * kBwdGPitch + tr_col]);
+      const u32x2 q0 = lds_read_tr16(&glo[rb * kBwdGPitch + tr_col]);
+      const u32x2 q1 = lds_read_tr16(&glo[(rb + 4) * kBwdGPitch + tr_col]);
+      pa[st] = __builtin_bit_cast(bf16x8, u32x4{x0[0], x0[1], x1[0], x1[1]});
+      pbh[st] = __builtin_bit_cast(bf16x8, u32x4{h0[0], h0[1], h1[0], h1[1]});
+      pbl[st] = __builtin_bit_cast(bf16x8, u32x4{q0[0], q0[1], q1[0], q1[1]});
+    }
+    // grad_x^T = phi G^T (see above) for the two 32-row halves as two independent chains,
+    // interleaved; each chain takes its products smallest first, hi x hi last.
+    constexpr int NH = TR / 32;
+    bf16x8 ghv[NH][2], glv[NH][2];
+#pragma unroll
+    for (int hh = 0; hh < NH; ++hh)
 #pragma unroll
       for (int js = 0; js < 2; ++js) {
         const int j0 = 16 * js + 8 * (lane >> 5);
-        const bf16x8 ghv = *reinterpret_cast<const bf16x8*>(&ghi[(32 * hh + (lane & 31)) * kBwdGPitch + j0]);
-        const bf16x8 glv = *reinterpret_cast<const bf16x8*>(&glo[(32 * hh + (lane & 31)) * kBwdGPitch + j0]);
-        d = __builtin_amdgcn_mfma_f32_32x32x16_bf16(bhi[js], glv, d, 0, 0, 0);
-        d = __builtin_amdgcn_mfma_f32_32x32x16_bf16(blo[js], ghv, d, 0, 0, 0);
-        d = __builtin_amdgcn_mfma_f32_32x32x16_bf16(bhi[js], ghv, d, 0, 0, 0);
+        ghv[hh][js] = *reinterpret_cast<const bf16x8*>(&ghi[(32 * hh + (lane & 31)) * kBwdGPitch + j0]);
+        glv[hh][js] = *reinterpret_cast<const bf16x8*>(&glo[(32 * hh + (lane & 31)) * kBwdGPitch + j0]);
       }
-      // Epilogue: lane l holds row l % 32, columns 32 wave + 8 q + 4 (l / 32) + 0..3 in d[4 q ..].
+    f32x16 d[NH];
+#pragma unroll
+    for (int hh = 0; hh < NH; ++hh) d[hh] = zero;
+#pragma unroll
+    for (int js = 0; js < 2; ++js) {
+#pragma unroll
+      for (int hh = 0; hh < NH; ++hh) d[hh] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(bhi[js], glv[hh][js], d[hh], 0, 0, 0);
+#pragma unroll
+      for (int hh = 0; hh < NH; ++hh) d[hh] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(blo[js], ghv[hh][js], d[hh], 0, 0, 0);
+#pragma unroll
+      for (int hh = 0; hh < NH; ++hh) d[hh] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(bhi[js], ghv[hh][js], d[hh], 0, 0, 0);
+    }
+    // grad_phi += x^T G over the steps (one chain, in step order).
+#pragma unroll
+    for (int st = 0; st < NST; ++st) {
+      dphi = __builtin_amdgcn_mfma_f32_32x32x16_bf16(pa[st], pbl[st], dphi, 0, 0, 0);
+      dphi = __builtin_amdgcn_mfma_f32_32x32x16_bf16(pa[st], pbh[st], dphi, 0, 0, 0);
+    }
+    // Epilogue: lane l holds row l % 32 of its half, columns 32 wave + 8 q + 4 (l / 32) + 0..3
+    // in d[hh][4 q ..].
+#pragma unroll
+    for (int hh = 0; hh < NH; ++hh) {
       const int row = 32 * hh + (lane & 31);
       const float c = cf[row];
 #pragma unroll
@@ -804,26 +842,9 @@ __global__ __launch_bounds__(64 * NW, MINW) void dynw_bwd_mfma_kernel(const __bf
         const bf16x4 x4 = *reinterpret_cast<const bf16x4*>(&xs[row * kBwdXPitch + cc]);
         bf16x4 o4;
 #pragma unroll
-        for (int r = 0; r < 4; ++r) o4[r] = (__bf16)(d[4 * q + r] + c * (float)x4[r]);
+        for (int r = 0; r < 4; ++r) o4[r] = (__bf16)(d[hh][4 * q + r] + c * (float)x4[r]);
         *reinterpret_cast<bf16x4*>(&gxs[row * kBwdXPitch + cc]) = o4;
       }
-    }
-    // grad_phi += x^T G over the block's 16-row steps.  A = x^T (lane l: column
-    // 32 wave + l % 32, rows 16 st + 8 (l / 32) + e), B = G (same rows, j = l % 32).
-#pragma unroll
-    for (int st = 0; st < TR / 16; ++st) {
-      const int rb = 16 * st + tr_row;
-      const u32x2 x0 = lds_read_tr16(&xs[rb * kBwdXPitch + 32 * wave + tr_col]);
-      const u32x2 x1 = lds_read_tr16(&xs[(rb + 4) * kBwdXPitch + 32 * wave + tr_col]);
-      const u32x2 h0 = lds_read_tr16(&ghi[rb * kBwdGPitch + tr_col]);
-      const u32x2 h1 = lds_read_tr16(&ghi[(rb + 4) * kBwdGPitch + tr_col]);
-      const u32x2 q0 = lds_read_tr16(&glo[rb * kBwdGPitch + tr_col]);
-      const u32x2 q1 = lds_read_tr16(&glo[(rb + 4) * kBwdGPitch + tr_col]);
-      const bf16x8 a2 = __builtin_bit_cast(bf16x8, u32x4{x0[0], x0[1], x1[0], x1[1]});
-      const bf16x8 b2hi = __builtin_bit_cast(bf16x8, u32x4{h0[0], h0[1], h1[0], h1[1]});
-      const bf16x8 b2lo = __builtin_bit_cast(bf16x8, u32x4{q0[0], q0[1], q1[0], q1[1]});
-      dphi = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a2, b2lo, dphi, 0, 0, 0);
-      dphi = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a2, b2hi, dphi, 0, 0, 0);
     }
     __syncthreads();
     // grad_x tile out: rows xr + XRPP i, 16 bytes at column xc (no grad_x: an empty span).
