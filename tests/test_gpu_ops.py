@@ -180,7 +180,9 @@ def test_add_residual_forward_backward(dtype, bo_dtype, shape):
                                         (300, 2048, torch.float16),
                                         # bf16 rows in bulk take the MFMA projection (ragged last tile)
                                         (1000, 4096, torch.bfloat16), (4096, 16384, torch.bfloat16),
-                                        (64, 1040, torch.bfloat16)])
+                                        (64, 1040, torch.bfloat16),
+                                        # a last K chunk that ends inside a wave's slice, a one-row tile
+                                        (257, 3008, torch.bfloat16)])
 def test_dynamic_weights_forward_backward(R, K, xdtype):
     import mhc
 
