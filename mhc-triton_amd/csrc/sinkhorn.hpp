@@ -172,6 +172,95 @@ __device__ __forceinline__ void sk_backward(const float (&mat)[16], float (&d)[1
   }
 }
 
+// The same gradient for iters <= TMAX from the scaling vectors of every round,
+// kept in registers instead of recomputed from checkpoints.  After t rounds
+// P = diag(u_t) P0 diag(v_t), with u_0 = v_0 = 1; the forward runs as in
+// sk_forward (carrying w = 1/u and z = 1/v) and keeps u_t and v_t, 8 floats
+// per round.  In round t the row normalisation maps u_t to u_{t+1} and the
+// column normalisation v_t to v_{t+1}, so
+//   row scale r_i = 1 / (rowsum_i + eps) = u_{t+1},i / u_t,i,  mr_ij = P0_ij u_{t+1},i v_t,j,
+//   col scale c_j = 1 / (colsum_j + eps) = v_{t+1},j / v_t,j,  mc_ij = P0_ij u_{t+1},i v_{t+1},j,
+// and the two normalisation backwards are those of sk_round_backward.  Per
+// round that is 40 VALU + 8 v_rcp forward and about 128 + 8 backward, against
+// 72 per recomputed round plus 144 per backward round for the checkpointed
+// sweep.  (Keeping w and z instead let the compiler reuse the forward's
+// reciprocals in the backward and hold both sets live: 303 VGPRs.)
+template <int TMAX>
+__device__ __forceinline__ void sk_backward_scaled(const float (&mat)[16], float (&d)[16], int iters, float eps) {
+  float p0[16];
+  uint32_t neg = 0u, zero = 0u;  // sgn(M) as two bit masks, so that M need not stay live
+#pragma unroll
+  for (int k = 0; k < 16; ++k) {
+    p0[k] = __builtin_fabsf(mat[k]) + eps;
+    neg |= (mat[k] < 0.f ? 1u : 0u) << k;
+    zero |= (mat[k] == 0.f ? 1u : 0u) << k;
+  }
+  float U[TMAX + 1][4], V[TMAX + 1][4];
+#pragma unroll
+  for (int k = 0; k < 4; ++k) U[0][k] = V[0][k] = 1.f;
+  {
+    float w[4] = {1.f, 1.f, 1.f, 1.f}, z[4] = {1.f, 1.f, 1.f, 1.f};
+#pragma unroll
+    for (int t = 0; t < TMAX; ++t) {
+      if (t < iters) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const float dot = p0[4 * i] * V[t][0] + p0[4 * i + 1] * V[t][1] + p0[4 * i + 2] * V[t][2] +
+                            p0[4 * i + 3] * V[t][3];
+          w[i] = __builtin_fmaf(eps, w[i], dot);
+          U[t + 1][i] = fast_rcp(w[i]);
+        }
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const float dot = U[t + 1][0] * p0[j] + U[t + 1][1] * p0[4 + j] + U[t + 1][2] * p0[8 + j] +
+                            U[t + 1][3] * p0[12 + j];
+          z[j] = __builtin_fmaf(eps, z[j], dot);
+          V[t + 1][j] = fast_rcp(z[j]);
+        }
+      }
+    }
+  }
+#pragma unroll
+  for (int t = TMAX - 1; t >= 0; --t) {
+    if (t < iters) {
+      float r[4], c[4], a[16];
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        r[k] = t == 0 ? U[1][k] : U[t + 1][k] * fast_rcp(U[t][k]);
+        c[k] = t == 0 ? V[1][k] : V[t + 1][k] * fast_rcp(V[t][k]);
+      }
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) a[4 * i + j] = p0[4 * i + j] * U[t + 1][i];
+      // Column normalisation: dmr[:,j] = d[:,j] c_j - <d[:,j], mc[:,j]> c_j.
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const float dot =
+            (d[j] * a[j] + d[4 + j] * a[4 + j] + d[8 + j] * a[8 + j] + d[12 + j] * a[12 + j]) * V[t + 1][j];
+        const float dc = dot * c[j];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) d[4 * i + j] = __builtin_fmaf(d[4 * i + j], c[j], -dc);
+      }
+      // Row normalisation: dm[i,:] = dmr[i,:] r_i - <dmr[i,:], mr[i,:]> r_i.
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const float dot = d[4 * i] * (a[4 * i] * V[t][0]) + d[4 * i + 1] * (a[4 * i + 1] * V[t][1]) +
+                          d[4 * i + 2] * (a[4 * i + 2] * V[t][2]) + d[4 * i + 3] * (a[4 * i + 3] * V[t][3]);
+        const float dr = dot * r[i];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) d[4 * i + j] = __builtin_fmaf(d[4 * i + j], r[i], -dr);
+      }
+    }
+  }
+  // d|M|/dM = sgn(M), sgn(0) = 0.
+#pragma unroll
+  for (int e = 0; e < 16; ++e) {
+    const float sg = (zero >> e) & 1u ? 0.f : ((neg >> e) & 1u ? -1.f : 1.f);
+    d[e] *= sg;
+  }
+}
+
 // ---------------------------------------------------------------------------
 // 16-lane form, for the latency-bound per-row kernels (a handful of matrices,
 // one per batch row): one matrix is spread over 16 consecutive lanes, lane
