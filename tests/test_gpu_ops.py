@@ -43,8 +43,11 @@ def test_sinkhorn_forward(dtype):
     assert rel_err(to_np(P), O.sinkhorn(to_np(M), 20, 1e-8)) < TOL[dtype]
 
 
-@pytest.mark.parametrize("iters", [0, 1, 7, 20, 33])
+@pytest.mark.parametrize("iters", [0, 1, 7, 20, 21, 33])
 def test_sinkhorn_forward_backward_iters(iters):
+    """Up to 20 rounds the aligned backward keeps every round's scaling vectors in registers;
+    beyond that, and on the unaligned path, it recomputes states from checkpoints.  Both forms
+    are held to the oracle and to each other."""
     import mhc
 
     g = gen(1)
@@ -59,6 +62,13 @@ def test_sinkhorn_forward_backward_iters(iters):
     ref = O.sinkhorn_backward(to_np(M), to_np(dP), iters, 1e-8)
     assert rel_err(to_np(Ml.grad), ref) < 1e-4
     assert Ml.grad[0, 0, 0].item() == 0.0 and Ml.grad[7, 2, 1].item() == 0.0
+    # the same matrices at an offset of one element: the scalar path, checkpointed backward
+    flat = torch.cat([torch.zeros(1, device=DEV), M.reshape(-1)]).requires_grad_(True)
+    Mu = flat[1:].view(300, 4, 4)
+    assert Mu.data_ptr() % 16 != 0
+    mhc.sinkhorn_knopp(Mu, iters, 1e-8).backward(dP)
+    gu = flat.grad[1:].view(300, 4, 4)
+    assert rel_err(to_np(gu), to_np(Ml.grad)) < 1e-5
 
 
 def test_sinkhorn_config2_column_sums_and_oracle():
