@@ -192,7 +192,9 @@ def test_add_residual_forward_backward(dtype, bo_dtype, shape):
                                         (1000, 4096, torch.bfloat16), (4096, 16384, torch.bfloat16),
                                         (64, 1040, torch.bfloat16),
                                         # a last K chunk that ends inside a wave's slice, a one-row tile
-                                        (257, 3008, torch.bfloat16)])
+                                        (257, 3008, torch.bfloat16),
+                                        # one 16-k step (seven of the eight waves' slices past K)
+                                        (65, 16, torch.bfloat16)])
 def test_dynamic_weights_forward_backward(R, K, xdtype):
     import mhc
 
