@@ -230,6 +230,28 @@ def test_dynamic_weights_forward_backward(R, K, xdtype):
     assert rel_err(np.array([a.grad.item() for a in leaves[3:]]), np.array(ga)) < 1e-4
 
 
+@pytest.mark.parametrize("R,K", [(1000, 4096), (257, 3008)])
+def test_dynamic_weights_mfma_paths_are_deterministic(R, K):
+    """The MFMA projection adds its waves' tile results and the K chunks in a fixed order, and the
+    backward's grad_phi / bias partials likewise: two calls give the same bits."""
+    import mhc
+
+    g = gen(8)
+    x = randn((R, K), g, torch.bfloat16, scale=1 / 64)
+    phi = randn((K, 24), g, scale=0.02)
+    bias = randn((24,), g, scale=0.1)
+    alphas = [torch.tensor([v], device=DEV) for v in (0.1, 0.2, 0.3)]
+    gouts = [randn((R, 4), g), randn((R, 4), g), randn((R, 4, 4), g)]
+    runs = []
+    for _ in range(2):
+        leaves = [t.clone().requires_grad_(True) for t in (x, phi, bias, *alphas)]
+        outs = mhc.fused_dynamic_weights(*leaves, 20, 1e-6)
+        torch.autograd.backward(list(outs), gouts)
+        runs.append([o.detach() for o in outs] + [t.grad for t in leaves])
+    for a, b in zip(*runs):
+        assert torch.equal(a, b)
+
+
 def test_dynamic_weights_default_init_sgn_zero():
     """phi = 0 with the module's default bias: scaled_res has 12 exact zeros,
     whose gradient follows torch (sgn(0) = 0)."""
