@@ -194,7 +194,9 @@ def test_add_residual_forward_backward(dtype, bo_dtype, shape):
                                         # a last K chunk that ends inside a wave's slice, a one-row tile
                                         (257, 3008, torch.bfloat16),
                                         # one 16-k step (seven of the eight waves' slices past K)
-                                        (65, 16, torch.bfloat16)])
+                                        (65, 16, torch.bfloat16),
+                                        # K % 16 = 8: the VALU projection forward, the MFMA backward
+                                        (100, 1000, torch.bfloat16)])
 def test_dynamic_weights_forward_backward(R, K, xdtype):
     import mhc
 
