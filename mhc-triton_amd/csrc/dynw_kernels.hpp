@@ -398,6 +398,10 @@ __global__ __launch_bounds__(kThreads) void dynw_finalize_rows_kernel(const floa
   const int64_t r = live ? r_grp : R - 1;  // idle groups redo the last row and store nothing
   const float* p = part + r * nK * kPart;
   float raw_res = 0.f, raw_pp = 0.f, sumsq = 0.f;
+  // unrolled so that the chunks' loads are in flight together (the sums keep
+  // chunk order): 8.4 us at R = 16384, nK = 16, against 10.9 us rolled and
+  // 15.2 us unrolled by 16
+#pragma unroll 8
   for (int k = 0; k < nK; ++k, p += kPart) {
     raw_res += p[8 + e];
     raw_pp += p[e & 7];
