@@ -437,13 +437,15 @@ __global__ __launch_bounds__(kThreads) void dynw_bwd_rows_kernel(const float* __
                                                                  InRow g_res, const float* __restrict__ part20,
                                                                  int nblk, float* __restrict__ rowbuf, int64_t R,
                                                                  int64_t K, int iters, float eps) {
-  static_assert(RPW == 1 || RPW == 4, "rows per workgroup");
-  __shared__ float slots[kSkSlots * 64];
+  static_assert(RPW == 1 || RPW == 4 || RPW == 16, "rows per workgroup");
+  // RPW = 16 (gradients as rows only, no part20): every wave runs four rows.
+  constexpr int kRowWaves = RPW == 16 ? 4 : 1;
+  __shared__ float slots[kSkSlots * 64 * kRowWaves];
   __shared__ float red[4][20];
   __shared__ float quarter[4][4][20];  // [wave][16-lane row][value]
   const int wave = threadIdx.x >> 6;
   const int lane = threadIdx.x & 63;
-  if (part20) {
+  if (RPW != 16 && part20) {
     const int64_t rw = (int64_t)blockIdx.x * RPW + (RPW == 4 ? wave : 0);
     const int k0 = RPW == 4 ? lane : wave * 64 + lane;
     const int kstep = RPW == 4 ? 64 : 256;
@@ -484,16 +486,19 @@ __global__ __launch_bounds__(kThreads) void dynw_bwd_rows_kernel(const float* __
                         quarter[wave][3][lane];
     }
   }
-  __syncthreads();
-  if (wave != 0) return;
+  if constexpr (RPW != 16) {
+    __syncthreads();
+    if (wave != 0) return;
+  }
   const int e = lane & 15;
   const int j = e & 3;
-  const int64_t r_grp = (int64_t)blockIdx.x * RPW + (lane >> 4);
-  const bool live = r_grp < R && (lane >> 4) < RPW;
+  const int64_t r_grp = (int64_t)blockIdx.x * RPW + (RPW == 16 ? 4 * wave : 0) + (lane >> 4);
+  const bool live = r_grp < R && (RPW == 16 || (lane >> 4) < RPW);
   const int64_t r = live ? r_grp : R - 1;  // idle groups redo the last row and store nothing
   const int rr = RPW == 4 ? (lane >> 4) : 0;  // this group's row in `red`
-  const float gpre = part20 ? red[rr][j] : (g_pre.p ? g_pre.p[r * g_pre.stride + j] : 0.f);
-  const float gres = part20 ? red[rr][4 + e] : (g_res.p ? g_res.p[r * g_res.stride + e] : 0.f);
+  const bool from_part = RPW != 16 && part20;
+  const float gpre = from_part ? red[rr][j] : (g_pre.p ? g_pre.p[r * g_pre.stride + j] : 0.f);
+  const float gres = from_part ? red[rr][4 + e] : (g_res.p ? g_res.p[r * g_res.stride + e] : 0.f);
   const float gpost = g_post.p ? g_post.p[r * g_post.stride + j] : 0.f;
   const float* a = aux + r * kPart;
   const float inv_rms = a[kOut];
@@ -503,7 +508,8 @@ __global__ __launch_bounds__(kThreads) void dynw_bwd_rows_kernel(const float* __
   // H_res = Sinkhorn(|s_res| + eps): gradient w.r.t. s_res.
   const float s_res = inv_rms * ar * raw_res + P.bias_res[e];
   const float gs_res = iters == 20 ? sk16_backward_fixed<20>(s_res, gres, eps)
-                                   : sk16_backward<kSkSlots>(s_res, gres, iters, eps, slots + lane, 64);
+                                   : sk16_backward<kSkSlots>(s_res, gres, iters, eps,
+                                                             slots + (RPW == 16 ? wave * kSkSlots * 64 : 0) + lane, 64);
   // H_pre = sigmoid / (sum + eps) on lanes 0..3, H_post = 2 sigmoid on lanes 4..7.
   const bool is_pre = (e & 4) == 0;
   const float al_pp = is_pre ? *P.alpha_pre : *P.alpha_post;
