@@ -159,6 +159,27 @@ static WidePlan wide_plan(int64_t R, int64_t K) {
   return p;
 }
 
+// Row chunks of the MFMA backward (dynw_bwd_mfma_kernel): one 8-wave workgroup
+// fits a CU, so about kMfmaTargetWg workgroups, each walking a long chunk: its
+// pipeline fills and drains once per chunk, and fewer chunks leave fewer grad_phi
+// partials.  At R = K = 16384, 4 chunks of 4096 rows (256 workgroups) took
+// 179-181 us against 199-203 us for 16 (1024 workgroups) and 223-224 us for 32.
+// Never more chunks than the wide plan w (whose workspace holds the partials);
+// chunks are split further while a chunk's buffer spans would pass 2^31 bytes.
+static WidePlan mfma_bwd_plan(int64_t R, int64_t K, const WidePlan& w) {
+  const int64_t ncb = (K + 32 * kBwdWaves - 1) / (32 * kBwdWaves);
+  int64_t nr = (kMfmaTargetWg + ncb - 1) / ncb;
+  if (nr > w.nR) nr = w.nR;
+  for (;;) {
+    WidePlan p;
+    p.RC = (R + nr - 1) / nr;
+    p.nR = (int)((R + p.RC - 1) / p.RC);
+    const int64_t span_rows = p.RC + 4 * kBwdRows;
+    if (nr >= w.nR || (span_ok(span_rows * K, 2) && span_ok(span_rows * kRow, 4))) return nr >= w.nR ? w : p;
+    nr = 2 * nr < w.nR ? 2 * nr : w.nR;
+  }
+}
+
 extern "C" size_t mhc_dynamic_weights_backward_workspace_bytes(int64_t R, int64_t K) {
   if (R <= 0) return 0;
   const WidePlan w = wide_plan(R, K);
@@ -211,25 +232,28 @@ extern "C" int mhc_dynamic_weights_backward(const void* x, int dtype_x, const fl
   if (int rc = hip_status(hipGetLastError(), "dynamic_weights_backward rows launch")) return rc;
   const bool phi_vec = aligned16(phi);
   const WidePlan w = wide_plan(R, K);
+  const bool mfma_ok =
+      dtype_x == MHC_DTYPE_BF16 && R >= kMfmaMinRows && K % 8 == 0 && aligned16(x) && (!grad_x || aligned16(grad_x));
+  // the row chunks of the pass that runs (the MFMA plan has at most w.nR)
+  const WidePlan pl = mfma_ok ? mfma_bwd_plan(R, K, w) : w;
   char* split_ws = (char*)workspace + align256((size_t)R * kRow * sizeof(float));
-  float* gphi_part = (w.nR > 1 && grad_phi) ? (float*)split_ws : nullptr;
+  float* gphi_part = (pl.nR > 1 && grad_phi) ? (float*)split_ws : nullptr;
   float* bias_part = nullptr;  // MFMA path, split rows: per-chunk grad_bias / grad_alpha records
   int rc;
   // (the kernel's buffer spans reach up to four blocks past a chunk's rows)
-  if (dtype_x == MHC_DTYPE_BF16 && R >= kMfmaMinRows && K % 8 == 0 && aligned16(x) && (!grad_x || aligned16(grad_x)) &&
-      span_ok((w.RC + 4 * kBwdRows) * K, 2) && span_ok((w.RC + 4 * kBwdRows) * kRow, 4)) {
+  if (mfma_ok && span_ok((pl.RC + 4 * kBwdRows) * K, 2) && span_ok((pl.RC + 4 * kBwdRows) * kRow, 4)) {
     // bf16 rows in bulk: grad_x and grad_phi on MFMA.
-    if (w.nR > 1 && (grad_bias || grad_alpha))
+    if (pl.nR > 1 && (grad_bias || grad_alpha))
       bias_part = (float*)(split_ws + align256((size_t)w.nR * K * kOut * sizeof(float)));
     const unsigned ncb = (unsigned)((K + 32 * kBwdWaves - 1) / (32 * kBwdWaves));
-    dynw_bwd_mfma_kernel<><<<dim3(ncb, (unsigned)w.nR), 64 * kBwdWaves, 0, st>>>(
+    dynw_bwd_mfma_kernel<><<<dim3(ncb, (unsigned)pl.nR), 64 * kBwdWaves, 0, st>>>(
         (const __bf16*)x, phi, rowbuf, (__bf16*)grad_x, grad_phi, gphi_part, bias_part, grad_bias, grad_alpha, R, K,
-        w.RC);
+        pl.RC);
     rc = hip_status(hipGetLastError(), "dynamic_weights_backward mfma launch");
   } else {
     rc = MHC_DISPATCH_DTYPE(dtype_x, [&] {
       return hip_status(launch_dynw_bwd_wide<T, T>((const T*)x, phi, rowbuf, (T*)grad_x, grad_phi, gphi_part,
-                                                   grad_bias, grad_alpha, R, K, w.RC, (unsigned)w.nR, phi_vec, st),
+                                                   grad_bias, grad_alpha, R, K, pl.RC, (unsigned)pl.nR, phi_vec, st),
                         "dynamic_weights_backward wide launch");
     });
   }
@@ -237,7 +261,7 @@ extern "C" int mhc_dynamic_weights_backward(const void* x, int dtype_x, const fl
   const int64_t n = gphi_part ? K * kOut : 0;
   const int64_t nt = n + (bias_part ? 27 : 0);
   dynw_gphi_reduce_kernel<><<<dim3((unsigned)((nt + kThreads - 1) / kThreads)), kThreads, 0, st>>>(
-      gphi_part, grad_phi, n, w.nR, bias_part, grad_bias, grad_alpha);
+      gphi_part, grad_phi, n, pl.nR, bias_part, grad_bias, grad_alpha);
   return hip_status(hipGetLastError(), "dynamic_weights_backward grad_phi reduce launch");
 }
 

@@ -654,9 +654,11 @@ inline hipError_t launch_dynw_bwd_wide(const TX* x, const float* phi, const floa
 //           interleaved.
 // The LDS padding leaves 2-way bank conflicts on the transpose and epilogue
 // reads; making those reads conflict-free (wrong results, timing only) saved
-// 1%.  At R = K = 16384 the kernel takes about 200 us; copies of it without
-// the grad_x stores took 168 us and without the MFMA work 181 us, against
-// 170 us for a plain copy of the same strips.  Requires K % 8 == 0 and
+// 1%.  At R = K = 16384 the kernel takes about 181 us with 4 row chunks of
+// 4096 rows (one workgroup per CU), 200 us with 16 chunks of 1024; with 16
+// chunks, copies of it without the grad_x stores took 168 us and without the
+// MFMA work 181 us, against 170 us for a plain copy of the same strips
+// (1024 workgroups).  Requires K % 8 == 0 and
 // 16-byte aligned x and grad_x.  Grid (K / kBwdCols column blocks, row
 // chunks); outputs as dynw_bwd_wide_kernel: grad_phi direct with one chunk,
 // else per-chunk partials.  Column block 0 of each row chunk also sums the
