@@ -189,6 +189,10 @@ struct Span<T, true> {
     return __builtin_amdgcn_raw_buffer_load_b128(r, (int)(e * (uint32_t)sizeof(T)), 0, NT ? 2 : 0);
   }
   template <bool NT>
+  __device__ __forceinline__ uint32_t load4(uint32_t e) const {
+    return __builtin_amdgcn_raw_buffer_load_b32(r, (int)(e * (uint32_t)sizeof(T)), 0, NT ? 2 : 0);
+  }
+  template <bool NT>
   __device__ __forceinline__ void store16(uint32_t e, u32x4 v) const {
     __builtin_amdgcn_raw_buffer_store_b128(v, r, (int)(e * (uint32_t)sizeof(T)), 0, NT ? 2 : 0);
   }

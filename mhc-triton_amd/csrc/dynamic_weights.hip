@@ -44,11 +44,11 @@ struct MfmaPlan {
   int nK;               // chunks
   int64_t rows_per_wg;  // multiple of 32
   int ngr;              // row ranges
-  size_t part_bytes, packed_bytes;
+  size_t part_bytes;
 };
 
 static bool mfma_shape_ok(int64_t R, int64_t K) {
-  return R >= kMfmaMinRows && K > 0 && K % 16 == 0 && span_ok(32 * K, 2);
+  return R >= kMfmaMinRows && K > 0 && K % 16 == 0 && span_ok(32 * K, 2) && span_ok(K * kOut, 4);
 }
 
 static MfmaPlan mfma_plan(int64_t R, int64_t K) {
@@ -65,7 +65,6 @@ static MfmaPlan mfma_plan(int64_t R, int64_t K) {
   p.rows_per_wg = 32 * tpw;
   p.ngr = (int)((R + p.rows_per_wg - 1) / p.rows_per_wg);
   p.part_bytes = align256((size_t)R * p.nK * kPart * sizeof(float));
-  p.packed_bytes = (size_t)p.nsteps * 3 * 64 * 16;
   return p;
 }
 
@@ -81,7 +80,7 @@ extern "C" size_t mhc_dynamic_weights_workspace_bytes(int64_t R, int64_t K) {
   size_t need = align256((size_t)R * p.nK * kPart * sizeof(float));
   if (mfma_shape_ok(R, K)) {
     const MfmaPlan m = mfma_plan(R, K);
-    if (m.part_bytes + m.packed_bytes > need) need = m.part_bytes + m.packed_bytes;
+    if (m.part_bytes > need) need = m.part_bytes;
   }
   return need;
 }
@@ -109,12 +108,8 @@ extern "C" int mhc_dynamic_weights_forward(const void* x, int dtype_x, const flo
   if (dtype_x == MHC_DTYPE_BF16 && mfma_shape_ok(R, K) && aligned16(x)) {
     // bf16 rows in bulk: the projection on MFMA (HBM-bound instead of VALU-bound).
     const MfmaPlan m = mfma_plan(R, K);
-    u32x4* packed = (u32x4*)((char*)workspace + m.part_bytes);
-    dynw_pack_phi_kernel<><<<dim3((unsigned)((m.nsteps * 64 + kThreads - 1) / kThreads)), kThreads, 0, st>>>(
-        phi, packed, m.nsteps);
-    if (int rc = hip_status(hipGetLastError(), "dynamic_weights_forward pack launch")) return rc;
     dynw_mfma_kernel<><<<dim3((unsigned)m.ngr, (unsigned)m.nK), 64 * kMfmaWaves, 0, st>>>(
-        (const __bf16*)x, packed, part, R, K, m.nK, m.rows_per_wg);
+        (const __bf16*)x, phi, part, R, K, m.nK, m.rows_per_wg);
     if (int rc = hip_status(hipGetLastError(), "dynamic_weights_forward mfma launch")) return rc;
     nK = m.nK;
   } else {

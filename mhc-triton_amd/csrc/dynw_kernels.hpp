@@ -100,37 +100,12 @@ __global__ __launch_bounds__(kThreads) void dynw_partial_kernel(const TX* __rest
 // O(2^-27 |phi|), and all three are applied, so the projection keeps fp32
 // accuracy (two parts leave 2^-18, which the 20-round Sinkhorn of H_res
 // amplifies to ~1e-4 relative at K = 16384); columns 24..31 of B are zero.
-// dynw_pack_phi_kernel writes the fragments once per call in the exact order
-// the waves read them: packed[(s * 3 + h) * 64 + lane] (16 bytes) for K step
-// s (16 k values) and part h.
+// Each wave splits the phi values of its K slice into the three parts once,
+// in registers, as the kernel starts (a separate packing kernel took 5 us at
+// K = 16384).
 // ---------------------------------------------------------------------------
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
-
-template <int = 0>
-__global__ __launch_bounds__(kThreads) void dynw_pack_phi_kernel(const float* __restrict__ phi,
-                                                                 u32x4* __restrict__ packed, int64_t nsteps) {
-  const int64_t t = (int64_t)blockIdx.x * kThreads + threadIdx.x;  // (step, lane)
-  if (t >= nsteps * 64) return;
-  const int64_t s = t >> 6;
-  const int lane = (int)(t & 63);
-  const int col = lane & 31;
-  const int64_t k0 = s * 16 + (lane >> 5) * 8;
-  bf16x8 hi, mid, lo;
-#pragma unroll
-  for (int j = 0; j < 8; ++j) {
-    const float v = col < kOut ? phi[(k0 + j) * kOut + col] : 0.f;
-    const __bf16 h = (__bf16)v;
-    const float r1 = v - (float)h;  // exact in fp32
-    const __bf16 m = (__bf16)r1;
-    hi[j] = h;
-    mid[j] = m;
-    lo[j] = (__bf16)(r1 - (float)m);
-  }
-  packed[(s * 3) * 64 + lane] = __builtin_bit_cast(u32x4, hi);
-  packed[(s * 3 + 1) * 64 + lane] = __builtin_bit_cast(u32x4, mid);
-  packed[(s * 3 + 2) * 64 + lane] = __builtin_bit_cast(u32x4, lo);
-}
 
 // Forward projection on MFMA, K-slice form.  A workgroup of NW waves owns a
 // K chunk of NW * S steps and a range of rows; wave w owns the chunk's steps
@@ -152,7 +127,8 @@ __global__ __launch_bounds__(kThreads) void dynw_pack_phi_kernel(const float* __
 // squares [24], which the VALU forms from the A fragments alongside the MFMAs
 // (v_dot2_f32_bf16 would take a quarter of the instructions, but its sums are
 // not fp32-accurate: H_pre moved by 6e-3 relative at K = 4096).  Requires
-// K % 16 == 0, a 16-byte aligned x and rows_per_wg * K * 2 bytes under 2^31.
+// K % 16 == 0, a 16-byte aligned x, and rows_per_wg * K * 2 and K * 24 * 4
+// bytes under 2^31.
 constexpr int kMfmaWaves = 8;                             // waves per workgroup (2 per SIMD)
 constexpr int kMfmaSteps = 8;                             // 16-k steps per wave slice
 constexpr int kMfmaChunkSteps = kMfmaWaves * kMfmaSteps;  // steps per K chunk
@@ -161,7 +137,7 @@ constexpr int kMfmaRedPitch = 36;                         // floats per (wave, c
 
 template <int NW = kMfmaWaves, int S = kMfmaSteps>
 __global__ __launch_bounds__(64 * NW, 2) void dynw_mfma_kernel(const __bf16* __restrict__ x,
-                                                             const u32x4* __restrict__ packed,
+                                                             const float* __restrict__ phi,
                                                              float* __restrict__ part, int64_t R, int64_t K, int nK,
                                                              int64_t rows_per_wg) {
   constexpr int kThr = 64 * NW;
@@ -179,14 +155,26 @@ __global__ __launch_bounds__(64 * NW, 2) void dynw_mfma_kernel(const __bf16* __r
   const int64_t s0 = (int64_t)kc * (NW * S) + (int64_t)wave * S;  // the slice's first step
   int nvalid = (int)(nsteps - s0 < S ? nsteps - s0 : S);         // its steps inside K
   if (nvalid < 0) nvalid = 0;
-  u32x4 bf[S][3];
-#pragma unroll
-  for (int i = 0; i < S; ++i)
-#pragma unroll
-    for (int h = 0; h < 3; ++h) bf[i][h] = i < nvalid ? packed[((s0 + i) * 3 + h) * 64 + lane] : u32x4{0u, 0u, 0u, 0u};
   const int64_t rbeg = (int64_t)blockIdx.x * rows_per_wg;
   const int64_t rend = rbeg + rows_per_wg < R ? rbeg + rows_per_wg : R;
   if (rbeg >= rend) return;  // the whole workgroup
+  // The slice's phi values, one fp32 per (step, element) and lane: lane l,
+  // element j of step i -> phi[16 (s0 + i) + 8 (l / 32) + j][l % 32], through a
+  // buffer span so that steps past K and columns 24..31 read zeros with no branch.
+  const Span<float, true> phs(phi, K * kOut);
+  uint32_t pv[S][8];
+  {
+    const int col = lane & 31;
+    constexpr uint32_t kOobF32 = 0x20000000u;  // 2^31 bytes: past any span
+#pragma unroll
+    for (int i = 0; i < S; ++i)
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        const int64_t k = 16 * (s0 + i) + 8 * (lane >> 5) + j;
+        pv[i][j] = phs.load4<false>((i < nvalid && col < kOut) ? (uint32_t)(k * kOut + col) : kOobF32);
+      }
+  }
+  u32x4 bf[S][3];  // filled below, while the first tiles' loads are in flight
   const int64_t ntile = (rend - rbeg + 31) / 32;
   const Span<__bf16, true> xs(x + rbeg * K, (rend - rbeg) * K);
   const int lr = lane / L, lc = lane % L;
@@ -276,6 +264,26 @@ __global__ __launch_bounds__(64 * NW, 2) void dynw_mfma_kernel(const __bf16* __r
   aload(0, a[0]);
   __builtin_amdgcn_sched_barrier(0);  // tile 0's loads first: the first wait is for them alone
   aload(1, a[1]);
+  __builtin_amdgcn_sched_barrier(0);
+  // phi in three bf16 parts, phi = hi + mid + lo + O(2^-27 |phi|), while the
+  // first two tiles' loads are in flight
+#pragma unroll
+  for (int i = 0; i < S; ++i) {
+    bf16x8 hi, mid, lo;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const float v = __uint_as_float(pv[i][j]);
+      const __bf16 h = (__bf16)v;
+      const float r1 = v - (float)h;  // exact in fp32
+      const __bf16 m = (__bf16)r1;
+      hi[j] = h;
+      mid[j] = m;
+      lo[j] = (__bf16)(r1 - (float)m);
+    }
+    bf[i][0] = __builtin_bit_cast(u32x4, hi);
+    bf[i][1] = __builtin_bit_cast(u32x4, mid);
+    bf[i][2] = __builtin_bit_cast(u32x4, lo);
+  }
   for (int64_t t = 0; t < ntile; t += 2) {
     astage(a[0]);
     aload(t + 2, a[0]);
