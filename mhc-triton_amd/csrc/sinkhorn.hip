@@ -7,9 +7,11 @@
 // bf16/fp16); across the wave the accesses cover one contiguous span.  The
 // forward is VALU-bound at 20 rounds (40 VALU ops and 8 v_rcp per round in
 // the scaling-vector form of sk_forward); the backward keeps every round's
-// scaling vectors in registers for up to 20 rounds (sk_backward_scaled: 129 us
-// at 2^20 matrices, 20 rounds, against 175 us for the checkpointed reverse
-// sweep, which more rounds and the unaligned path keep).
+// scaling vectors in registers for up to 20 rounds and carries the adjoint in
+// scaled coordinates (sk_backward_scaled: 95-100 us at 2^20 matrices, 20
+// rounds, against 131 us for the explicit normalisation backward on the same
+// states and 175 us for the checkpointed reverse sweep, which more rounds and
+// the unaligned path keep).
 #include "sinkhorn.hpp"
 
 namespace mhc {

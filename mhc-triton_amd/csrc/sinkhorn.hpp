@@ -176,15 +176,20 @@ __device__ __forceinline__ void sk_backward(const float (&mat)[16], float (&d)[1
 // kept in registers instead of recomputed from checkpoints.  After t rounds
 // P = diag(u_t) P0 diag(v_t), with u_0 = v_0 = 1; the forward runs as in
 // sk_forward (carrying w = 1/u and z = 1/v) and keeps u_t and v_t, 8 floats
-// per round.  In round t the row normalisation maps u_t to u_{t+1} and the
-// column normalisation v_t to v_{t+1}, so
-//   row scale r_i = 1 / (rowsum_i + eps) = u_{t+1},i / u_t,i,  mr_ij = P0_ij u_{t+1},i v_t,j,
-//   col scale c_j = 1 / (colsum_j + eps) = v_{t+1},j / v_t,j,  mc_ij = P0_ij u_{t+1},i v_{t+1},j,
-// and the two normalisation backwards are those of sk_round_backward.  Per
-// round that is 40 VALU + 8 v_rcp forward and about 128 + 8 backward, against
-// 72 per recomputed round plus 144 per backward round for the checkpointed
-// sweep.  (Keeping w and z instead let the compiler reuse the forward's
-// reciprocals in the backward and hold both sets live: 303 VGPRs.)
+// per round.  Round t maps u_t to u_{t+1} = r u_t (r = 1 / (rowsum + eps)) and
+// then v_t to v_{t+1} = c v_t (c = 1 / (colsum + eps)).  The adjoint is
+// carried in scaled coordinates: the gradient dP of a state P0 u v^T is held
+// as g = dP * u v^T (elementwise).  The column normalisation backward,
+// dA_ij = c_j (dB_ij - sum_k dB_kj B_kj), then reads
+//   g_ij <- g_ij - u_{t+1},i v_{t+1},j sum_k g_kj P0_kj,
+// because B = P0 u_{t+1} v_{t+1}^T and c_j v_t,j = v_{t+1},j; and the row
+// normalisation backward, dP_ij = r_i (dA_ij - sum_l dA_il A_il),
+//   g_ij <- g_ij - v_t,j u_{t+1},i sum_l g_il P0_il,
+// because A = P0 u_{t+1} v_t^T and r_i u_t,i = u_{t+1},i.  A round is two
+// 16-term dot passes over g * P0 and two FMA updates, 72 VALU and no v_rcp
+// (the explicit form of sk_round_backward on the scaled state took about
+// 128 + 8 v_rcp); the forward is 40 VALU + 8 v_rcp per round.  g starts as
+// dP_T * u_T v_T^T and ends as dP0 (u_0 = v_0 = 1).
 template <int TMAX>
 __device__ __forceinline__ void sk_backward_scaled(const float (&mat)[16], float (&d)[16], int iters, float eps) {
   float p0[16];
@@ -222,34 +227,30 @@ __device__ __forceinline__ void sk_backward_scaled(const float (&mat)[16], float
   }
 #pragma unroll
   for (int t = TMAX - 1; t >= 0; --t) {
-    if (t < iters) {
-      float r[4], c[4], a[16];
-#pragma unroll
-      for (int k = 0; k < 4; ++k) {
-        r[k] = t == 0 ? U[1][k] : U[t + 1][k] * fast_rcp(U[t][k]);
-        c[k] = t == 0 ? V[1][k] : V[t + 1][k] * fast_rcp(V[t][k]);
-      }
+    if (t == iters - 1) {  // the last round: g = dP_T * u_T v_T^T
 #pragma unroll
       for (int i = 0; i < 4; ++i)
 #pragma unroll
-        for (int j = 0; j < 4; ++j) a[4 * i + j] = p0[4 * i + j] * U[t + 1][i];
-      // Column normalisation: dmr[:,j] = d[:,j] c_j - <d[:,j], mc[:,j]> c_j.
+        for (int j = 0; j < 4; ++j) d[4 * i + j] *= U[t + 1][i] * V[t + 1][j];
+    }
+    if (t < iters) {
+      // column normalisation of round t
+      float e[4];
 #pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const float dot =
-            (d[j] * a[j] + d[4 + j] * a[4 + j] + d[8 + j] * a[8 + j] + d[12 + j] * a[12 + j]) * V[t + 1][j];
-        const float dc = dot * c[j];
+      for (int j = 0; j < 4; ++j)
+        e[j] = (d[j] * p0[j] + d[4 + j] * p0[4 + j] + d[8 + j] * p0[8 + j] + d[12 + j] * p0[12 + j]) * V[t + 1][j];
 #pragma unroll
-        for (int i = 0; i < 4; ++i) d[4 * i + j] = __builtin_fmaf(d[4 * i + j], c[j], -dc);
-      }
-      // Row normalisation: dm[i,:] = dmr[i,:] r_i - <dmr[i,:], mr[i,:]> r_i.
+      for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) d[4 * i + j] = __builtin_fmaf(-U[t + 1][i], e[j], d[4 * i + j]);
+      // row normalisation of round t
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        const float dot = d[4 * i] * (a[4 * i] * V[t][0]) + d[4 * i + 1] * (a[4 * i + 1] * V[t][1]) +
-                          d[4 * i + 2] * (a[4 * i + 2] * V[t][2]) + d[4 * i + 3] * (a[4 * i + 3] * V[t][3]);
-        const float dr = dot * r[i];
+        const float f = (d[4 * i] * p0[4 * i] + d[4 * i + 1] * p0[4 * i + 1] + d[4 * i + 2] * p0[4 * i + 2] +
+                         d[4 * i + 3] * p0[4 * i + 3]) *
+                        U[t + 1][i];
 #pragma unroll
-        for (int j = 0; j < 4; ++j) d[4 * i + j] = __builtin_fmaf(d[4 * i + j], r[i], -dr);
+        for (int j = 0; j < 4; ++j) d[4 * i + j] = __builtin_fmaf(-V[t][j], f, d[4 * i + j]);
       }
     }
   }
