@@ -196,7 +196,10 @@ def test_add_residual_forward_backward(dtype, bo_dtype, shape):
                                         # one 16-k step (seven of the eight waves' slices past K)
                                         (65, 16, torch.bfloat16),
                                         # K % 16 = 8: the VALU projection forward, the MFMA backward
-                                        (100, 1000, torch.bfloat16)])
+                                        (100, 1000, torch.bfloat16),
+                                        # MFMA backward row chunks of 188 rows (two whole 64-row
+                                        # blocks and a partial one), eight chunk partials
+                                        (1500, 8192, torch.bfloat16)])
 def test_dynamic_weights_forward_backward(R, K, xdtype):
     import mhc
 
