@@ -10,8 +10,11 @@
 // scaling vectors in registers for up to 20 rounds and carries the adjoint in
 // scaled coordinates (sk_backward_scaled: 95-100 us at 2^20 matrices, 20
 // rounds, against 131 us for the explicit normalisation backward on the same
-// states and 175 us for the checkpointed reverse sweep, which more rounds and
-// the unaligned path keep).
+// states and 175 us for the checkpointed reverse sweep).  From 21 to 64
+// rounds it recomputes the vectors in 16-round segments from checkpoints
+// (sk_backward_segmented; fwd + bwd at 2^20 matrices: 190 against 255 us at
+// 21 rounds, 436 against 818 us at 64); more rounds and the unaligned path
+// keep the checkpointed sweep.
 #include "sinkhorn.hpp"
 
 namespace mhc {
@@ -52,6 +55,8 @@ __global__ __launch_bounds__(kThreads) void sinkhorn_fwd_kernel(const T* __restr
 }
 
 constexpr int kSkScaledMax = 20;  // rounds the scaling-vector backward keeps in registers
+constexpr int kSkSegRounds = 16;  // rounds per segment of the segmented backward
+constexpr int kSkSegs = 4;        // its segments: up to 64 rounds
 
 template <typename T, typename TD, bool VEC>
 __global__ __launch_bounds__(kThreads) void sinkhorn_bwd_kernel(const T* __restrict__ M, const TD* __restrict__ dP,
@@ -66,6 +71,8 @@ __global__ __launch_bounds__(kThreads) void sinkhorn_bwd_kernel(const T* __restr
   // does not depend on the checkpoint count.
   if (VEC && iters <= kSkScaledMax)
     sk_backward_scaled<kSkScaledMax>(m, d, iters, eps);
+  else if (VEC && iters <= kSkSegRounds * kSkSegs)
+    sk_backward_segmented<kSkSegRounds, kSkSegs>(m, d, iters, eps);
   else
     sk_backward<VEC ? 10 : 5>(m, d, iters, eps);
   store_mat<T, VEC>(dM + i * 16, d);

@@ -262,6 +262,116 @@ __device__ __forceinline__ void sk_backward_scaled(const float (&mat)[16], float
   }
 }
 
+// The scaled-coordinate gradient for more rounds than fit in registers:
+// NSEG segments of up to TSEG rounds.  The forward keeps only the carried
+// reciprocal vectors (w, z) at the start of each segment; the backward then
+// walks the segments from the last, recomputes the segment's u and v from its
+// checkpoint (the same rcp of the same carried values, so bit-identical to the
+// forward's) and runs sk_backward_scaled's round backward over them.  Every
+// round is recomputed once, against several times for the explicit-state
+// checkpoints of sk_backward.  Requires iters <= TSEG * NSEG.
+template <int TSEG, int NSEG>
+__device__ __forceinline__ void sk_backward_segmented(const float (&mat)[16], float (&d)[16], int iters, float eps) {
+  float p0[16];
+  uint32_t neg = 0u, zero = 0u;
+#pragma unroll
+  for (int k = 0; k < 16; ++k) {
+    p0[k] = __builtin_fabsf(mat[k]) + eps;
+    neg |= (mat[k] < 0.f ? 1u : 0u) << k;
+    zero |= (mat[k] == 0.f ? 1u : 0u) << k;
+  }
+  // one round of the carried iteration: w from v, u = rcp(w), z from u, v = rcp(z)
+  auto round = [&](float (&w)[4], float (&z)[4], const float (&v)[4], float (&u1)[4], float (&v1)[4]) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const float dot = p0[4 * i] * v[0] + p0[4 * i + 1] * v[1] + p0[4 * i + 2] * v[2] + p0[4 * i + 3] * v[3];
+      w[i] = __builtin_fmaf(eps, w[i], dot);
+      u1[i] = fast_rcp(w[i]);
+    }
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const float dot = u1[0] * p0[j] + u1[1] * p0[4 + j] + u1[2] * p0[8 + j] + u1[3] * p0[12 + j];
+      z[j] = __builtin_fmaf(eps, z[j], dot);
+      v1[j] = fast_rcp(z[j]);
+    }
+  };
+  float cw[NSEG][4], cz[NSEG][4];
+  {
+    float w[4] = {1.f, 1.f, 1.f, 1.f}, z[4] = {1.f, 1.f, 1.f, 1.f}, v[4] = {1.f, 1.f, 1.f, 1.f};
+#pragma unroll
+    for (int k = 0; k < NSEG; ++k) {
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        cw[k][q] = w[q];
+        cz[k][q] = z[q];
+      }
+      const int tend = iters < (k + 1) * TSEG ? iters : (k + 1) * TSEG;
+      for (int t = k * TSEG; t < tend; ++t) {
+        float u1[4], v1[4];
+        round(w, z, v, u1, v1);
+#pragma unroll
+        for (int q = 0; q < 4; ++q) v[q] = v1[q];
+      }
+    }
+    // g = dP_T * u_T v_T^T
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const float u = fast_rcp(w[i]);
+#pragma unroll
+      for (int j = 0; j < 4; ++j) d[4 * i + j] *= u * fast_rcp(z[j]);
+    }
+  }
+  for (int k = (iters + TSEG - 1) / TSEG - 1; k >= 0; --k) {
+    const int t0 = k * TSEG;
+    float U[TSEG + 1][4], V[TSEG + 1][4], w[4], z[4];
+#pragma unroll
+    for (int q = 0; q < 4; ++q) w[q] = z[q] = 1.f;
+#pragma unroll
+    for (int c = 0; c < NSEG; ++c)
+      if (c == k) {
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          w[q] = cw[c][q];
+          z[q] = cz[c][q];
+        }
+      }
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      U[0][q] = fast_rcp(w[q]);
+      V[0][q] = fast_rcp(z[q]);
+    }
+#pragma unroll
+    for (int tt = 0; tt < TSEG; ++tt)
+      if (t0 + tt < iters) round(w, z, V[tt], U[tt + 1], V[tt + 1]);
+#pragma unroll
+    for (int tt = TSEG - 1; tt >= 0; --tt) {
+      if (t0 + tt < iters) {
+        float e[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+          e[j] = (d[j] * p0[j] + d[4 + j] * p0[4 + j] + d[8 + j] * p0[8 + j] + d[12 + j] * p0[12 + j]) * V[tt + 1][j];
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+#pragma unroll
+          for (int j = 0; j < 4; ++j) d[4 * i + j] = __builtin_fmaf(-U[tt + 1][i], e[j], d[4 * i + j]);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const float f = (d[4 * i] * p0[4 * i] + d[4 * i + 1] * p0[4 * i + 1] + d[4 * i + 2] * p0[4 * i + 2] +
+                           d[4 * i + 3] * p0[4 * i + 3]) *
+                          U[tt + 1][i];
+#pragma unroll
+          for (int j = 0; j < 4; ++j) d[4 * i + j] = __builtin_fmaf(-V[tt][j], f, d[4 * i + j]);
+        }
+      }
+    }
+  }
+#pragma unroll
+  for (int e = 0; e < 16; ++e) {
+    const float sg = (zero >> e) & 1u ? 0.f : ((neg >> e) & 1u ? -1.f : 1.f);
+    d[e] *= sg;
+  }
+}
+
 // ---------------------------------------------------------------------------
 // 16-lane form, for the latency-bound per-row kernels (a handful of matrices,
 // one per batch row): one matrix is spread over 16 consecutive lanes, lane

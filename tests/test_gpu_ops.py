@@ -43,10 +43,11 @@ def test_sinkhorn_forward(dtype):
     assert rel_err(to_np(P), O.sinkhorn(to_np(M), 20, 1e-8)) < TOL[dtype]
 
 
-@pytest.mark.parametrize("iters", [0, 1, 7, 20, 21, 33])
+@pytest.mark.parametrize("iters", [0, 1, 7, 20, 21, 33, 64, 65])
 def test_sinkhorn_forward_backward_iters(iters):
     """Up to 20 rounds the aligned backward keeps every round's scaling vectors in registers;
-    beyond that, and on the unaligned path, it recomputes states from checkpoints.  Both forms
+    from 21 to 64 it recomputes them segment by segment (16 rounds each) from checkpoints; beyond
+    that, and on the unaligned path, it recomputes explicit states from checkpoints.  The forms
     are held to the oracle and to each other."""
     import mhc
 
