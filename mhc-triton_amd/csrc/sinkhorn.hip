@@ -13,8 +13,10 @@
 // states and 175 us for the checkpointed reverse sweep).  From 21 to 64
 // rounds it recomputes the vectors in 16-round segments from checkpoints
 // (sk_backward_segmented; fwd + bwd at 2^20 matrices: 190 against 255 us at
-// 21 rounds, 436 against 818 us at 64); more rounds and the unaligned path
-// keep the checkpointed sweep.
+// 21 rounds, 436 against 818 us at 64); past 64 rounds it keeps the
+// checkpointed sweep.  The unaligned (element-wise load) path runs the same
+// forms (fwd + bwd at 20 rounds: 130-134 against 241-245 us with the
+// checkpointed sweep it used before).
 #include "sinkhorn.hpp"
 
 namespace mhc {
@@ -66,12 +68,12 @@ __global__ __launch_bounds__(kThreads) void sinkhorn_bwd_kernel(const T* __restr
   float m[16], d[16];
   load_mat<T, VEC>(M + i * 16, m);
   load_mat<TD, VEC>(dP + i * 16, d);
-  // The element-wise loads of the unaligned path need more registers: there
-  // five checkpoints keep 3 waves per SIMD (ten would leave one).  The result
-  // does not depend on the checkpoint count.
-  if (VEC && iters <= kSkScaledMax)
+  // Past 64 rounds the explicit-state checkpoints: on the unaligned path five
+  // keep 3 waves per SIMD (its element-wise loads need more registers; ten
+  // would leave one).  The result does not depend on the checkpoint count.
+  if (iters <= kSkScaledMax)
     sk_backward_scaled<kSkScaledMax>(m, d, iters, eps);
-  else if (VEC && iters <= kSkSegRounds * kSkSegs)
+  else if (iters <= kSkSegRounds * kSkSegs)
     sk_backward_segmented<kSkSegRounds, kSkSegs>(m, d, iters, eps);
   else
     sk_backward<VEC ? 10 : 5>(m, d, iters, eps);

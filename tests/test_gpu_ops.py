@@ -45,10 +45,10 @@ def test_sinkhorn_forward(dtype):
 
 @pytest.mark.parametrize("iters", [0, 1, 7, 20, 21, 33, 64, 65])
 def test_sinkhorn_forward_backward_iters(iters):
-    """Up to 20 rounds the aligned backward keeps every round's scaling vectors in registers;
-    from 21 to 64 it recomputes them segment by segment (16 rounds each) from checkpoints; beyond
-    that, and on the unaligned path, it recomputes explicit states from checkpoints.  The forms
-    are held to the oracle and to each other."""
+    """Up to 20 rounds the backward keeps every round's scaling vectors in registers; from 21 to
+    64 it recomputes them segment by segment (16 rounds each) from checkpoints; beyond that it
+    recomputes explicit states from checkpoints.  Each is held to the oracle, and the 16-byte
+    load path to the element-wise one."""
     import mhc
 
     g = gen(1)
@@ -63,7 +63,7 @@ def test_sinkhorn_forward_backward_iters(iters):
     ref = O.sinkhorn_backward(to_np(M), to_np(dP), iters, 1e-8)
     assert rel_err(to_np(Ml.grad), ref) < 1e-4
     assert Ml.grad[0, 0, 0].item() == 0.0 and Ml.grad[7, 2, 1].item() == 0.0
-    # the same matrices at an offset of one element: the scalar path, checkpointed backward
+    # the same matrices at an offset of one element: the element-wise load path
     flat = torch.cat([torch.zeros(1, device=DEV), M.reshape(-1)]).requires_grad_(True)
     Mu = flat[1:].view(300, 4, 4)
     assert Mu.data_ptr() % 16 != 0
