@@ -281,7 +281,7 @@ __device__ __forceinline__ void sk_backward_segmented(const float (&mat)[16], fl
     zero |= (mat[k] == 0.f ? 1u : 0u) << k;
   }
   // one round of the carried iteration: w from v, u = rcp(w), z from u, v = rcp(z)
-  auto round = [&](float (&w)[4], float (&z)[4], const float (&v)[4], float (&u1)[4], float (&v1)[4]) {
+  auto sk_step = [&](float (&w)[4], float (&z)[4], const float (&v)[4], float (&u1)[4], float (&v1)[4]) {
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const float dot = p0[4 * i] * v[0] + p0[4 * i + 1] * v[1] + p0[4 * i + 2] * v[2] + p0[4 * i + 3] * v[3];
@@ -308,7 +308,7 @@ __device__ __forceinline__ void sk_backward_segmented(const float (&mat)[16], fl
       const int tend = iters < (k + 1) * TSEG ? iters : (k + 1) * TSEG;
       for (int t = k * TSEG; t < tend; ++t) {
         float u1[4], v1[4];
-        round(w, z, v, u1, v1);
+        sk_step(w, z, v, u1, v1);
 #pragma unroll
         for (int q = 0; q < 4; ++q) v[q] = v1[q];
       }
@@ -342,7 +342,7 @@ __device__ __forceinline__ void sk_backward_segmented(const float (&mat)[16], fl
     }
 #pragma unroll
     for (int tt = 0; tt < TSEG; ++tt)
-      if (t0 + tt < iters) round(w, z, V[tt], U[tt + 1], V[tt + 1]);
+      if (t0 + tt < iters) sk_step(w, z, V[tt], U[tt + 1], V[tt + 1]);
 #pragma unroll
     for (int tt = TSEG - 1; tt >= 0; --tt) {
       if (t0 + tt < iters) {
