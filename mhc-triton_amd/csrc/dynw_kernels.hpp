@@ -554,9 +554,12 @@ __global__ __launch_bounds__(kThreads) void dynw_bwd_rows_kernel(const float* __
 // With one row chunk grad_phi is written directly; otherwise each chunk
 // writes gphi_part[chunk][k][0:24] and dynw_gphi_reduce_kernel sums the
 // chunks in order.  The per-row record is the same for every thread of the
-// workgroup (scalar loads).  Workgroup (0, 0) also sums the per-row records
-// into grad_bias [24] and grad_alpha [3] (threads stride over rows, then a
-// fixed-order block sum).  launch_dynw_bwd_wide picks one-wave workgroups
+// workgroup (scalar loads).  With grad_bias or grad_alpha requested, the
+// launcher adds one column of workgroups, whose workgroup (last, 0) sums the
+// per-row records into grad_bias [24] and grad_alpha [3] (threads stride over
+// rows, then a fixed-order block sum) alongside the others instead of ahead
+// of its own columns; the rows' x loads are issued four at a time (at the
+// layer's R = 4: 4.8 against 7.2 us).  launch_dynw_bwd_wide picks one-wave workgroups
 // (kWideThreads = 64) when R <= 64: the work is then a few loads and ~50 FMAs
 // per k, so the pass is latency-bound and wants every CU busy -- at the
 // layer's R = 4, K = 16384, 256 one-wave workgroups take 3.1 us against 6.6 us
@@ -573,7 +576,9 @@ __global__ __launch_bounds__(NT) void dynw_bwd_wide_kernel(const TX* __restrict_
                                                                  float* __restrict__ gbias,
                                                                  float* __restrict__ galpha, int64_t R, int64_t K,
                                                                  int64_t RC, bool phi_vec) {
-  if (blockIdx.x == 0 && blockIdx.y == 0 && (gbias || galpha)) {
+  if ((gbias || galpha) && blockIdx.x == gridDim.x - 1) {
+    // the launcher's extra column of workgroups: (last, 0) sums the records, the rest have no work
+    if (blockIdx.y != 0) return;
     __shared__ float lds[4 * 27];
     float acc[27];
 #pragma unroll
@@ -590,6 +595,7 @@ __global__ __launch_bounds__(NT) void dynw_bwd_wide_kernel(const TX* __restrict_
 #pragma unroll
       for (int g = 0; g < 3; ++g) if (galpha) galpha[g] = acc[24 + g];
     }
+    return;
   }
   const int64_t k = (int64_t)blockIdx.x * NT + threadIdx.x;
   if (k >= K || (!gx && !gphi)) return;
@@ -599,16 +605,26 @@ __global__ __launch_bounds__(NT) void dynw_bwd_wide_kernel(const TX* __restrict_
   load_phi_row(phi, k, phi_vec, ph);
 #pragma unroll
   for (int j = 0; j < kOut; ++j) gp[j] = 0.f;
-  for (int64_t r = r_beg; r < r_end; ++r) {
-    const float* rb = rowbuf + r * kRow;
-    const float xv = to_f32(x[r * K + k]);
-    float v = rb[24] * xv;
+  // four rows at a time, their x loads issued together
+  for (int64_t r0 = r_beg; r0 < r_end; r0 += 4) {
+    float xq[4];
 #pragma unroll
-    for (int j = 0; j < kOut; ++j) {
-      v += rb[j] * ph[j];
-      gp[j] += xv * rb[j];
+    for (int q = 0; q < 4; ++q) xq[q] = r0 + q < r_end ? to_f32(x[(r0 + q) * K + k]) : 0.f;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      if (r0 + q < r_end) {
+        const int64_t r = r0 + q;
+        const float* rb = rowbuf + r * kRow;
+        const float xv = xq[q];
+        float v = rb[24] * xv;
+#pragma unroll
+        for (int j = 0; j < kOut; ++j) {
+          v += rb[j] * ph[j];
+          gp[j] += xv * rb[j];
+        }
+        if (gx) gx[r * K + k] = from_f32<TG>(v);
+      }
     }
-    if (gx) gx[r * K + k] = from_f32<TG>(v);
   }
   float* o = gphi_part ? gphi_part + ((int64_t)blockIdx.y * K + k) * kOut : gphi;
   if (o) {
@@ -622,11 +638,11 @@ inline hipError_t launch_dynw_bwd_wide(const TX* x, const float* phi, const floa
                                        float* gphi_part, float* gbias, float* galpha, int64_t R, int64_t K,
                                        int64_t RC, unsigned nR, bool phi_vec, hipStream_t st) {
   if (R <= kWideThreads) {
-    const unsigned ncol = K > 0 ? (unsigned)((K + kWideThreads - 1) / kWideThreads) : 1u;
+    const unsigned ncol = (K > 0 ? (unsigned)((K + kWideThreads - 1) / kWideThreads) : 1u) + (gbias || galpha ? 1u : 0u);
     dynw_bwd_wide_kernel<TX, TG, kWideThreads><<<dim3(ncol, nR), kWideThreads, 0, st>>>(
         x, phi, rowbuf, gx, gphi, gphi_part, gbias, galpha, R, K, RC, phi_vec);
   } else {
-    const unsigned ncol = K > 0 ? (unsigned)((K + kThreads - 1) / kThreads) : 1u;
+    const unsigned ncol = (K > 0 ? (unsigned)((K + kThreads - 1) / kThreads) : 1u) + (gbias || galpha ? 1u : 0u);
     dynw_bwd_wide_kernel<TX, TG, kThreads><<<dim3(ncol, nR), kThreads, 0, st>>>(
         x, phi, rowbuf, gx, gphi, gphi_part, gbias, galpha, R, K, RC, phi_vec);
   }
