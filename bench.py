@@ -18,7 +18,9 @@ accumulation.  Inputs are resident in HBM before the timed region.
 
 Printed: one JSON line (metric, value = tokens/s of the whole job, roofline of
 the dominant kernel measured with HIP events on the stream it runs on, the CPU
-baseline of the reference's PyTorch path timed on this host).
+baseline of the reference's PyTorch path timed on this host).  The default
+config3 run also times configs 4 and 5 (GPU legs only) and reports them under
+"workloads"; --no-workloads skips them.
 
 Workloads (reference benchmark shapes, src/mhc/module.py layer):
   config3  dim 4096 bf16, B=4 S=4096, dynamic fused weights (the headline)
@@ -87,6 +89,9 @@ def _parse():
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--workload", default="config3", choices=sorted(WORKLOADS))
+    ap.add_argument("--no-workloads", action="store_true",
+                    help="skip the GPU legs of configs 4 and 5 that the default (config3) run adds under "
+                         "'workloads'")
     ap.add_argument("--cpu-reps", type=int, default=3,
                     help="timed runs of the cpu_baseline leg at the workload's shape, after one warm-up "
                          "(0 disables it)")
@@ -502,6 +507,28 @@ def _gpu_leg(cfg, steps, warmup):
                 elem=H.element_size(), device=torch.cuda.get_device_name(dev))
 
 
+def _workload_summary(name, cfg, r) -> dict:
+    """The figures of one workload's GPU leg, in the units of the main line."""
+    B, S, D = cfg["B"], cfg["S"], cfg["D"]
+    T, e = B * S, r["elem"]
+    fu, bu = ALGO_UNITS[cfg["dynamic"]]
+    add_gbs = 9 * D * e * T / (r["add_ms"] * 1e-3) / 1e9
+    return {
+        "workload": f"{name}: HyperConnection layer fwd+bwd, dim={D}, num_streams=4, "
+                    f"{'dynamic fused' if cfg['dynamic'] else 'static'} weights, sinkhorn_iters=20",
+        "B": B, "S": S, "D": D, "dtype": cfg["dtype"],
+        "ms_per_step": round(r["ms"], 5),
+        "tokens_per_s": round(T / (r["ms"] * 1e-3), 1),
+        "layer_roofline": {"algorithmic_bytes_per_step": (fu + bu) * D * e * T,
+                           "frac": round((fu + bu) * D * e * T / (r["ms"] * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)},
+        "fwd_only": {"ms_per_step": round(r["fwd_ms"], 5), "tokens_per_s": round(T / (r["fwd_ms"] * 1e-3), 1),
+                     "frac": round(fu * D * e * T / (r["fwd_ms"] * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)},
+        "closure_forward": {"us": round(r["add_ms"] * 1e3, 1), "achieved_GBps": round(add_gbs, 1),
+                            "frac": round(add_gbs / HBM_PEAK_GBS, 4), "timed_launches": r["add_samples"],
+                            "traffic": MEASURED_TRAFFIC.get(name), "traffic_measured_at": TRAFFIC_COMMIT},
+    }
+
+
 def _cpu_leg(cfg, reps: int = 3, seq: int | None = None):
     """The reference's pure-PyTorch layer (restated in oracle/torch_path.py), on the host
     cores, at the workload's own shape (B, S, D): forward, and forward + autograd backward,
@@ -639,6 +666,15 @@ def main() -> int:
     _log(f"bench: gpu {r['ms']:.4f} ms/step (wall {r['wall_ms']:.4f}), fwd {r['fwd_ms']:.4f} ms, "
          f"H_new kernel {r['add_ms'] * 1e3:.1f} us")
 
+    # Configs 4 and 5 ride along with the default config-3 run (GPU legs only, about a second each).
+    workloads = {}
+    if args.workload == "config3" and not args.no_workloads:
+        for name in ("config4", "config5"):
+            wr = _gpu_leg(WORKLOADS[name], args.steps, args.warmup)
+            workloads[name] = _workload_summary(name, WORKLOADS[name], wr)
+            _log(f"bench: {name} {wr['ms']:.4f} ms/step, layer {workloads[name]['layer_roofline']['frac']:.4f} of "
+                 f"8 TB/s, H_new kernel {wr['add_ms'] * 1e3:.1f} us")
+
     cpu = None
     if args.cpu_reps > 0:
         _log("bench: cpu baseline ...")
@@ -694,6 +730,8 @@ def main() -> int:
         "device": r["device"],
         "cpu_baseline": cpu,
     }
+    if workloads:
+        out["workloads"] = workloads
     print(json.dumps(out), flush=True)
     return 0
 

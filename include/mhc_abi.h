@@ -248,6 +248,18 @@ int mhc_layer_mix_backward(const void* H, int dtype, const void* d_branch_input,
                            int64_t B, int64_t S, int64_t D,
                            void* workspace, size_t workspace_bytes, mhc_stream_t stream);
 
+/* dH of a layer whose weights w [B,24] come from the caller's own ops (the
+ * unfused dynamic path, module.py:141-163), with the sequence mean's share
+ * folded in:  dH[b,s,m,:] = H_pre[m] d_bi + sum_n H_res[n,m] dH_new[n]
+ *                          + grad_x[b, m*D:(m+1)*D] / S,
+ * where grad_x [B,4D] f32 is the gradient of x = H.mean(1).reshape(B, 4D)
+ * (module.py:123).  One pass, rounded once to dtype; replaces the mix
+ * backward's dH plus autograd's broadcast add of the mean's gradient.
+ * dH_new may be NULL (H_new received no gradient). */
+int mhc_layer_mix_dh(const void* d_branch_input, const void* dH_new, int dtype, const float* w,
+                     const float* grad_x, void* dH, int64_t B, int64_t S, int64_t D,
+                     mhc_stream_t stream);
+
 /* Layer closure forward (module.py:179-180 with H_residual recomputed):
  * H_new[n] = sum_m H_res[n,m] H[m] + H_post[n] bo, H_new in dtype_h. */
 int mhc_layer_add_forward(const void* H, int dtype_h, const void* branch_output, int dtype_bo,

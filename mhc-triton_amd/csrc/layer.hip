@@ -548,3 +548,17 @@ extern "C" int mhc_layer_mix_backward(const void* H, int dtype, const void* d_br
   reduce_split_kernel<20, 4><<<dim3((unsigned)B, 5), kRedThreads, 0, st>>>(part, dH_pre, dH_res, (int)nblk);
   return hip_status(hipGetLastError(), "layer mix backward reduce launch");
 }
+
+extern "C" int mhc_layer_mix_dh(const void* d_branch_input, const void* dH_new, int dtype, const float* w,
+                                const float* grad_x, void* dH, int64_t B, int64_t S, int64_t D,
+                                mhc_stream_t stream) {
+  if (int rc = check_bsd("layer_mix_dh", B, S, D)) return rc;
+  if (B * S * D == 0) return MHC_OK;
+  if (!d_branch_input || !w || !grad_x || !dH) {
+    set_error("layer_mix_dh: null pointer");
+    return MHC_ERR_ARG;
+  }
+  return MHC_DISPATCH_DTYPE(dtype, [&] {
+    return dh_dispatch<T>(d_branch_input, dH_new, grad_x, w, dH, B, S, D, (hipStream_t)stream);
+  });
+}

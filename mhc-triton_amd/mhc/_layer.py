@@ -186,6 +186,24 @@ def mix_backward(H, d_bi, dH_new, w, need_dH: bool = True):
     return dH, dpre, dres
 
 
+def mix_dh(d_bi, dH_new, w, grad_x, H_shape, h_dtype):
+    """mhc_layer_mix_dh: dH = H_pre d_bi + H_res^T dH_new + grad_x / S in one pass, in h_dtype.
+    d_bi / dH_new / grad_x may be None (no gradient reached them: zeros)."""
+    B, S, _, D = H_shape
+    dev = _lib.require_gpu(d_bi, dH_new, w, grad_x)
+    d_bi = torch.zeros(B, S, D, device=dev, dtype=h_dtype) if d_bi is None else d_bi.contiguous().to(h_dtype)
+    dH_new = None if dH_new is None else dH_new.contiguous().to(h_dtype)
+    grad_x = torch.zeros(B, 4 * D, device=dev, dtype=torch.float32) if grad_x is None else _f32(grad_x)
+    w = _f32(w)
+    dH = torch.empty(B, S, 4, D, device=dev, dtype=h_dtype)
+    lib = _lib.load()
+    with _lib.on_device(dev):
+        _lib.check(lib.mhc_layer_mix_dh(d_bi.data_ptr(), _lib.ptr(dH_new), _lib.dtype_code(dH), w.data_ptr(),
+                                        grad_x.data_ptr(), dH.data_ptr(), B, S, D, _lib.stream(dev)),
+                   "layer_mix_dh")
+    return dH
+
+
 def add_forward(H, branch_output, w):
     """mhc_layer_add_forward: H_new = H_res @ H + H_post * branch_output, in H's dtype."""
     B, S, _, D = H.shape
@@ -283,12 +301,51 @@ class _StaticLayer(torch.autograd.Function):
         return (dH, *_static_param_grads(params, gbias), None)
 
 
-class _GenericLayer(torch.autograd.Function):
-    """Node A for weights produced by torch ops (the unfused dynamic path,
-    module.py:141-163): (H, w) -> (branch_input, w, link, post_link), differentiable in w."""
+def _pool_links(H: torch.Tensor, x: torch.Tensor):
+    """The sequence-mean node's three gradient carriers: a view of H (-> dH_new), an unwritten
+    [B,S,D] stride-0 tensor in H's dtype (-> d_branch_input) and an unwritten [B,24] f32 one
+    (-> the weights w).  Node A reads none of their values."""
+    B, S, _, D = H.shape
+    return H.view_as(H), H.new_empty(()).expand(B, S, D), x.new_empty(()).expand(B, 24)
+
+
+class _PoolNode(torch.autograd.Function):
+    """Sequence mean of the unfused dynamic layer (module.py:123, 141-163), the node that writes dH:
+    H -> (x [B,4D] f32, H_link, bi_link, w_link).
+
+    x feeds the torch ops that make the weights; the links feed node A (``_GenericLayer``), whose
+    backward returns dH_new, d_branch_input and w as their gradients.  The engine runs this node's
+    backward after the weights' backward, so it holds grad_x too and writes
+    dH = H_pre d_bi + H_res^T dH_new + grad_x / S in one pass, rounded once (mhc_layer_mix_dh),
+    where a plain mean would have autograd add a broadcast grad_x / S into H.grad in two more."""
 
     @staticmethod
-    def forward(ctx, H, w_in):
+    def forward(ctx, H):
+        from ._kernels import mean_pool
+
+        x = mean_pool(H)
+        ctx.shape = H.shape
+        ctx.h_dtype = H.dtype
+        ctx.set_materialize_grads(False)
+        return (x, *_pool_links(H, x))
+
+    @staticmethod
+    def backward(ctx, gx, dH_new, d_bi, w):
+        if w is None:  # node A's backward did not run in this call, so nothing reaches H
+            return None
+        return mix_dh(d_bi, dH_new, w, gx, ctx.shape, ctx.h_dtype)
+
+
+class _GenericLayer(torch.autograd.Function):
+    """Node A for weights produced by torch ops (the unfused dynamic path, module.py:141-163):
+    (H_link, w, bi_link, w_link) -> (branch_input, w, link, post_link), differentiable in w.
+
+    H_link, bi_link and w_link come from ``_PoolNode``.  The backward runs the reductions only
+    (dH_pre, dH_res) and hands dH_new, d_branch_input and w to the pool node as the links'
+    gradients; that node writes dH once grad_x is known."""
+
+    @staticmethod
+    def forward(ctx, H, w_in, bi_link, w_link):
         w = _f32(w_in)
         bi = branch_input(H, w)
         ctx.save_for_backward(H, w)
@@ -299,11 +356,13 @@ class _GenericLayer(torch.autograd.Function):
     @staticmethod
     def backward(ctx, d_bi, d_w, d_link, d_post):
         H, w = ctx.saved_tensors
-        dH, dpre, dres = mix_backward(H, d_bi, d_link, w, need_dH=ctx.needs_input_grad[0])
+        _, dpre, dres = mix_backward(H, d_bi, d_link, w, need_dH=False)
         gw = torch.cat([dpre, torch.zeros_like(dpre) if d_post is None else d_post, dres], dim=1)
         if d_w is not None:
             gw = gw + d_w
-        return dH, gw.to(ctx.w_dtype)
+        to_pool = ctx.needs_input_grad[0]
+        return ((d_link if to_pool else None), gw.to(ctx.w_dtype), (d_bi if to_pool else None),
+                (w if to_pool else None))
 
 
 class _LayerAdd(torch.autograd.Function):

@@ -56,6 +56,7 @@ _SIGNATURES = {
     "mhc_layer_static_forward": (_I, [_P, _I, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I, _P]),
     "mhc_layer_branch_input": (_I, [_P, _I, _P, _P, _I64, _I64, _I64, _P]),
     "mhc_layer_mix_backward": (_I, [_P, _I, _P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _P, _SZ, _P]),
+    "mhc_layer_mix_dh": (_I, [_P, _P, _I, _P, _P, _P, _I64, _I64, _I64, _P]),
     "mhc_layer_add_forward": (_I, [_P, _I, _P, _I, _P, _P, _I64, _I64, _I64, _P]),
     "mhc_layer_add_backward": (_I, [_P, _I, _P, _I, _P, _P, _P, _I64, _I64, _I64, _P, _SZ, _P]),
     "mhc_layer_dynamic_backward": (

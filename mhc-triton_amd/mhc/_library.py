@@ -338,6 +338,32 @@ def _(H, d_bi, dH_new, w):
     return H.new_empty(H.shape), _f32_like(H, B, 4), _f32_like(H, B, 16)
 
 
+@_op("layer_mix_reduce")
+def layer_mix_reduce(H: Tensor, d_bi: Optional[Tensor], dH_new: Optional[Tensor], w: Tensor) -> Tuple[Tensor, Tensor]:
+    """(dH_pre [B,4] f32, dH_res [B,16] f32): the reductions of layer_mix_backward without dH, on
+    the same reduction-only pass as the eager layer."""
+    _, dpre, dres = _l.mix_backward(H, d_bi, dH_new, w, need_dH=False)
+    return dpre, dres
+
+
+@layer_mix_reduce.register_fake
+def _(H, d_bi, dH_new, w):
+    B = H.shape[0]
+    return _f32_like(H, B, 4), _f32_like(H, B, 16)
+
+
+@_op("layer_mix_dh")
+def layer_mix_dh(d_bi: Optional[Tensor], dH_new: Optional[Tensor], w: Tensor, grad_x: Optional[Tensor],
+                 H: Tensor) -> Tensor:
+    """dH = H_pre d_bi + H_res^T dH_new + grad_x / S in H's dtype (H gives shape and dtype only)."""
+    return _l.mix_dh(d_bi, dH_new, w, grad_x, H.shape, H.dtype)
+
+
+@layer_mix_dh.register_fake
+def _(d_bi, dH_new, w, grad_x, H):
+    return H.new_empty(H.shape)
+
+
 @_op("layer_add_forward")
 def layer_add_forward(H: Tensor, branch_output: Tensor, w: Tensor) -> Tensor:
     return _l.add_forward(H, branch_output, w)
@@ -359,6 +385,21 @@ def _(dH_new, branch_output, w):
     return branch_output.new_empty(branch_output.shape), _f32_like(dH_new, dH_new.shape[0], 4)
 
 
+def snapshot_links(H: Tensor, w: Tensor):
+    """The closure's gradient carriers in traced code: a snapshot of H (-> dH_new) and an
+    unwritten [B, 4] tensor (-> dH_post).
+
+    Eager mode passes a view of H and raises if H's version counter moved before the closure
+    runs.  Traced code cannot guard on a version counter (dynamo makes it a data-dependent
+    value), and under functionalization a view would see an in-place change of H made between
+    forward and the closure call.  The snapshot keeps the reference's semantics, where the
+    closure holds H_residual computed at forward time (reference src/mhc/module.py:177-180).
+    With the closure in the same graph inductor drops the copy (H unchanged) or orders the
+    closure's read before the deferred write-back (H changed in place); a closure called
+    outside the compiled region reads a materialised copy."""
+    return H.clone(), w.new_empty((w.shape[0], 4))
+
+
 class DynamicLayer(torch.autograd.Function):
     """Node A, dynamic fused weights: H -> (branch_input, w, link, post_link)."""
 
@@ -371,7 +412,7 @@ class DynamicLayer(torch.autograd.Function):
         ctx.iters = iters
         ctx.eps = eps
         ctx.set_materialize_grads(False)
-        return (bi, w, *_l._links(H, w))
+        return (bi, w, *snapshot_links(H, w))
 
     @staticmethod
     def backward(ctx, d_bi, d_w, d_link, d_post):
@@ -391,7 +432,7 @@ class StaticLayer(torch.autograd.Function):
         ctx.save_for_backward(H, w, *params)
         ctx.iters = iters
         ctx.set_materialize_grads(False)
-        return (bi, w, *_l._links(H, w))
+        return (bi, w, *snapshot_links(H, w))
 
     @staticmethod
     def backward(ctx, d_bi, d_w, d_link, d_post):
@@ -400,27 +441,47 @@ class StaticLayer(torch.autograd.Function):
         return (dH, *_l._static_param_grads(params, gbias), None)
 
 
-class GenericLayer(torch.autograd.Function):
-    """Node A for weights produced by torch ops (the unfused dynamic path):
-    (H, w) -> (branch_input, w, link, post_link)."""
+class PoolNode(torch.autograd.Function):
+    """Sequence mean of the unfused dynamic layer, the node that writes dH:
+    H -> (x [B,4D] f32, H_link, bi_link, w_link); the traced form of ``_layer._PoolNode``."""
 
     @staticmethod
-    def forward(ctx, H, w_in):
+    def forward(ctx, H):
+        x = torch.ops.mhc.mean_pool(H)
+        ctx.save_for_backward(H)
+        ctx.set_materialize_grads(False)
+        return (x, *_l._pool_links(H, x))
+
+    @staticmethod
+    def backward(ctx, gx, dH_new, d_bi, w):
+        H, = ctx.saved_tensors
+        if w is None:
+            return None
+        return torch.ops.mhc.layer_mix_dh(d_bi, dH_new, w, gx, H)
+
+
+class GenericLayer(torch.autograd.Function):
+    """Node A for weights produced by torch ops (the unfused dynamic path):
+    (H_link, w, bi_link, w_link) -> (branch_input, w, link, post_link); the traced form of
+    ``_layer._GenericLayer``."""
+
+    @staticmethod
+    def forward(ctx, H, w_in, bi_link, w_link):
         w = w_in.float()
         bi = torch.ops.mhc.layer_branch_input(H, w)
         ctx.save_for_backward(H, w)
         ctx.w_dtype = w_in.dtype
         ctx.set_materialize_grads(False)
-        return (bi, w.clone() if w is w_in else w, *_l._links(H, w))
+        return (bi, w.clone() if w is w_in else w, *snapshot_links(H, w))
 
     @staticmethod
     def backward(ctx, d_bi, d_w, d_link, d_post):
         H, w = ctx.saved_tensors
-        dH, dpre, dres = torch.ops.mhc.layer_mix_backward(H, d_bi, d_link, w)
+        dpre, dres = torch.ops.mhc.layer_mix_reduce(H, d_bi, d_link, w)
         gw = torch.cat([dpre, torch.zeros_like(dpre) if d_post is None else d_post, dres], dim=1)
         if d_w is not None:
             gw = gw + d_w
-        return dH, gw.to(ctx.w_dtype)
+        return d_link, gw.to(ctx.w_dtype), d_bi, w
 
 
 class LayerAdd(torch.autograd.Function):

@@ -15,7 +15,7 @@ import torch.nn as nn
 
 from . import _layer, _library
 from ._kernels import mean_pool
-from .ops import fused_dynamic_weights, sinkhorn_knopp
+from .ops import fused_add_residual, fused_dynamic_weights, fused_stream_mix, sinkhorn_knopp
 
 
 class HyperConnection(nn.Module):
@@ -96,12 +96,16 @@ class HyperConnection(nn.Module):
             raise ValueError(f"H must be (batch, seq, {self.num_streams}, {self.dim}), got {tuple(H.shape)}")
 
     def _unfused_weights(self, H: torch.Tensor, traced: bool = False) -> torch.Tensor:
-        """Packed weights [B,24] of the unfused dynamic path (reference
-        src/mhc/module.py:141-163): RMS-normalised mean, three Linears, sigmoid
-        (no x2 on H_post), normalisation with 1e-8 and Sinkhorn with eps 1e-8."""
-        B = H.shape[0]
-        n = self.num_streams
+        """Packed weights [B,24] of the unfused dynamic path from H (mean-pool included)."""
         pooled = torch.ops.mhc.mean_pool(H) if traced else _MeanPool.apply(H)
+        return self._unfused_weights_from(pooled, traced)
+
+    def _unfused_weights_from(self, pooled: torch.Tensor, traced: bool = False) -> torch.Tensor:
+        """Packed weights [B,24] of the unfused dynamic path (reference src/mhc/module.py:141-163)
+        from the sequence mean x [B,4D]: RMS-normalised x, three Linears, sigmoid (no x2 on
+        H_post), normalisation with 1e-8 and Sinkhorn with eps 1e-8."""
+        B = pooled.shape[0]
+        n = self.num_streams
         x = pooled.to(self.W_pre.weight.dtype)
         rms = torch.sqrt((x * x).mean(dim=-1, keepdim=True) + self.eps)
         x = x / rms
@@ -122,10 +126,11 @@ class HyperConnection(nn.Module):
         """(H_post [B,4], H_pre [B,4], H_res [B,4,4]), fp32 and differentiable, in the order
         of the reference's ``_compute_weights`` (reference src/mhc/module.py:103-163).
 
-        ``forward`` does not call this: the layer kernels derive the same weights inside
-        the fused path.  It serves callers that inspect or log the mixing weights, on the
-        same HIP ops (mean-pool, ``fused_dynamic_weights``, ``sinkhorn_knopp``).  The
-        mean-pool is taken in fp32, as in ``forward``.
+        ``forward`` derives the same weights inside the layer kernels and calls this method
+        only when a subclass overrides it (then it composes the reference's way, see
+        ``forward``).  It serves callers that inspect or log the mixing weights, on the same
+        HIP ops (mean-pool, ``fused_dynamic_weights``, ``sinkhorn_knopp``).  The mean-pool is
+        taken in fp32, as in ``forward``.
         """
         self._check_input(H)
         B = H.shape[0]
@@ -151,15 +156,26 @@ class HyperConnection(nn.Module):
         """H (batch, seq, 4, dim) -> (branch_input (batch, seq, dim), add_residual).
 
         ``add_residual`` recomputes ``H_res @ H`` from ``H`` instead of keeping ``H_residual``
-        (the reference's closure captures it, module.py:177-180).  It therefore raises if ``H``
-        was modified in place between ``forward`` and the call, where the reference would still
-        see the old values.  A strided ``H`` is made contiguous once, here, and that copy serves
-        the forward, the closure and the backward.
+        (the reference's closure captures it, module.py:177-180).  In eager mode it therefore
+        raises if ``H`` was modified in place between ``forward`` and the call, where the
+        reference would still see the old values.  The check reads ``H``'s version counter,
+        which every view of one storage shares: an in-place write to another slice of a buffer
+        that ``H`` is a slice of also raises (pass a clone of the slice to avoid that).  Under
+        torch.compile the closure reads a snapshot of ``H`` instead (the reference's
+        semantics; inductor drops the copy when the closure runs in the same graph).  A strided
+        ``H`` is made contiguous once, here, and that copy serves the forward, the closure and
+        the backward.
+
+        A subclass that overrides ``_compute_weights`` gets the reference's composition on the
+        HIP ops: its weights, ``fused_stream_mix`` and a closure over ``H_residual`` that calls
+        ``fused_add_residual`` (module.py:165-182).
         """
         self._check_input(H)
+        if type(self)._compute_weights is not HyperConnection._compute_weights:
+            return self._forward_composed(H)
+        H = H.contiguous()
         if torch.compiler.is_compiling():
             return self._forward_traced(H)
-        H = H.contiguous()
         version = H._version
         if not self.dynamic:
             bi, w, link, post_link = _layer._StaticLayer.apply(H, self.H_pre_base, self.H_post_base,
@@ -169,20 +185,23 @@ class HyperConnection(nn.Module):
                                                                 self.H_res_base, self.alpha_pre, self.alpha_post,
                                                                 self.alpha_res, self.sinkhorn_iters, self.eps)
         else:
-            bi, w, link, post_link = _layer._GenericLayer.apply(H, self._unfused_weights(H))
+            x, h_link, bi_link, w_link = _layer._PoolNode.apply(H)
+            bi, w, link, post_link = _layer._GenericLayer.apply(h_link, self._unfused_weights_from(x), bi_link,
+                                                                w_link)
 
         def add_residual(branch_output: torch.Tensor) -> torch.Tensor:
             if H._version != version:
                 raise RuntimeError(
                     "HyperConnection: H was modified in place after forward(H); add_residual recomputes "
-                    "H_res @ H from H and would mix the modified values. Clone H before modifying it.")
+                    "H_res @ H from H and would mix the modified values. Clone H before modifying it "
+                    "(the version counter is shared by every view of H's storage).")
             return _layer._LayerAdd.apply(link, branch_output, w, post_link)
 
         return bi, add_residual
 
     def _forward_traced(self, H: torch.Tensor):
-        """The same two nodes as ``forward``, on the torch.library ops, with the closure's
-        gradients passed to node A through a link output instead of a side channel."""
+        """The same two nodes as ``forward``, on the torch.library ops; the closure reads a
+        snapshot of the (contiguous) H."""
         if not self.dynamic:
             bi, w, link, post_link = _library.StaticLayer.apply(H, self.H_pre_base, self.H_post_base,
                                                                 self.H_res_base, self.sinkhorn_iters)
@@ -191,12 +210,26 @@ class HyperConnection(nn.Module):
                                                                  self.H_res_base, self.alpha_pre, self.alpha_post,
                                                                  self.alpha_res, self.sinkhorn_iters, self.eps)
         else:
-            bi, w, link, post_link = _library.GenericLayer.apply(H, self._unfused_weights(H, traced=True))
+            x, h_link, bi_link, w_link = _library.PoolNode.apply(H)
+            bi, w, link, post_link = _library.GenericLayer.apply(h_link, self._unfused_weights_from(x, True),
+                                                                 bi_link, w_link)
 
         def add_residual(branch_output: torch.Tensor) -> torch.Tensor:
             return _library.LayerAdd.apply(link, branch_output, w, post_link)
 
         return bi, add_residual
+
+    def _forward_composed(self, H: torch.Tensor):
+        """The reference's forward (module.py:165-182) on the HIP ops, for subclasses that
+        override ``_compute_weights``: the override's (H_post, H_pre, H_res), then
+        ``fused_stream_mix``, and a closure over ``H_residual`` calling ``fused_add_residual``."""
+        H_post, H_pre, H_res = self._compute_weights(H)
+        branch_input, H_residual = fused_stream_mix(H.contiguous(), H_pre, H_res)
+
+        def add_residual(branch_output: torch.Tensor) -> torch.Tensor:
+            return fused_add_residual(H_residual, branch_output, H_post)
+
+        return branch_input, add_residual
 
     def extra_repr(self) -> str:
         return (

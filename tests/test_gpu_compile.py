@@ -99,7 +99,7 @@ def test_compiled_layer_step_matches_oracle_and_eager(dynamic, fused, dtype, bac
     """bi, add = hc(H); H_new = add(bo) with bo an independent leaf, compiled (fullgraph) with
     aot_eager and with the default inductor backend: bit-identical to eager, and within the
     stated tolerances of the float64 oracle layer (fp32: 1e-5 forward, 1e-4 gradients; bf16:
-    2e-2 outputs, 1e-3 parameter gradients)."""
+    2e-2 outputs, 1e-4 parameter gradients)."""
     hc, H, _, gHn, gbi = _layer_case(dynamic, fused, dtype)
     g = torch.Generator().manual_seed(7)
     bo = torch.randn(gbi.shape, generator=g).to(dtype).to(DEV)
@@ -130,7 +130,8 @@ def test_compiled_layer_step_matches_oracle_and_eager(dynamic, fused, dtype, bac
     obi, oHn, cache = O.layer_forward(p, to_np(H), to_np(bo), dynamic, fused or not dynamic, hc.sinkhorn_iters,
                                       hc.eps)
     og = {k.replace(".weight", ""): v for k, v in O.layer_backward(p, cache, to_np(gHn), to_np(gbi)).items()}
-    ftol, gtol, ptol = (1e-5, 1e-4, 1e-4) if dtype == torch.float32 else (2e-2, 2e-2, 1e-3)
+    ftol, gtol = (1e-5, 1e-4) if dtype == torch.float32 else (2e-2, 2e-2)
+    ptol = 1e-4
     assert rel_err(to_np(compiled["bi"]), obi) < ftol and rel_err(to_np(compiled["H_new"]), oHn) < ftol
     assert rel_err(to_np(compiled["H"]), og["H"]) < gtol and rel_err(to_np(compiled["bo"]), og["bo"]) < gtol
     for n in p:
@@ -156,6 +157,71 @@ def test_compiled_layer_with_dynamic_shapes():
         case = (H[:, :S].contiguous(), W, gHn[:, :S].contiguous(), gbi[:, :S].contiguous())
         _assert_identical(_run(step, hc, *case, 1), _run(step_c, hc, *case, 1))
     assert counters["stats"]["unique_graphs"] == 1
+
+
+@pytest.mark.parametrize("backend", ["aot_eager", "inductor"])
+@pytest.mark.parametrize("dynamic,fused", [(True, True), (False, True), (True, False)])
+def test_compiled_layer_with_strided_h(dynamic, fused, backend):
+    """A strided H under torch.compile: the traced forward makes it contiguous once; outputs and
+    gradients (returned in H's own strides) match eager bit for bit and the float64 oracle."""
+    hc, H, _, gHn, gbi = _layer_case(dynamic, fused, torch.float32, S=40, D=128)
+    bo = torch.randn(gbi.shape, generator=torch.Generator().manual_seed(9)).to(DEV)
+    Ht = H.permute(0, 1, 3, 2).contiguous().permute(0, 1, 3, 2)
+    assert not Ht.is_contiguous() and torch.equal(Ht, H)
+
+    def step(Hl, bol):
+        bi, add = hc(Hl)
+        return bi, add(bol)
+
+    def run(f):
+        hc.zero_grad(set_to_none=True)
+        Hl, bol = Ht.detach().requires_grad_(True), bo.clone().requires_grad_(True)
+        bi, Hn = f(Hl, bol)
+        torch.autograd.backward([bi, Hn], [gbi, gHn])
+        assert Hl.grad.shape == Hl.shape
+        out = {"bi": bi.detach(), "H_new": Hn.detach(), "H": Hl.grad.contiguous(), "bo": bol.grad}
+        out.update({n.replace(".weight", ""): p.grad for n, p in hc.named_parameters()})
+        return out
+
+    eager = run(step)
+    compiled = run(_compile(step, backend=backend))
+    if backend == "inductor" and not fused:
+        for k in eager:
+            assert rel_err(to_np(compiled[k]), to_np(eager[k])) < 1e-5, k
+    else:
+        _assert_identical(eager, compiled)
+    p = {n.replace(".weight", ""): to_np(v) for n, v in hc.named_parameters()}
+    obi, oHn, cache = O.layer_forward(p, to_np(H), to_np(bo), dynamic, fused or not dynamic, hc.sinkhorn_iters,
+                                      hc.eps)
+    og = {k.replace(".weight", ""): v for k, v in O.layer_backward(p, cache, to_np(gHn), to_np(gbi)).items()}
+    assert rel_err(to_np(compiled["bi"]), obi) < 1e-5 and rel_err(to_np(compiled["H_new"]), oHn) < 1e-5
+    assert rel_err(to_np(compiled["H"]), og["H"]) < 1e-4 and rel_err(to_np(compiled["bo"]), og["bo"]) < 1e-4
+    for n in p:
+        assert rel_err(to_np(compiled[n]).reshape(np.shape(og[n])), og[n]) < 1e-4, n
+
+
+@pytest.mark.parametrize("backend", ["aot_eager", "inductor"])
+@pytest.mark.parametrize("dynamic,fused", [(True, True), (False, True), (True, False)])
+def test_compiled_closure_reads_h_as_it_was_at_forward(dynamic, fused, backend):
+    """H changed in place between forward and the closure call, inside a compiled function: the
+    closure mixes H as it was at forward time (the reference's closure holds H_residual,
+    module.py:177-180), and the change itself still reaches H.  Eager raises instead; traced code
+    cannot read a version counter, so the traced layer takes a snapshot of H."""
+    hc, H, _, _, gbi = _layer_case(dynamic, fused, torch.float32, S=32, D=128)
+    bo = torch.randn(gbi.shape, generator=torch.Generator().manual_seed(11)).to(DEV)
+
+    def step(Hm, bol):
+        bi, add = hc(Hm)
+        Hm.mul_(2.0)
+        return bi, add(bol)
+
+    Hm = H.clone()
+    with torch.no_grad():
+        bi, Hn = _compile(step, backend=backend)(Hm, bo)
+    assert torch.equal(Hm, 2.0 * H)
+    obi, oHn, _ = O.layer_forward({n.replace(".weight", ""): to_np(v) for n, v in hc.named_parameters()},
+                                  to_np(H), to_np(bo), dynamic, fused or not dynamic, hc.sinkhorn_iters, hc.eps)
+    assert rel_err(to_np(bi), obi) < 1e-5 and rel_err(to_np(Hn), oHn) < 1e-5
 
 
 def test_compiled_public_ops_match_eager_bitwise():
@@ -260,6 +326,10 @@ def _opcheck_cases():
         ("layer_static_backward", (H, bi, H, dpost, *base, wS, 20)),
         ("layer_branch_input", (H, wL)),
         ("layer_mix_backward", (H, bi, H, wL)),
+        ("layer_mix_reduce", (H, bi, H, wL)),
+        ("layer_mix_reduce", (H, None, None, wL)),
+        ("layer_mix_dh", (bi, H, wL, xL, H)),
+        ("layer_mix_dh", (None, None, wL, None, H)),
         ("layer_add_forward", (H, bo, wL)),
         ("layer_add_backward", (H, bo, wL)),
         ("stream_expand", (rg(bo.float()), 0.5, torch.bfloat16)),
@@ -268,7 +338,7 @@ def _opcheck_cases():
     return _CASES
 
 
-N_CASES = 20
+N_CASES = 24
 
 
 def test_opcheck_covers_every_registered_op():

@@ -3,14 +3,15 @@
 
 What is checked, per config:
 * the dynamic (or static) weights: the oracle computes them from the sequence
-  mean of H (taken by torch in fp32 on the GPU, a [B, 4D] result) and the
+  mean of H (taken by torch in float64 on the GPU, a [B, 4D] result) and the
   module parameters;
 * branch_input, H_new, dH and d branch_output: against torch fp32 arithmetic
   on the GPU with the oracle's weights (normwise relative error <= 2e-2, the
   bf16/fp16 output tolerance);
-* every parameter gradient: the oracle's weight backward fed torch fp32
-  reductions of the upstream gradients (dH_pre = sum d_bi * H[n],
-  dH_res = sum dH_new[n] * H[m], dH_post = sum dH_new[n] * bo), <= 1e-3;
+* every parameter gradient: the oracle's weight backward fed float64
+  reductions of the upstream gradients, taken on the GPU (dH_pre = sum d_bi * H[n],
+  dH_res = sum dH_new[n] * H[m], dH_post = sum dH_new[n] * bo over all S * D
+  terms) and the float64 sequence mean, <= 1e-4 (the fp32-gradient tolerance);
 * branch_input, H_new, d branch_output and dH once more, against the float64
   value of each expression from the layer's own fp32 weights, rounded once to
   the bf16 / fp16 output: within one unit in the last place, and bit-identical
@@ -25,7 +26,7 @@ import torch
 
 from helpers import rel_err, to_np
 from oracle import mhc_oracle as O
-from test_gpu_rounding import check_layer_rounding
+from test_gpu_rounding import _red, _red44, check_layer_rounding
 
 pytestmark = pytest.mark.gpu
 
@@ -66,7 +67,7 @@ def test_full_size_layer(name):
     p = {n: to_np(v) for n, v in hc.named_parameters()}
     Hf = H.float()
     if c["dynamic"]:
-        x = to_np(Hf.mean(dim=1).reshape(B, 4 * D))
+        x = to_np(H.double().mean(dim=1).reshape(B, 4 * D))
         bias = np.concatenate([p["H_pre_base"], p["H_post_base"], p["H_res_base"].reshape(16)])
         al = [float(p[k][0]) for k in ("alpha_pre", "alpha_post", "alpha_res")]
         H_pre, H_post, H_res = O.dynamic_weights(x, p["phi"], bias, *al, 20, 1e-6)
@@ -86,12 +87,13 @@ def test_full_size_layer(name):
     assert rel_err(to_np(H_new), to_np(hn_ref)) < 2e-2
     del hn_ref
 
-    # upstream reductions in fp32 (torch), weight backward in the oracle
+    # upstream reductions in float64 on the GPU, weight backward in the oracle
     dbf, dnf = dbi.float(), dHn.float()
-    dpre = to_np((dbf[:, :, None, :] * Hf).sum(dim=(1, 3)))
-    dres = to_np(torch.stack([torch.stack([(dnf[:, :, n] * Hf[:, :, m]).sum(dim=(1, 2)) for m in range(4)], -1)
-                              for n in range(4)], 1))
-    dpost = to_np((dnf * bo.float()[:, :, None, :]).sum(dim=(1, 3)))
+    H64 = H.double()
+    dpre = to_np(_red(dbi.double(), H64))
+    dres = to_np(_red44(dHn.double(), H64))
+    del H64
+    dpost = to_np(_red(bo.double(), dHn.double()))
     if c["dynamic"]:
         gx, gphi, gbias, ga = O.dynamic_weights_backward(x, p["phi"], bias, *al, dpre, dpost, dres, 20, 1e-6)
         ref = {"phi": gphi, "H_pre_base": gbias[0:4], "H_post_base": gbias[4:8],
@@ -102,8 +104,10 @@ def test_full_size_layer(name):
                                                dres, 20)
         ref = {"H_pre_base": gq, "H_post_base": gp, "H_res_base": gr}
         gx = None
-    for n, prm in hc.named_parameters():
-        assert rel_err(to_np(prm.grad).reshape(ref[n].shape), ref[n]) < 1e-3, n
+    perr = {n: rel_err(to_np(prm.grad).reshape(ref[n].shape), ref[n]) for n, prm in hc.named_parameters()}
+    print(f"full-size {name} parameter gradients:", {n: f"{e:.2e}" for n, e in perr.items()}, flush=True)
+    for n, e in perr.items():
+        assert e < 1e-4, (n, perr)
 
     # dH = H_pre d_bi + H_res^T dH_new (+ grad_x / S) and d_bo = sum_n H_post[n] dH_new[n]
     dH_ref = wp[:, None, :, None] * dbf[:, :, None, :]

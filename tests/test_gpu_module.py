@@ -67,6 +67,7 @@ def check_layer(hc, H, bo, dHn, dbi, fwd_tol, h_tol, p_tol):
     errs = {"bi": rel_err(to_np(bi), obi), "H_new": rel_err(to_np(Hn), oHn)}
     for k, v in og.items():
         errs["d" + k] = rel_err(to_np(grads[k]).reshape(np.shape(v)), v)
+    print("layer errors:", {k: f"{e:.2e}" for k, e in errs.items()}, flush=True)
     assert bi.dtype == H.dtype and Hn.dtype == H.dtype
     assert errs["bi"] < fwd_tol and errs["H_new"] < fwd_tol, errs
     assert errs["dH"] < h_tol and errs["dbo"] < h_tol, errs
@@ -88,13 +89,13 @@ def test_config1_fp32_dynamic(phi_std):
 def test_dynamic_low_precision(dtype):
     """Config 3 / 4 at reduced size: bf16 / fp16 H, fp32 parameters."""
     hc, H, bo, dHn, dbi = make_case(2, 96, 448, dtype, phi_std=0.02)
-    check_layer(hc, H, bo, dHn, dbi, 2e-2, 2e-2, 1e-3)
+    check_layer(hc, H, bo, dHn, dbi, 2e-2, 2e-2, 1e-4)
 
 
 def test_static_fp16():
     """Config 5 at reduced size: dynamic=False, fp16 H, H_res_base ~ N(0, 1)."""
     hc, H, bo, dHn, dbi = make_case(4, 64, 256, torch.float16, dynamic=False, res_std=1.0)
-    check_layer(hc, H, bo, dHn, dbi, 2e-2, 2e-2, 1e-3)
+    check_layer(hc, H, bo, dHn, dbi, 2e-2, 2e-2, 1e-4)
 
 
 def test_static_fp32():
@@ -110,7 +111,7 @@ def test_unfused_dynamic_fp32():
 def test_ragged_dim_bf16():
     """D not a multiple of the 8-element vector: the scalar-path kernels."""
     hc, H, bo, dHn, dbi = make_case(3, 17, 100, torch.bfloat16, phi_std=0.02)
-    check_layer(hc, H, bo, dHn, dbi, 2e-2, 2e-2, 1e-3)
+    check_layer(hc, H, bo, dHn, dbi, 2e-2, 2e-2, 1e-4)
 
 
 @pytest.mark.parametrize("dynamic,fused", [(True, True), (False, True), (True, False)])
@@ -295,3 +296,58 @@ def test_training_steps_change_parameters():
         opt.step()
     changed = sum(1 for n, p in hc.named_parameters() if not torch.allclose(p, init[n]))
     assert changed > 0
+
+
+@pytest.mark.parametrize("dynamic,fused,dtype", [(True, True, torch.float32), (True, True, torch.bfloat16),
+                                                 (False, True, torch.float32), (True, False, torch.float32)])
+def test_overridden_compute_weights_drives_forward(dynamic, fused, dtype):
+    """A subclass that overrides _compute_weights changes the layer, as in the reference's forward
+    (module.py:165-182): here it halves H_pre.  Outputs and every gradient match float64 torch
+    autograd of the reference's composition with the halved H_pre."""
+    import mhc
+    from oracle import torch_path as TP
+
+    class HalfPre(mhc.HyperConnection):
+        def _compute_weights(self, H):
+            H_post, H_pre, H_res = super()._compute_weights(H)
+            return H_post, 0.5 * H_pre, H_res
+
+    hc0, H, bo, dHn, dbi = make_case(2, 24, 64, dtype, dynamic=dynamic, fused=fused, phi_std=0.05, res_std=0.5)
+    hc = HalfPre(64, dynamic=dynamic, use_fused_weights=fused).to(DEV)
+    hc.load_state_dict(hc0.state_dict())
+    bi, Hn, grads = run_gpu(hc, H, bo, dHn, dbi)
+
+    leaves = {n: p.detach().double().cpu().requires_grad_(True) for n, p in hc.named_parameters()}
+    Hl = H.detach().double().cpu().requires_grad_(True)
+    bol = bo.detach().double().cpu().requires_grad_(True)
+    H_post, H_pre, H_res = TP.layer_weights(leaves, Hl, dynamic, fused or not dynamic, hc.sinkhorn_iters, hc.eps)
+    rbi, rhr = TP.stream_mix(Hl, 0.5 * H_pre, H_res)
+    rHn = TP.add_residual(rhr, bol, H_post)
+    torch.autograd.backward([rHn, rbi], [dHn.double().cpu(), dbi.double().cpu()])
+    ftol, gtol = (1e-5, 1e-4) if dtype == torch.float32 else (2e-2, 2e-2)
+    assert rel_err(to_np(bi), to_np(rbi)) < ftol and rel_err(to_np(Hn), to_np(rHn)) < ftol
+    assert rel_err(to_np(grads["H"]), to_np(Hl.grad)) < gtol and rel_err(to_np(grads["bo"]), to_np(bol.grad)) < gtol
+    for n, leaf in leaves.items():
+        err = rel_err(to_np(grads[n.replace(".weight", "")]).reshape(leaf.shape), to_np(leaf.grad))
+        assert err < 1e-4, (n, err)
+    # the base class keeps the fused layer path: its branch_input uses the full H_pre
+    bi0, _ = hc0(H)
+    assert rel_err(to_np(bi), 0.5 * to_np(bi0)) < (1e-5 if dtype == torch.float32 else 2e-2)
+
+
+def test_in_place_check_covers_views_of_one_buffer():
+    """The closure's in-place check reads H's version counter, which every view of one storage
+    shares: a write to another slice of the buffer H is a slice of also raises.  A clone of the
+    slice is independent of the buffer."""
+    hc, H, bo, _, _ = make_case(2, 16, 64, torch.float32, phi_std=0.05)
+    buf = torch.stack([H, H])
+    _, add = hc(buf[0])
+    with torch.no_grad():
+        buf[1].zero_()
+    with pytest.raises(RuntimeError, match="modified in place"):
+        add(bo)
+    _, add = hc(buf[0].clone())
+    with torch.no_grad():
+        buf[1].zero_()
+    _, oHn, _ = O.layer_forward(params_np(hc), to_np(H), to_np(bo))
+    assert rel_err(to_np(add(bo)), oHn) < 1e-5

@@ -139,11 +139,28 @@ def _layer_case(kind, dtype, B, S, D, seed):
     return hc, H, bo, dHn, dbi
 
 
+# The kernels' grad_x (the mean-pool's gradient, added to dH as grad_x / S) comes from fp32
+# reductions over all S * D tokens, like the parameter gradients, and is held to the same
+# fp32-gradient tolerance: an absolute allowance of GX_TOL times the largest |grad_x / S| of the
+# float64 reference, on top of the rounding allowance of the rest of dH.
+GX_TOL = 1e-4
+
+
+def _unfused_weights_backward(hc, x, gw):
+    """grad_x of the unfused weights (torch ops in fp32, as the layer runs them) for the packed
+    weight gradient gw [B, 24]."""
+    xl = x.detach().clone().requires_grad_(True)
+    w = hc._unfused_weights_from(xl)
+    (gx,) = torch.autograd.grad(w, xl, gw)
+    return gx
+
+
 def check_layer_rounding(kind, hc, H, bo, dHn, dbi):
     """Runs the layer's launchers (the ones HyperConnection.forward / backward call) and
     checks branch_input, H_new, d branch_output and dH against the once-rounded float64
-    expressions built from the layer's own weights w [B, 24]."""
-    from mhc import _layer
+    expressions built from the layer's own weights w [B, 24].  dH includes grad_x / S for
+    the dynamic and unfused layers."""
+    from mhc import _kernels, _layer
 
     B, S, _, D = H.shape
     if kind == "dynamic":
@@ -153,7 +170,8 @@ def check_layer_rounding(kind, hc, H, bo, dHn, dbi):
         params = (hc.H_pre_base, hc.H_post_base, hc.H_res_base)
         bi, w = _layer.static_forward(H, *params, hc.sinkhorn_iters)
     else:
-        w = hc._unfused_weights(H).detach().float().contiguous()
+        x = _kernels.mean_pool(H)
+        w = hc._unfused_weights_from(x).detach().float().contiguous()
         bi = _layer.branch_input(H, w)
     H_new = _layer.add_forward(H, bo, w)
     d_bo, dH_post = _layer.add_backward(dHn, bo, w)
@@ -162,7 +180,9 @@ def check_layer_rounding(kind, hc, H, bo, dHn, dbi):
     elif kind == "static":
         dH, _ = _layer.static_backward(H, dbi, dHn, dH_post, *params, w, hc.sinkhorn_iters)
     else:
-        dH, _, _ = _layer.mix_backward(H, dbi, dHn, w)
+        _, dpre_k, dres_k = _layer.mix_backward(H, dbi, dHn, w, need_dH=False)
+        gx_k = _unfused_weights_backward(hc, x, torch.cat([dpre_k, dH_post, dres_k], dim=1))
+        dH = _layer.mix_dh(dbi, dHn, w, gx_k, H.shape, H.dtype)
     torch.cuda.synchronize()
 
     w64 = w.double()
@@ -183,20 +203,27 @@ def check_layer_rounding(kind, hc, H, bo, dHn, dbi):
     dpost = _red(bo64, dHn64)
     assert rel_err(to_np(dH_post), to_np(dpost)) < 1e-5
     dH64, dHa = _dh_ref(dbi64, dHn64, wpre, wres)
-    if kind == "dynamic":
-        # + grad_x / S, the mean-pool's share.  grad_x comes from the float64 weight backward
-        # fed float64 reductions over all S * D tokens; the kernel's grad_x comes from fp32
-        # reductions, held to 1e-3 relative at the full sizes (test_gpu_fullsize.py), so this
-        # one term is allowed 1e-3 of its magnitude (the weight 2^24 / 8 * 1e-3 below).
+    if kind != "static":
+        # + grad_x / S, the mean-pool's share, with grad_x from the float64 weight backward fed
+        # float64 reductions over all S * D tokens.
         dpre = _red(dbi64, H64)
         dres = _red44(dHn64, H64)
-        bias = np.concatenate([to_np(hc.H_pre_base), to_np(hc.H_post_base), to_np(hc.H_res_base).reshape(16)])
-        al = [float(to_np(a)[0]) for a in (hc.alpha_pre, hc.alpha_post, hc.alpha_res)]
-        gx, *_ = O.dynamic_weights_backward(to_np(x), to_np(hc.phi), bias, *al, to_np(dpre), to_np(dH_post),
-                                            to_np(dres), hc.sinkhorn_iters, hc.eps)
+        if kind == "dynamic":
+            bias = np.concatenate([to_np(hc.H_pre_base), to_np(hc.H_post_base), to_np(hc.H_res_base).reshape(16)])
+            al = [float(to_np(a)[0]) for a in (hc.alpha_pre, hc.alpha_post, hc.alpha_res)]
+            gx, *_ = O.dynamic_weights_backward(to_np(x), to_np(hc.phi), bias, *al, to_np(dpre), to_np(dH_post),
+                                                to_np(dres), hc.sinkhorn_iters, hc.eps)
+        else:
+            p = {n.replace(".weight", ""): to_np(v) for n, v in hc.named_parameters()}
+            gx = O.unfused_weights_backward(
+                to_np(x), p["W_pre"], p["W_post"], p["W_res"], p["scale_pre"], p["scale_post"], p["scale_res"],
+                p["H_pre_base"], p["H_post_base"], p["H_res_base"], to_np(dH_post), to_np(dpre), to_np(dres),
+                hc.sinkhorn_iters, hc.eps)["x"]
         gxs = torch.tensor(gx, device=DEV).reshape(B, 1, 4, D) / S
         dH64 = dH64 + gxs
-        dHa = dHa + gxs.abs() * (1.0 + 1e-3 * 2.0 ** 24 / 8)
+        # an absolute allowance of GX_TOL * max|grad_x / S|, expressed in the helper's terms
+        # (it allows 8 * 2^-24 times the absolute-term sum)
+        dHa = dHa + gxs.abs() + GX_TOL * float(gxs.abs().max()) * 2.0 ** 24 / 8
     assert_rounded_once(dH, dH64, dHa, f"{kind} layer dH")
 
 
@@ -213,20 +240,33 @@ def test_layer_rounds_once_ragged_dim():
     check_layer_rounding("dynamic", hc, H, bo, dHn, dbi)
 
 
-def test_module_uses_the_checked_launchers():
+@pytest.mark.parametrize("kind", ["dynamic", "unfused"])
+def test_module_uses_the_checked_launchers(kind):
     """HyperConnection.forward / backward give the same bits as the launcher sequence that
-    check_layer_rounding runs, so its checks hold for the module."""
-    from mhc import _layer
+    check_layer_rounding runs, so its checks hold for the module's full dH (grad_x / S
+    included)."""
+    from mhc import _kernels, _layer
 
-    hc, H, bo, dHn, dbi = _layer_case("dynamic", torch.bfloat16, 2, 64, 256, seed=5)
+    hc, H, bo, dHn, dbi = _layer_case(kind, torch.bfloat16, 2, 64, 256, seed=5)
     Hl, bol = H.clone().requires_grad_(True), bo.clone().requires_grad_(True)
     bi, add = hc(Hl)
     Hn = add(bol)
     torch.autograd.backward([Hn, bi], [dHn, dbi])
-    params = (hc.phi, hc.H_pre_base, hc.H_post_base, hc.H_res_base, hc.alpha_pre, hc.alpha_post, hc.alpha_res)
-    bi2, x, w, aux = _layer.dynamic_forward(H, *params, hc.sinkhorn_iters, hc.eps)
-    Hn2 = _layer.add_forward(H, bo, w)
-    d_bo2, dpost = _layer.add_backward(dHn, bo, w)
-    dH2, *_ = _layer.dynamic_backward(H, dbi, dHn, dpost, *params, x, w, aux, hc.sinkhorn_iters, hc.eps)
+    if kind == "dynamic":
+        params = (hc.phi, hc.H_pre_base, hc.H_post_base, hc.H_res_base, hc.alpha_pre, hc.alpha_post,
+                  hc.alpha_res)
+        bi2, x, w, aux = _layer.dynamic_forward(H, *params, hc.sinkhorn_iters, hc.eps)
+        Hn2 = _layer.add_forward(H, bo, w)
+        d_bo2, dpost = _layer.add_backward(dHn, bo, w)
+        dH2, *_ = _layer.dynamic_backward(H, dbi, dHn, dpost, *params, x, w, aux, hc.sinkhorn_iters, hc.eps)
+    else:
+        x = _kernels.mean_pool(H)
+        w = hc._unfused_weights_from(x).detach().float().contiguous()
+        bi2 = _layer.branch_input(H, w)
+        Hn2 = _layer.add_forward(H, bo, w)
+        d_bo2, dpost = _layer.add_backward(dHn, bo, w)
+        _, dpre, dres = _layer.mix_backward(H, dbi, dHn, w, need_dH=False)
+        gx = _unfused_weights_backward(hc, x, torch.cat([dpre, dpost, dres], dim=1))
+        dH2 = _layer.mix_dh(dbi, dHn, w, gx, H.shape, H.dtype)
     for a, b in ((bi, bi2), (Hn, Hn2), (bol.grad, d_bo2), (Hl.grad, dH2)):
         assert torch.equal(a, b)

@@ -99,6 +99,129 @@ class _OracleLaunchers:
         return torch.tensor(d_bo), torch.tensor(dpost)
 
 
+class _UnfusedLaunchers:
+    """float64 oracle stand-ins for the launchers of the unfused dynamic layer (the sequence-mean
+    node that writes dH, node A's reductions, the closure), so that the pool node's wiring runs on
+    the CPU: dH_new, d_branch_input and w must reach it through the links, and grad_x / S must
+    land in dH once.  torch's Sinkhorn stands in for the HIP one."""
+
+    @staticmethod
+    def mean_pool(H):
+        B, S, n, D = H.shape
+        return H.detach().mean(dim=1).reshape(B, n * D)
+
+    @staticmethod
+    def branch_input(H, w):
+        B = H.shape[0]
+        wn = w.detach().numpy()
+        bi, _ = O.stream_mix(H.detach().numpy(), wn[:, 0:4], wn[:, 8:].reshape(B, 4, 4))
+        return torch.tensor(bi)
+
+    @staticmethod
+    def mix_backward(H, d_bi, dH_new, w, need_dH=True):
+        B, S, _, D = H.shape
+        wn = w.detach().numpy()
+        d_bi = np.zeros((B, S, D)) if d_bi is None else d_bi.numpy()
+        dHn = np.zeros((B, S, 4, D)) if dH_new is None else dH_new.numpy()
+        dH, dpre, dres = O.stream_mix_backward(d_bi, dHn, H.detach().numpy(), wn[:, 0:4], wn[:, 8:].reshape(B, 4, 4))
+        return (torch.tensor(dH) if need_dH else None), torch.tensor(dpre), torch.tensor(dres.reshape(B, 16))
+
+    @staticmethod
+    def mix_dh(d_bi, dH_new, w, grad_x, H_shape, h_dtype):
+        B, S, _, D = H_shape
+        wn = w.detach().numpy()
+        d_bi = np.zeros((B, S, D)) if d_bi is None else d_bi.numpy()
+        dHn = np.zeros((B, S, 4, D)) if dH_new is None else dH_new.numpy()
+        gx = np.zeros((B, 4 * D)) if grad_x is None else grad_x.numpy()
+        dH, _, _ = O.stream_mix_backward(d_bi, dHn, np.zeros((B, S, 4, D)), wn[:, 0:4], wn[:, 8:].reshape(B, 4, 4))
+        return torch.tensor(dH + gx.reshape(B, 1, 4, D) / S)
+
+
+def _unfused_case(monkeypatch):
+    from mhc import _kernels, module
+    from mhc._torch_baseline import sinkhorn_knopp_torch
+
+    for name in ("branch_input", "mix_backward", "mix_dh"):
+        monkeypatch.setattr(_layer, name, getattr(_UnfusedLaunchers, name))
+    for name in ("add_forward", "add_backward"):
+        monkeypatch.setattr(_layer, name, getattr(_OracleLaunchers, name))
+    monkeypatch.setattr(_kernels, "mean_pool", _UnfusedLaunchers.mean_pool)
+    monkeypatch.setattr(module, "sinkhorn_knopp", sinkhorn_knopp_torch)
+    # node A hands the kernels fp32 weights; float64 here keeps the check at rounding level
+    monkeypatch.setattr(_layer, "_f32", lambda t: t.contiguous())
+    g = np.random.default_rng(5)
+    B, S, D = 2, 3, 4
+    hc = mhc.HyperConnection(D, dynamic=True, use_fused_weights=False).double()
+    with torch.no_grad():
+        for prm in hc.parameters():
+            prm.copy_(torch.tensor(g.standard_normal(tuple(prm.shape)) * 0.5))
+    p = {n.replace(".weight", ""): prm.detach().numpy().copy() for n, prm in hc.named_parameters()}
+    arrays = [g.standard_normal(s) for s in ((B, S, 4, D), (B, S, D), (B, S, 4, D), (B, S, D))]
+    return hc, p, arrays
+
+
+def _unfused_grads_close(hc, H, g):
+    g = {k.replace(".weight", ""): v for k, v in g.items()}
+    assert np.abs(H.grad.numpy() - g["H"]).max() < 1e-12
+    for n, prm in hc.named_parameters():
+        k = n.replace(".weight", "")
+        assert np.abs(prm.grad.numpy() - g[k].reshape(prm.shape)).max() < 1e-12, n
+
+
+def test_unfused_layer_writes_dh_in_the_pool_node(monkeypatch):
+    """Unfused dynamic layer, closure called twice: node A hands dH_new, d_branch_input and w to
+    the sequence-mean node, which adds grad_x / S itself; dH and every parameter gradient equal
+    the oracle's (the sum over the two closure calls)."""
+    hc, p, (H_np, bo_np, dHn_np, dbi_np) = _unfused_case(monkeypatch)
+    H = torch.tensor(H_np, requires_grad=True)
+    bi, add = hc(H)
+    Hn1 = add(torch.tensor(bo_np))
+    Hn2 = add(torch.tensor(2 * bo_np))
+    torch.autograd.backward([Hn1, Hn2, bi], [torch.tensor(dHn_np), torch.tensor(0.5 * dHn_np), torch.tensor(dbi_np)])
+    _, _, c1 = O.layer_forward(p, H_np, bo_np, dynamic=True, fused=False, iters=hc.sinkhorn_iters, eps=hc.eps)
+    _, _, c2 = O.layer_forward(p, H_np, 2 * bo_np, dynamic=True, fused=False, iters=hc.sinkhorn_iters, eps=hc.eps)
+    g1 = O.layer_backward(p, c1, dHn_np, dbi_np)
+    g2 = O.layer_backward(p, c2, 0.5 * dHn_np, np.zeros_like(dbi_np))
+    _unfused_grads_close(hc, H, {k: g1[k] + g2[k] for k in g1})
+
+
+def test_unfused_partial_backward_then_branch_input(monkeypatch):
+    """autograd.grad(H_new, branch_output) runs only the closure; bi.backward() afterwards gives
+    the branch_input-only gradients, with grad_x / S still folded into dH by the pool node."""
+    hc, p, (H_np, bo_np, dHn_np, dbi_np) = _unfused_case(monkeypatch)
+    H = torch.tensor(H_np, requires_grad=True)
+    bo = torch.tensor(bo_np, requires_grad=True)
+    bi, add = hc(H)
+    Hn = add(bo)
+    (d_bo,) = torch.autograd.grad(Hn, bo, torch.tensor(dHn_np), retain_graph=True)
+    _, _, cache = O.layer_forward(p, H_np, bo_np, dynamic=True, fused=False, iters=hc.sinkhorn_iters, eps=hc.eps)
+    assert np.abs(d_bo.numpy() - O.layer_backward(p, cache, dHn_np, dbi_np)["bo"]).max() < 1e-12
+    bi.backward(torch.tensor(dbi_np))
+    _unfused_grads_close(hc, H, O.layer_backward(p, cache, np.zeros_like(dHn_np), dbi_np))
+
+
+def test_unfused_parameters_only_and_h_without_grad(monkeypatch):
+    """Gradients of the parameters alone (the pool node's backward is not needed and does not
+    run), and a forward on an H that does not require grad (no pool node is recorded)."""
+    hc, p, (H_np, bo_np, dHn_np, dbi_np) = _unfused_case(monkeypatch)
+    _, _, cache = O.layer_forward(p, H_np, bo_np, dynamic=True, fused=False, iters=hc.sinkhorn_iters, eps=hc.eps)
+    full = {k.replace(".weight", ""): v for k, v in O.layer_backward(p, cache, dHn_np, dbi_np).items()}
+    H = torch.tensor(H_np, requires_grad=True)
+    bi, add = hc(H)
+    Hn = add(torch.tensor(bo_np))
+    params = list(hc.named_parameters())
+    gs = torch.autograd.grad([Hn, bi], [prm for _, prm in params], [torch.tensor(dHn_np), torch.tensor(dbi_np)])
+    for (n, prm), gv in zip(params, gs):
+        k = n.replace(".weight", "")
+        assert np.abs(gv.numpy() - full[k].reshape(prm.shape)).max() < 1e-12, n
+    assert H.grad is None
+    bi, add = hc(torch.tensor(H_np))
+    torch.autograd.backward([add(torch.tensor(bo_np)), bi], [torch.tensor(dHn_np), torch.tensor(dbi_np)])
+    for n, prm in hc.named_parameters():
+        k = n.replace(".weight", "")
+        assert np.abs(prm.grad.numpy() - full[k].reshape(prm.shape)).max() < 1e-12, n
+
+
 def _static_case(monkeypatch):
     for name in ("static_forward", "static_backward", "add_forward", "add_backward"):
         monkeypatch.setattr(_layer, name, getattr(_OracleLaunchers, name))

@@ -19,7 +19,7 @@ OPS = {
     "add_residual_forward", "add_residual_backward", "dynamic_weights_forward", "dynamic_weights_backward",
     "mean_pool", "layer_dynamic_forward", "layer_dynamic_backward", "layer_static_forward",
     "layer_static_backward", "layer_branch_input", "layer_mix_backward", "layer_add_forward",
-    "layer_add_backward", "stream_expand", "stream_collapse",
+    "layer_add_backward", "layer_mix_dh", "layer_mix_reduce", "stream_expand", "stream_collapse",
 }
 BF = torch.bfloat16
 F32 = torch.float32
@@ -73,6 +73,10 @@ def test_fake_kernels_give_the_launchers_output_shapes_and_dtypes():
         assert sig([ops.layer_branch_input(H, e(B, 24))]) == [((B, S, D), BF, "cuda")]
         assert sig(ops.layer_mix_backward(H, bi, H, e(B, 24))) == [
             ((B, S, 4, D), BF, "cuda"), ((B, 4), F32, "cuda"), ((B, 16), F32, "cuda")]
+        assert sig(ops.layer_mix_reduce(H, bi, H, e(B, 24))) == [((B, 4), F32, "cuda"), ((B, 16), F32, "cuda")]
+        assert sig(ops.layer_mix_reduce(H, None, None, e(B, 24))) == [((B, 4), F32, "cuda"), ((B, 16), F32, "cuda")]
+        assert sig([ops.layer_mix_dh(bi, H, e(B, 24), e(B, 4 * D), H)]) == [((B, S, 4, D), BF, "cuda")]
+        assert sig([ops.layer_mix_dh(None, None, e(B, 24), None, H)]) == [((B, S, 4, D), BF, "cuda")]
         assert sig([ops.layer_add_forward(H, bo, e(B, 24))]) == [((B, S, 4, D), BF, "cuda")]
         assert sig(ops.layer_add_backward(H, bo, e(B, 24))) == [((B, S, D), torch.float16, "cuda"),
                                                                 ((B, 4), F32, "cuda")]

@@ -76,3 +76,18 @@ def test_noalloc_rejects_shapes_beyond_the_scratch():
     assert _call(lib, True, H, phi, base, alphas, outs) == 3
     assert b"static array holds" in lib.mhc_last_error()
     assert _call(lib, False, H, phi, base, alphas, outs) == 0
+
+
+def test_noalloc_first_call_under_graph_capture():
+    """The first noalloc call of a process (which looks up the scratch array's device address)
+    made inside torch.cuda.graph capture: in a child process, so that no earlier call has
+    resolved the address or loaded the library's kernels.  Replays match the workspace entry
+    point bit for bit (tests/noalloc_capture_child.py)."""
+    import os
+    import subprocess
+    import sys
+
+    child = os.path.join(os.path.dirname(os.path.abspath(__file__)), "noalloc_capture_child.py")
+    run = subprocess.run([sys.executable, child], capture_output=True, text=True, timeout=180)
+    print(run.stdout, run.stderr[-2000:], flush=True)
+    assert run.returncode == 0, run.stdout + run.stderr[-2000:]
