@@ -4,6 +4,7 @@
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload config3]
     python bench.py --ops        # the low-level ops one by one (one JSON line)
     python bench.py --readme     # the reference's own benchmark table, same workloads
+    python bench.py --dynw-ceiling   # access-pattern ceilings of the MFMA dynamic-weights kernels
 
 One "step" is the HyperConnection layer's forward and backward over one
 synthetic batch, exactly as a transformer block uses it:
@@ -102,6 +103,10 @@ def _parse():
                     help="run the reference's published benchmark table (README.md:183-202, made by "
                          "benchmarks/benchmark.py) on this build: same workloads, same timing method, "
                          "beside the published H100 numbers, and exit")
+    ap.add_argument("--dynw-ceiling", action="store_true",
+                    help="time probe kernels with the access patterns of the MFMA dynamic-weights kernels "
+                         "(forward and backward, R = K = 16384 bf16), adding the kernels' costs one at a time, "
+                         "and the op itself in the same run")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="only run 3 plain device copies of 512 MiB (the known-size kernel that scales "
                          "rocprofv3 FETCH_SIZE / WRITE_SIZE readings into bytes) and exit")
@@ -190,6 +195,99 @@ def _stream_ceiling(tokens: int, row_bytes: int, caps=(0, 2, 3, 4, 6, 8), reps: 
         del a, b, c, w
         torch.cuda.empty_cache()
     return out
+
+
+DYNW_FWD_MODES = {0: "loads only", 1: "+ LDS staging and fragment reads", 2: "+ one workgroup barrier per tile",
+                  3: "+ split-K records (32 rows x 25 floats per tile and K chunk)"}
+DYNW_BWD_MODES = {0: "read only", 1: "copy (each vector stored back in place to grad_x)",
+                  2: "copy through LDS tiles with two barriers per block"}
+
+
+def _dynw_ceiling(R: int = 16384, K: int = 16384, reps: int = 20, warm: int = 3) -> dict:
+    """Probe kernels (csrc/probe/dynw_ceiling.hip) with the grids, per-lane loads, register pipelines
+    and LDS reservations of dynw_mfma_kernel and dynw_bwd_mfma_kernel at the op's plan for R = K,
+    each mode adding one of the kernels' costs; then the op's forward and backward, timed the same
+    way, whose kernels a rocprofv3 kernel trace of this run isolates."""
+    import ctypes
+
+    import torch
+
+    import mhc
+
+    path = os.path.join(ROOT, "mhc-triton_amd", "mhc", "libmhc_probe.so")
+    if not os.path.exists(path):
+        raise RuntimeError(f"{path} is not built (make -C mhc-triton_amd)")
+    lib = ctypes.CDLL(path)
+    fn = lib.mhc_probe_dynw
+    fn.restype = ctypes.c_int
+    fn.argtypes = [ctypes.c_int, ctypes.c_int] + [ctypes.c_void_p] * 2 + [ctypes.c_int64] * 3 + \
+        [ctypes.c_void_p] * 2
+    dev = "cuda:0"
+    g = torch.Generator(device=dev).manual_seed(0)
+    x = torch.randn((R, K), generator=g, device=dev).to(torch.bfloat16)
+    gx = torch.empty_like(x)
+    nK = (K // 16 + 63) // 64
+    part = torch.empty(R * nK * 25, device=dev)
+    sink = torch.zeros(256, dtype=torch.int32, device=dev)
+    stream = torch.cuda.current_stream().cuda_stream
+    xbytes = R * K * 2
+    # the ops' plans at R = K = 16384 (csrc/dynamic_weights.hip): 16 row ranges of 1024 rows per K
+    # chunk forward, 4 row chunks of 4096 rows per 256-column block backward
+    tiles = (R + 31) // 32
+    ngr = min(tiles, (256 + nK - 1) // nK)
+    fwd_rows = 32 * ((tiles + ngr - 1) // ngr)
+    bwd_rows = (R + 3) // 4
+
+    def timed(call):
+        for _ in range(warm):
+            call()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(reps):
+            call()
+        e1.record()
+        torch.cuda.synchronize()
+        return e0.elapsed_time(e1) * 1e3 / reps
+
+    def probe(pattern, mode, out, rows):
+        def call():
+            rc = fn(pattern, mode, x.data_ptr(), out.data_ptr() if out is not None else None, R, K, rows,
+                    sink.data_ptr(), stream)
+            if rc:
+                raise RuntimeError(f"mhc_probe_dynw({pattern}, {mode}) returned {rc}")
+        return call
+
+    res = {"forward": {}, "backward": {}}
+    for mode, what in DYNW_FWD_MODES.items():
+        us = timed(probe(0, mode, part, fwd_rows))
+        res["forward"][str(mode)] = {"what": what, "us": round(us, 1),
+                                     "frac": round(xbytes / (us * 1e-6) / (HBM_PEAK_GBS * 1e9), 4)}
+        _log(f"dynw ceiling forward mode {mode} ({what}): {us:.1f} us")
+    for mode, what in DYNW_BWD_MODES.items():
+        us = timed(probe(1, mode, gx, bwd_rows))
+        nbytes = xbytes * (1 if mode == 0 else 2)
+        res["backward"][str(mode)] = {"what": what, "us": round(us, 1),
+                                      "frac": round(nbytes / (us * 1e-6) / (HBM_PEAK_GBS * 1e9), 4)}
+        _log(f"dynw ceiling backward mode {mode} ({what}): {us:.1f} us")
+    phi = torch.randn((K, 24), generator=g, device=dev) * 0.02
+    bias = torch.randn(24, generator=g, device=dev)
+    al = [torch.tensor([0.1], device=dev) for _ in range(3)]
+    gw = [torch.randn(s, generator=g, device=dev) for s in ((R, 4), (R, 4), (R, 4, 4))]
+    xl = x.clone().requires_grad_(True)
+
+    def fwd():
+        mhc.fused_dynamic_weights(x, phi, bias, *al)
+
+    def fwd_bwd():
+        xl.grad = None
+        out = mhc.fused_dynamic_weights(xl, phi, bias, *al)
+        torch.autograd.backward(list(out), gw)
+
+    res["op"] = {"forward_us": round(timed(fwd), 1), "forward_backward_us": round(timed(fwd_bwd), 1),
+                 "note": "whole op calls (host time included); kernel times come from a kernel trace"}
+    res["plan"] = {"R": R, "K": K, "forward_rows_per_workgroup": fwd_rows, "k_chunks": nK,
+                   "backward_rows_per_chunk": bwd_rows, "x_bytes": xbytes}
+    return res
 
 
 def _calibrate_copy() -> int:
@@ -628,6 +726,13 @@ def main() -> int:
         return 1
     if args.calibrate_copy:
         return _calibrate_copy()
+    if args.dynw_ceiling:
+        from mhc import _lib
+
+        _lib.load()
+        print(json.dumps({"dynw_ceiling": _dynw_ceiling(), "unit": "us per launch", "peak_GBps": HBM_PEAK_GBS,
+                          "device": torch.cuda.get_device_name(0)}), flush=True)
+        return 0
     if args.stream_ceiling:
         cfg = WORKLOADS[args.workload]
         tokens, row_bytes = cfg["B"] * cfg["S"], cfg["D"] * (2 if cfg["dtype"] in ("bf16", "fp16") else 4)

@@ -68,3 +68,45 @@ def test_probe_moves_every_row(probe, mix, nt, cap, row_bytes):
         assert torch.equal(got, ref), f"output row {o}"
     if nw == 0:
         assert int(sink.abs().sum()) == 0  # the store that keeps the loads live never fires here
+
+
+@pytest.mark.parametrize("mode", [1, 2])
+@pytest.mark.parametrize("R,K,rows", [(1000, 512, 300), (256, 768, 64)])
+def test_dynw_backward_probe_copies_every_strip(mode, R, K, rows):
+    """bench.py --dynw-ceiling's backward pattern (the MFMA backward's 512-byte strips, 64-row
+    blocks, two blocks in flight) reads every element of x and writes every element of grad_x:
+    copied with the first word of each 16-byte vector XOR 1 (mode 1), or unchanged through the
+    LDS tiles (mode 2).  Row chunks end inside a block."""
+    lib = ctypes.CDLL(PROBE)
+    fn = lib.mhc_probe_dynw
+    fn.restype = ctypes.c_int
+    fn.argtypes = [ctypes.c_int, ctypes.c_int] + [ctypes.c_void_p] * 2 + [ctypes.c_int64] * 3 + [ctypes.c_void_p] * 2
+    g = torch.Generator(device="cuda").manual_seed(R + mode)
+    x = torch.randint(-2 ** 15, 2 ** 15 - 1, (R, K), generator=g, device="cuda", dtype=torch.int16)
+    gx = torch.full_like(x, -7)
+    sink = torch.zeros(256, dtype=torch.int32, device="cuda")
+    assert fn(1, mode, x.data_ptr(), gx.data_ptr(), R, K, rows, sink.data_ptr(),
+              torch.cuda.current_stream().cuda_stream) == 0
+    torch.cuda.synchronize()
+    want = x.view(torch.int32).reshape(R, K // 8, 4).clone()
+    if mode == 1:
+        want[:, :, 0] ^= 1
+    assert torch.equal(gx.view(torch.int32).reshape(R, K // 8, 4), want)
+
+
+@pytest.mark.parametrize("R,K,rows", [(1000, 2048, 320), (96, 1040, 64)])
+def test_dynw_forward_probe_writes_every_record(R, K, rows):
+    """The forward pattern's mode 3 writes one 25-float record per row and K chunk, as the
+    projection kernel does: its tile loop covers every row of every range."""
+    lib = ctypes.CDLL(PROBE)
+    fn = lib.mhc_probe_dynw
+    fn.restype = ctypes.c_int
+    fn.argtypes = [ctypes.c_int, ctypes.c_int] + [ctypes.c_void_p] * 2 + [ctypes.c_int64] * 3 + [ctypes.c_void_p] * 2
+    nK = (K // 16 + 63) // 64
+    x = torch.ones((R, K), device="cuda", dtype=torch.bfloat16)
+    part = torch.full((R * nK * 25,), float("nan"), device="cuda")
+    sink = torch.zeros(256, dtype=torch.int32, device="cuda")
+    assert fn(0, 3, x.data_ptr(), part.data_ptr(), R, K, rows, sink.data_ptr(),
+              torch.cuda.current_stream().cuda_stream) == 0
+    torch.cuda.synchronize()
+    assert not part.isnan().any()
