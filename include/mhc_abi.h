@@ -216,7 +216,10 @@ int mhc_layer_dynamic_forward(const void* H, int dtype, const float* phi,
  * B * D up to about 950k fits (B = 232 at D = 4096, any S).  The scratch
  * starts from nothing it has to find zeroed: each call overwrites every entry
  * it reads.  All calls on one GPU share that GPU's array, so calls that overlap
- * on one GPU (on different streams) race; serialise them. */
+ * on one GPU (on different streams) race; serialise them.  The array's address
+ * is looked up on the first call on each GPU and kept for the process: once
+ * this entry point has run on a GPU, do not call it there again after
+ * hipDeviceReset (which unloads the code object the address points into). */
 int mhc_layer_dynamic_forward_noalloc(const void* H, int dtype, const float* phi,
                                       const float* H_pre_base, const float* H_post_base,
                                       const float* H_res_base, const float* alpha_pre,

@@ -305,7 +305,9 @@ extern "C" int mhc_layer_dynamic_forward(const void* H, int dtype, const float* 
 // of the process.  In host code `scratch` only names the symbol; the device
 // address of each GPU's copy comes from hipGetSymbolAddress, taken once per
 // device with that device current, and kept in g_scratch_dev.  Calls that
-// overlap on one GPU (different streams) share the array and race.
+// overlap on one GPU (different streams) share the array and race.  The kept
+// address is never refreshed: hipDeviceReset on a GPU where the entry point
+// has run invalidates it, and the header rules out calls after one.
 // ---------------------------------------------------------------------------
 constexpr size_t kScratchBytes = MHC_NOALLOC_SCRATCH_BYTES;
 static __device__ __align__(256) unsigned char scratch[kScratchBytes];

@@ -200,7 +200,11 @@ def test_add_residual_forward_backward(dtype, bo_dtype, shape):
                                         (100, 1000, torch.bfloat16),
                                         # MFMA backward row chunks of 188 rows (two whole 64-row
                                         # blocks and a partial one), eight chunk partials
-                                        (1500, 8192, torch.bfloat16)])
+                                        (1500, 8192, torch.bfloat16),
+                                        # MFMA forward with rows in bulk: 9 chunks, the last one step
+                                        # long (seven of its eight waves' slices past K), a last row
+                                        # range of 11 tiles (an odd count, the last one partial)
+                                        (21845, 8208, torch.bfloat16)])
 def test_dynamic_weights_forward_backward(R, K, xdtype):
     import mhc
 
@@ -236,7 +240,7 @@ def test_dynamic_weights_forward_backward(R, K, xdtype):
     assert rel_err(np.array([a.grad.item() for a in leaves[3:]]), np.array(ga)) < 1e-4
 
 
-@pytest.mark.parametrize("R,K", [(1000, 4096), (257, 3008)])
+@pytest.mark.parametrize("R,K", [(1000, 4096), (257, 3008), (21845, 8208)])
 def test_dynamic_weights_mfma_paths_are_deterministic(R, K):
     """The MFMA projection adds its waves' tile results and the K chunks in a fixed order, and the
     backward's grad_phi / bias partials likewise: two calls give the same bits."""
