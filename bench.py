@@ -203,16 +203,20 @@ DYNW_BWD_MODES = {0: "read only", 1: "copy (each vector stored back in place to 
                   2: "copy through LDS tiles with two barriers per block"}
 
 
-def _dynw_ceiling(R: int = 16384, K: int = 16384, reps: int = 20, warm: int = 3) -> dict:
+def _dynw_ceiling(R: int = 16384, K: int = 16384, reps: int = 10, warm: int = 2, rounds: int = 3) -> dict:
     """Probe kernels (csrc/probe/dynw_ceiling.hip) with the grids, per-lane loads, register pipelines
     and LDS reservations of dynw_mfma_kernel and dynw_bwd_mfma_kernel at the op's plan for R = K,
-    each mode adding one of the kernels' costs; then the op's forward and backward, timed the same
-    way, whose kernels a rocprofv3 kernel trace of this run isolates."""
+    each mode adding one of the kernels' costs, and the op's forward and backward launchers beside
+    them.  The box's kernel times drift by 10-20% over seconds of back-to-back streaming, so the
+    probes and the launchers alternate in rounds and each figure is the median over rounds; a
+    rocprofv3 kernel trace of this run splits the launchers' time into their kernels."""
     import ctypes
+    import statistics
 
     import torch
 
-    import mhc
+    from mhc import _backward as KB
+    from mhc import _kernels as KF
 
     path = os.path.join(ROOT, "mhc-triton_amd", "mhc", "libmhc_probe.so")
     if not os.path.exists(path):
@@ -241,7 +245,9 @@ def _dynw_ceiling(R: int = 16384, K: int = 16384, reps: int = 20, warm: int = 3)
     def timed(call):
         for _ in range(warm):
             call()
+        torch.cuda.synchronize()
         e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        torch.cuda._sleep(1 << 20)  # the host queues the first calls while this spins
         e0.record()
         for _ in range(reps):
             call()
@@ -257,36 +263,44 @@ def _dynw_ceiling(R: int = 16384, K: int = 16384, reps: int = 20, warm: int = 3)
                 raise RuntimeError(f"mhc_probe_dynw({pattern}, {mode}) returned {rc}")
         return call
 
-    res = {"forward": {}, "backward": {}}
-    for mode, what in DYNW_FWD_MODES.items():
-        us = timed(probe(0, mode, part, fwd_rows))
-        res["forward"][str(mode)] = {"what": what, "us": round(us, 1),
-                                     "frac": round(xbytes / (us * 1e-6) / (HBM_PEAK_GBS * 1e9), 4)}
-        _log(f"dynw ceiling forward mode {mode} ({what}): {us:.1f} us")
-    for mode, what in DYNW_BWD_MODES.items():
-        us = timed(probe(1, mode, gx, bwd_rows))
-        nbytes = xbytes * (1 if mode == 0 else 2)
-        res["backward"][str(mode)] = {"what": what, "us": round(us, 1),
-                                      "frac": round(nbytes / (us * 1e-6) / (HBM_PEAK_GBS * 1e9), 4)}
-        _log(f"dynw ceiling backward mode {mode} ({what}): {us:.1f} us")
     phi = torch.randn((K, 24), generator=g, device=dev) * 0.02
     bias = torch.randn(24, generator=g, device=dev)
     al = [torch.tensor([0.1], device=dev) for _ in range(3)]
     gw = [torch.randn(s, generator=g, device=dev) for s in ((R, 4), (R, 4), (R, 4, 4))]
-    xl = x.clone().requires_grad_(True)
+    H_pre, _, _, aux = KF.fused_dynamic_weights_forward(x, phi, bias, *al, return_aux=True)
 
     def fwd():
-        mhc.fused_dynamic_weights(x, phi, bias, *al)
+        KF.fused_dynamic_weights_forward(x, phi, bias, *al)
 
-    def fwd_bwd():
-        xl.grad = None
-        out = mhc.fused_dynamic_weights(xl, phi, bias, *al)
-        torch.autograd.backward(list(out), gw)
+    def bwd():
+        KB.fused_dynamic_weights_backward(x, phi, bias, al, aux, H_pre, *gw, 20, 1e-6)
 
-    res["op"] = {"forward_us": round(timed(fwd), 1), "forward_backward_us": round(timed(fwd_bwd), 1),
-                 "note": "whole op calls (host time included); kernel times come from a kernel trace"}
+    t = {}
+    for rnd in range(rounds):
+        for mode in DYNW_FWD_MODES:
+            t.setdefault(("forward", mode), []).append(timed(probe(0, mode, part, fwd_rows)))
+        t.setdefault(("op", "forward"), []).append(timed(fwd))
+        for mode in DYNW_BWD_MODES:
+            t.setdefault(("backward", mode), []).append(timed(probe(1, mode, gx, bwd_rows)))
+        t.setdefault(("op", "backward"), []).append(timed(bwd))
+        _log(f"dynw ceiling round {rnd + 1}/{rounds}: " +
+             ", ".join(f"{k[0]} {k[1]} {v[-1]:.1f}" for k, v in t.items()))
+    med = {k: statistics.median(v) for k, v in t.items()}
+    res = {"forward": {}, "backward": {}}
+    for mode, what in DYNW_FWD_MODES.items():
+        us = med[("forward", mode)]
+        res["forward"][str(mode)] = {"what": what, "us": round(us, 1),
+                                     "frac": round(xbytes / (us * 1e-6) / (HBM_PEAK_GBS * 1e9), 4)}
+    for mode, what in DYNW_BWD_MODES.items():
+        us = med[("backward", mode)]
+        nbytes = xbytes * (1 if mode == 0 else 2)
+        res["backward"][str(mode)] = {"what": what, "us": round(us, 1),
+                                      "frac": round(nbytes / (us * 1e-6) / (HBM_PEAK_GBS * 1e9), 4)}
+    res["op"] = {"forward_us": round(med[("op", "forward")], 1), "backward_us": round(med[("op", "backward")], 1),
+                 "note": "launcher calls (all of each op's kernels); per-kernel times come from a kernel trace"}
     res["plan"] = {"R": R, "K": K, "forward_rows_per_workgroup": fwd_rows, "k_chunks": nK,
-                   "backward_rows_per_chunk": bwd_rows, "x_bytes": xbytes}
+                   "backward_rows_per_chunk": bwd_rows, "x_bytes": xbytes, "rounds": rounds,
+                   "launches_per_figure": reps}
     return res
 
 
@@ -324,6 +338,9 @@ def _ops_leg(n: int = 20, warm: int = 3) -> dict:
         torch.cuda.synchronize()
         a = torch.cuda.Event(enable_timing=True)
         b = torch.cuda.Event(enable_timing=True)
+        # a bounded spin kernel ahead of the first event keeps the GPU busy while the host
+        # queues the first calls, so the host's start-up latency stays out of the interval
+        torch.cuda._sleep(1 << 20)
         a.record()
         for _ in range(calls):
             fn()
@@ -369,7 +386,7 @@ def _ops_leg(n: int = 20, warm: int = 3) -> dict:
         4 * 4 * D * 4)
     xt = torch.randn((T, 4 * D), generator=g, device=dev).bfloat16()
     rec("dynamic_weights_fwd R=16384 K=16384 bf16",
-        timed(lambda: K.fused_dynamic_weights_forward(xt, phi, bias, *al), 5), T * 4 * D * e)
+        timed(lambda: K.fused_dynamic_weights_forward(xt, phi, bias, *al)), T * 4 * D * e)
     xl = xt.clone().requires_grad_(True)
     phl = phi.clone().requires_grad_(True)
     gs = [torch.randn((T, 4), generator=g, device=dev), torch.randn((T, 4), generator=g, device=dev),
@@ -380,7 +397,7 @@ def _ops_leg(n: int = 20, warm: int = 3) -> dict:
         torch.autograd.grad(o, [xl, phl], gs)
 
     # x read by the forward, x read and grad_x written by the backward
-    rec("dynamic_weights_fwd+bwd R=16384 K=16384 bf16", timed(fwd_bwd, 5), 3 * T * 4 * D * e)
+    rec("dynamic_weights_fwd+bwd R=16384 K=16384 bf16", timed(fwd_bwd), 3 * T * 4 * D * e)
     return out
 
 
