@@ -22,6 +22,9 @@
 //   2  copy through LDS: the block staged in an x tile, a barrier, copied to a
 //        grad_x tile, a barrier, stored from there (the kernel's two
 //        barriers per block and its tile traffic)
+//   3  as 2 with the tiles doubled by block parity: each pair of blocks stores
+//        both grad_x tiles after the second block's barrier (64-KiB store
+//        bursts per workgroup, three barriers per pair)
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
@@ -155,6 +158,31 @@ __global__ __launch_bounds__(kBwdThreads, mhc::kBwdMinWaves) void dynw_bwd_patte
       load_block(b + kAhead, v);
 #pragma unroll
       for (int i = 0; i < kNX; ++i) gxsp.store16<true>(off(b, i), o[i]);
+    } else if constexpr (MODE == 3) {
+      // two x tiles and two grad_x tiles by block parity; the second block of each pair stores
+      // both blocks' grad_x tiles after its barrier (64-KiB bursts, three barriers per pair)
+      const int par = (int)(b & 1);
+      __bf16* xp = xt + par * (2 * kTR * kBwdPitch);
+      __bf16* gp = gt + par * (2 * kTR * kBwdPitch);
+#pragma unroll
+      for (int i = 0; i < kNX; ++i) *reinterpret_cast<u32x4*>(&xp[(xr + kXRPP * i) * kBwdPitch + xc]) = v[i];
+      __syncthreads();
+      load_block(b + kAhead, v);
+      const int yr = (xr + 1) % kXRPP;
+#pragma unroll
+      for (int i = 0; i < kNX; ++i)
+        *reinterpret_cast<u32x4*>(&gp[(yr + kXRPP * i) * kBwdPitch + xc]) =
+            *reinterpret_cast<const u32x4*>(&xp[(yr + kXRPP * i) * kBwdPitch + xc]);
+      if (par) {
+        __syncthreads();
+#pragma unroll
+        for (int q = 0; q < 2; ++q) {
+          const __bf16* gq = gt + q * (2 * kTR * kBwdPitch);
+#pragma unroll
+          for (int i = 0; i < kNX; ++i)
+            gxsp.store16<true>(off(b - 1 + q, i), *reinterpret_cast<const u32x4*>(&gq[(xr + kXRPP * i) * kBwdPitch + xc]));
+        }
+      }
     } else {
 #pragma unroll
       for (int i = 0; i < kNX; ++i) *reinterpret_cast<u32x4*>(&xt[(xr + kXRPP * i) * kBwdPitch + xc]) = v[i];
@@ -189,13 +217,15 @@ __global__ __launch_bounds__(kBwdThreads, mhc::kBwdMinWaves) void dynw_bwd_patte
 constexpr size_t kFwdLds = sizeof(u32x4) * kFwdWaves * 32 * kL +
                            sizeof(float) * 2 * kFwdWaves * mhc::kMfmaRedCols * mhc::kMfmaRedPitch;
 constexpr size_t kBwdLds = sizeof(__bf16) * (2 * kTR * kBwdPitch + 2 * kTR * mhc::kBwdGPitch) + sizeof(float) * kTR;
+// mode 3: two x and two grad_x tiles (the x tile of parity p at p * 2 tiles, its grad_x tile after it)
+constexpr size_t kBwdLds3 = kBwdLds + sizeof(__bf16) * 2 * kTR * kBwdPitch;
 
 }  // namespace
 
 // Forward pattern over x [R, K] bf16 with mode 0..3 (above), the kernel's plan:
 // nK chunks of kFwdWaves * kFwdSteps * 16 columns, row ranges of rows_per_wg;
 // `part` holds R * nK * 25 floats (mode 3).  Backward pattern over x and
-// grad_x [R, K] bf16 with mode 0..2 and row chunks of RC rows.  `sink` is 1 KiB
+// grad_x [R, K] bf16 with mode 0..3 and row chunks of RC rows.  `sink` is 1 KiB
 // of device memory that keeps loaded values live.  Returns 0, 1 for a bad
 // argument, 2 for a launch error.
 extern "C" int mhc_probe_dynw(int pattern, int mode, const void* x, void* out, int64_t R, int64_t K,
@@ -226,6 +256,7 @@ extern "C" int mhc_probe_dynw(int pattern, int mode, const void* x, void* out, i
       case 0: dynw_bwd_pattern_kernel<0><<<grid, kBwdThreads, kBwdLds, st>>>(xb, g, R, K, rows, s); break;
       case 1: dynw_bwd_pattern_kernel<1><<<grid, kBwdThreads, kBwdLds, st>>>(xb, g, R, K, rows, s); break;
       case 2: dynw_bwd_pattern_kernel<2><<<grid, kBwdThreads, kBwdLds, st>>>(xb, g, R, K, rows, s); break;
+      case 3: dynw_bwd_pattern_kernel<3><<<grid, kBwdThreads, kBwdLds3, st>>>(xb, g, R, K, rows, s); break;
       default: return 1;
     }
   } else {

@@ -70,13 +70,13 @@ def test_probe_moves_every_row(probe, mix, nt, cap, row_bytes):
         assert int(sink.abs().sum()) == 0  # the store that keeps the loads live never fires here
 
 
-@pytest.mark.parametrize("mode", [1, 2])
+@pytest.mark.parametrize("mode", [1, 2, 3])
 @pytest.mark.parametrize("R,K,rows", [(1000, 512, 300), (256, 768, 64)])
 def test_dynw_backward_probe_copies_every_strip(mode, R, K, rows):
     """bench.py --dynw-ceiling's backward pattern (the MFMA backward's 512-byte strips, 64-row
     blocks, two blocks in flight) reads every element of x and writes every element of grad_x:
     copied with the first word of each 16-byte vector XOR 1 (mode 1), or unchanged through the
-    LDS tiles (mode 2).  Row chunks end inside a block."""
+    LDS tiles (modes 2 and 3).  Row chunks end inside a block."""
     lib = ctypes.CDLL(PROBE)
     fn = lib.mhc_probe_dynw
     fn.restype = ctypes.c_int
