@@ -27,7 +27,7 @@ using mhc::u32x4;
 constexpr int kLanes = 256;
 constexpr int kTileBytes = kLanes * 16;
 
-template <int NA, int NB, int NC, int NW, bool NT>
+template <int NA, int NB, int NC, int NW, bool NT, bool NTS>
 __global__ __launch_bounds__(kLanes) void stream_probe_kernel(const char* __restrict__ a, const char* __restrict__ b,
                                                               const char* __restrict__ c, char* __restrict__ w,
                                                               int64_t row_bytes, uint32_t tiles_per_token,
@@ -59,7 +59,7 @@ __global__ __launch_bounds__(kLanes) void stream_probe_kernel(const char* __rest
     for (int o = 0; o < NW; ++o) {
       u32x4 s = tot + u32x4{(uint32_t)o, 0u, 0u, 0u};
       if constexpr (NR > 0) s += v[o % NR];
-      sw.store16<NT>((uint32_t)(o * row_bytes) + col, s);
+      sw.store16<NTS>((uint32_t)(o * row_bytes) + col, s);
     }
   } else {
     if (tot.x == 0x9e3779b9u && tot.y == 0x7f4a7c15u && tot.z == tot.w) sink[threadIdx.x] = tot.x;
@@ -70,7 +70,7 @@ __global__ __launch_bounds__(kLanes) void stream_probe_kernel(const char* __rest
 // layer kernels' flattened items): item i of the [T, row_bytes / 16] vector
 // plane is token i / nvec, vector i % nvec, and a workgroup takes 256
 // consecutive items, so it may span two tokens.
-template <int NA, int NB, int NC, int NW, bool NT>
+template <int NA, int NB, int NC, int NW, bool NT, bool NTS>
 __global__ __launch_bounds__(kLanes) void stream_probe_flat_kernel(const char* __restrict__ a,
                                                                    const char* __restrict__ b,
                                                                    const char* __restrict__ c, char* __restrict__ w,
@@ -112,7 +112,7 @@ __global__ __launch_bounds__(kLanes) void stream_probe_flat_kernel(const char* _
       for (int o = 0; o < NW; ++o) {
         u32x4 s = tot + u32x4{(uint32_t)o, 0u, 0u, 0u};
         if constexpr (NR > 0) s += v[o % NR];
-        sw.store16<NT>((uint32_t)((trel * NW + o) * row_bytes) + col, s);
+        sw.store16<NTS>((uint32_t)((trel * NW + o) * row_bytes) + col, s);
       }
     }
   } else {
@@ -120,28 +120,33 @@ __global__ __launch_bounds__(kLanes) void stream_probe_flat_kernel(const char* _
   }
 }
 
-template <int NA, int NB, int NC, int NW>
-hipError_t launch(const void* a, const void* b, const void* c, void* w, int64_t tokens, int64_t row_bytes,
-                  size_t lds, bool nt, unsigned* sink, hipStream_t st) {
+template <int NA, int NB, int NC, int NW, bool NT, bool NTS>
+hipError_t launch_policy(const void* a, const void* b, const void* c, void* w, int64_t tokens, int64_t row_bytes,
+                         size_t lds, unsigned* sink, hipStream_t st) {
   if (row_bytes % kTileBytes != 0) {
     const dim3 grid((unsigned)((tokens * (row_bytes / 16) + kLanes - 1) / kLanes));
-    if (nt)
-      stream_probe_flat_kernel<NA, NB, NC, NW, true><<<grid, kLanes, lds, st>>>(
-          (const char*)a, (const char*)b, (const char*)c, (char*)w, row_bytes, tokens, sink);
-    else
-      stream_probe_flat_kernel<NA, NB, NC, NW, false><<<grid, kLanes, lds, st>>>(
-          (const char*)a, (const char*)b, (const char*)c, (char*)w, row_bytes, tokens, sink);
+    stream_probe_flat_kernel<NA, NB, NC, NW, NT, NTS><<<grid, kLanes, lds, st>>>(
+        (const char*)a, (const char*)b, (const char*)c, (char*)w, row_bytes, tokens, sink);
     return hipGetLastError();
   }
   const uint32_t tpt = (uint32_t)(row_bytes / kTileBytes);
   const dim3 grid((unsigned)(tokens * tpt));
-  if (nt)
-    stream_probe_kernel<NA, NB, NC, NW, true><<<grid, kLanes, lds, st>>>(
-        (const char*)a, (const char*)b, (const char*)c, (char*)w, row_bytes, tpt, sink);
-  else
-    stream_probe_kernel<NA, NB, NC, NW, false><<<grid, kLanes, lds, st>>>(
-        (const char*)a, (const char*)b, (const char*)c, (char*)w, row_bytes, tpt, sink);
+  stream_probe_kernel<NA, NB, NC, NW, NT, NTS><<<grid, kLanes, lds, st>>>(
+      (const char*)a, (const char*)b, (const char*)c, (char*)w, row_bytes, tpt, sink);
   return hipGetLastError();
+}
+
+// policy: 0 plain loads and stores, 1 nt loads and stores, 2 nt loads and plain
+// stores, 3 plain loads and nt stores
+template <int NA, int NB, int NC, int NW>
+hipError_t launch(const void* a, const void* b, const void* c, void* w, int64_t tokens, int64_t row_bytes,
+                  size_t lds, int policy, unsigned* sink, hipStream_t st) {
+  switch (policy) {
+    case 0: return launch_policy<NA, NB, NC, NW, false, false>(a, b, c, w, tokens, row_bytes, lds, sink, st);
+    case 1: return launch_policy<NA, NB, NC, NW, true, true>(a, b, c, w, tokens, row_bytes, lds, sink, st);
+    case 2: return launch_policy<NA, NB, NC, NW, true, false>(a, b, c, w, tokens, row_bytes, lds, sink, st);
+    default: return launch_policy<NA, NB, NC, NW, false, true>(a, b, c, w, tokens, row_bytes, lds, sink, st);
+  }
 }
 
 }  // namespace
@@ -152,12 +157,14 @@ hipError_t launch(const void* a, const void* b, const void* c, void* w, int64_t 
 // write mixes of the layer's streaming kernels and the plain references
 // (4,0,0,0) (4,0,0,1) (4,1,0,4) (4,1,0,1) (4,4,1,0) (1,0,0,1) (1,0,0,0)
 // (0,0,0,1), and those of the standalone ops (4,0,0,5) (1,0,0,4) (4,4,1,4).  wg_per_cu > 0 caps resident workgroups per CU (0: no cap).
+// nt is the cache policy: 0 plain, 1 nt (streaming) loads and stores, 2 nt
+// loads with plain stores, 3 plain loads with nt stores.
 // `sink` is 1 KiB of device memory that a read-only mix keeps live.  Returns
 // 0, 1 for an unsupported mix, shape or a missing array, 2 for a launch error.
 extern "C" int mhc_probe_stream(int na, int nb, int nc, int nw, const void* a, const void* b, const void* c, void* w,
                                 int64_t tokens, int64_t row_bytes, int wg_per_cu, int nt, void* sink,
                                 void* stream) {
-  if (tokens <= 0 || row_bytes <= 0 || row_bytes % 16 != 0) return 1;
+  if (tokens <= 0 || row_bytes <= 0 || row_bytes % 16 != 0 || nt < 0 || nt > 3) return 1;
   if ((na > 0 && !a) || (nb > 0 && !b) || (nc > 0 && !c) || (nw > 0 && !w) || (nw == 0 && !sink)) return 1;
   int rows = na > nb ? na : nb;
   rows = rows > nc ? rows : nc;
