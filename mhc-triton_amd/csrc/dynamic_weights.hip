@@ -32,7 +32,7 @@ static DynPlan dyn_plan(int64_t R, int64_t K) {
 
 static size_t align256(size_t v) { return (v + 255) & ~(size_t)255; }
 
-// MFMA plan for bf16 x with many rows (dynw_mfma_kernel): K chunks of
+// MFMA plan for bf16 / fp16 x with many rows (dynw_mfma_kernel): K chunks of
 // kMfmaChunkSteps steps (1024 k), and row ranges of whole 32-row tiles so that
 // about kMfmaTargetWg workgroups run, one per CU (the kernel's LDS allows one).
 // At R = K = 16384: 16 chunks x 16 ranges of 1024 rows.
@@ -105,11 +105,16 @@ extern "C" int mhc_dynamic_weights_forward(const void* x, int dtype_x, const flo
   hipStream_t st = (hipStream_t)stream;
   float* part = (float*)workspace;
   int nK = 0;
-  if (dtype_x == MHC_DTYPE_BF16 && mfma_shape_ok(R, K) && aligned16(x)) {
-    // bf16 rows in bulk: the projection on MFMA (HBM-bound instead of VALU-bound).
+  if ((dtype_x == MHC_DTYPE_BF16 || dtype_x == MHC_DTYPE_F16) && mfma_shape_ok(R, K) && aligned16(x)) {
+    // bf16 / fp16 rows in bulk: the projection on MFMA (HBM-bound instead of VALU-bound).
     const MfmaPlan m = mfma_plan(R, K);
-    dynw_mfma_kernel<><<<dim3((unsigned)m.ngr, (unsigned)m.nK), 64 * kMfmaWaves, 0, st>>>(
-        (const __bf16*)x, phi, part, R, K, m.nK, m.rows_per_wg);
+    const dim3 grid((unsigned)m.ngr, (unsigned)m.nK);
+    if (dtype_x == MHC_DTYPE_BF16)
+      dynw_mfma_kernel<__bf16><<<grid, 64 * kMfmaWaves, 0, st>>>((const __bf16*)x, phi, part, R, K, m.nK,
+                                                                 m.rows_per_wg);
+    else
+      dynw_mfma_kernel<_Float16><<<grid, 64 * kMfmaWaves, 0, st>>>((const _Float16*)x, phi, part, R, K, m.nK,
+                                                                   m.rows_per_wg);
     if (int rc = hip_status(hipGetLastError(), "dynamic_weights_forward mfma launch")) return rc;
     nK = m.nK;
   } else {
@@ -227,8 +232,8 @@ extern "C" int mhc_dynamic_weights_backward(const void* x, int dtype_x, const fl
   if (int rc = hip_status(hipGetLastError(), "dynamic_weights_backward rows launch")) return rc;
   const bool phi_vec = aligned16(phi);
   const WidePlan w = wide_plan(R, K);
-  const bool mfma_ok =
-      dtype_x == MHC_DTYPE_BF16 && R >= kMfmaMinRows && K % 8 == 0 && aligned16(x) && (!grad_x || aligned16(grad_x));
+  const bool mfma_ok = (dtype_x == MHC_DTYPE_BF16 || dtype_x == MHC_DTYPE_F16) && R >= kMfmaMinRows && K % 8 == 0 &&
+                       aligned16(x) && (!grad_x || aligned16(grad_x));
   // the row chunks of the pass that runs (the MFMA plan has at most w.nR)
   const WidePlan pl = mfma_ok ? mfma_bwd_plan(R, K, w) : w;
   char* split_ws = (char*)workspace + align256((size_t)R * kRow * sizeof(float));
@@ -237,13 +242,18 @@ extern "C" int mhc_dynamic_weights_backward(const void* x, int dtype_x, const fl
   int rc;
   // (the kernel's buffer spans reach up to four blocks past a chunk's rows)
   if (mfma_ok && span_ok((pl.RC + 4 * kBwdRows) * K, 2) && span_ok((pl.RC + 4 * kBwdRows) * kRow, 4)) {
-    // bf16 rows in bulk: grad_x and grad_phi on MFMA.
+    // bf16 / fp16 rows in bulk: grad_x and grad_phi on MFMA.
     if (pl.nR > 1 && (grad_bias || grad_alpha))
       bias_part = (float*)(split_ws + align256((size_t)w.nR * K * kOut * sizeof(float)));
-    const unsigned ncb = (unsigned)((K + 32 * kBwdWaves - 1) / (32 * kBwdWaves));
-    dynw_bwd_mfma_kernel<><<<dim3(ncb, (unsigned)pl.nR), 64 * kBwdWaves, 0, st>>>(
-        (const __bf16*)x, phi, rowbuf, (__bf16*)grad_x, grad_phi, gphi_part, bias_part, grad_bias, grad_alpha, R, K,
-        pl.RC);
+    const dim3 grid((unsigned)((K + 32 * kBwdWaves - 1) / (32 * kBwdWaves)), (unsigned)pl.nR);
+    if (dtype_x == MHC_DTYPE_BF16)
+      dynw_bwd_mfma_kernel<__bf16><<<grid, 64 * kBwdWaves, 0, st>>>(
+          (const __bf16*)x, phi, rowbuf, (__bf16*)grad_x, grad_phi, gphi_part, bias_part, grad_bias, grad_alpha, R, K,
+          pl.RC);
+    else
+      dynw_bwd_mfma_kernel<_Float16><<<grid, 64 * kBwdWaves, 0, st>>>(
+          (const _Float16*)x, phi, rowbuf, (_Float16*)grad_x, grad_phi, gphi_part, bias_part, grad_bias, grad_alpha,
+          R, K, pl.RC);
     rc = hip_status(hipGetLastError(), "dynamic_weights_backward mfma launch");
   } else {
     rc = MHC_DISPATCH_DTYPE(dtype_x, [&] {

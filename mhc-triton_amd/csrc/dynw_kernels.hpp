@@ -90,8 +90,9 @@ __global__ __launch_bounds__(kThreads) void dynw_partial_kernel(const TX* __rest
 }
 
 // ---------------------------------------------------------------------------
-// MFMA projection for many bf16 rows (the standalone op at R = tokens): the
-// [R, K] x [K, 24] product on v_mfma_f32_32x32x16_bf16.  Fragment layout of
+// MFMA projection for many bf16 or fp16 rows (the standalone op at R = tokens):
+// the [R, K] x [K, 24] product on v_mfma_f32_32x32x16_bf16 (fp16 x is split
+// exactly into two bf16 parts in registers).  Fragment layout of
 // that instruction (gfx950, checked on the device):
 //   A: lane l, element j -> A[l % 32][8 (l / 32) + j]          (x rows)
 //   B: lane l, element j -> B[8 (l / 32) + j][l % 32]          (phi columns)
@@ -135,8 +136,8 @@ constexpr int kMfmaChunkSteps = kMfmaWaves * kMfmaSteps;  // steps per K chunk
 constexpr int kMfmaRedCols = kPart;                       // 24 dot products and the sum of squares
 constexpr int kMfmaRedPitch = 36;                         // floats per (wave, column): 32 rows + pad
 
-template <int NW = kMfmaWaves, int S = kMfmaSteps>
-__global__ __launch_bounds__(64 * NW, 2) void dynw_mfma_kernel(const __bf16* __restrict__ x,
+template <typename TX, int NW = kMfmaWaves, int S = kMfmaSteps>
+__global__ __launch_bounds__(64 * NW, 2) void dynw_mfma_kernel(const TX* __restrict__ x,
                                                              const float* __restrict__ phi,
                                                              float* __restrict__ part, int64_t R, int64_t K, int nK,
                                                              int64_t rows_per_wg) {
@@ -146,6 +147,8 @@ __global__ __launch_bounds__(64 * NW, 2) void dynw_mfma_kernel(const __bf16* __r
   constexpr int NL = 32 / RPL;  // loads per lane per tile
   static_assert(64 % L == 0 && 32 % RPL == 0, "slice shape");
   constexpr int kRedWave = kMfmaRedCols * kMfmaRedPitch;
+  constexpr bool kXF16 = __is_same(TX, _Float16);
+  static_assert(kXF16 || __is_same(TX, __bf16), "x is bf16 or fp16");
   __shared__ __attribute__((aligned(16))) u32x4 xt[NW][32 * L];
   __shared__ __attribute__((aligned(16))) float red[2][NW * kRedWave];
   const int wave = threadIdx.x >> 6;
@@ -176,7 +179,7 @@ __global__ __launch_bounds__(64 * NW, 2) void dynw_mfma_kernel(const __bf16* __r
   }
   u32x4 bf[S][3];  // filled below, while the first tiles' loads are in flight
   const int64_t ntile = (rend - rbeg + 31) / 32;
-  const Span<__bf16, true> xs(x + rbeg * K, (rend - rbeg) * K);
+  const Span<TX, true> xs(x + rbeg * K, (rend - rbeg) * K);
   const int lr = lane / L, lc = lane % L;
   // element offset of load j of tile t: (32 t + RPL j + lr) K + 16 s0 + 8 lc (past K: never used)
   const uint32_t lbase = (uint32_t)(lr * K + 16 * s0 + 8 * lc);
@@ -184,7 +187,7 @@ __global__ __launch_bounds__(64 * NW, 2) void dynw_mfma_kernel(const __bf16* __r
   u32x4 a[2][NL];
   auto aload = [&](int64_t t, u32x4 (&d)[NL]) {
 #pragma unroll
-    for (int j = 0; j < NL; ++j) d[j] = xs.load16<true>(lbase + (uint32_t)((32 * t + RPL * j) * K));
+    for (int j = 0; j < NL; ++j) d[j] = xs.template load16<true>(lbase + (uint32_t)((32 * t + RPL * j) * K));
   };
   auto astage = [&](const u32x4 (&d)[NL]) {
 #pragma unroll
@@ -209,17 +212,43 @@ __global__ __launch_bounds__(64 * NW, 2) void dynw_mfma_kernel(const __bf16* __r
     for (int i = 0; i < S; ++i) {
       if (i < nvalid) {
         const u32x4 d = tile[fr * L + ((2 * i + half) ^ (fr & (L - 1)))];
-        const bf16x8 av = __builtin_bit_cast(bf16x8, d);
-        // smallest part first: the step sum sees the corrections before the bulk
-        st = __builtin_amdgcn_mfma_f32_32x32x16_bf16(av, __builtin_bit_cast(bf16x8, bf[i][2]), st, 0, 0, 0);
-        st = __builtin_amdgcn_mfma_f32_32x32x16_bf16(av, __builtin_bit_cast(bf16x8, bf[i][1]), st, 0, 0, 0);
-        st = __builtin_amdgcn_mfma_f32_32x32x16_bf16(av, __builtin_bit_cast(bf16x8, bf[i][0]), st, 0, 0, 0);
+        const bf16x8 p_hi = __builtin_bit_cast(bf16x8, bf[i][0]);
+        const bf16x8 p_mid = __builtin_bit_cast(bf16x8, bf[i][1]);
+        const bf16x8 p_lo = __builtin_bit_cast(bf16x8, bf[i][2]);
+        if constexpr (kXF16) {
+          // fp16 x: each value splits exactly into bf16 hi + lo (11 significant bits,
+          // 8 in hi, the rest in lo, |lo| <= 2^-9 |x|; bf16 keeps fp32's exponent
+          // range).  Five products, smallest first; x_lo * phi_lo (2^-27 of x phi,
+          // the size of phi's own split residual) is dropped.
+          const f16x8 hv = __builtin_bit_cast(f16x8, d);
+          bf16x8 xh, xl;
 #pragma unroll
-        for (int c = 0; c < 4; ++c) {
-          const float lo_ = __uint_as_float(d[c] << 16);
-          const float hi_ = __uint_as_float(d[c] & 0xffff0000u);
-          ss = fmaf(lo_, lo_, ss);
-          ss_hi = fmaf(hi_, hi_, ss_hi);
+          for (int j = 0; j < 8; ++j) {
+            const float f = (float)hv[j];
+            const __bf16 h = (__bf16)f;
+            xh[j] = h;
+            xl[j] = (__bf16)(f - (float)h);  // exact
+            if (j & 1) ss_hi = fmaf(f, f, ss_hi);
+            else ss = fmaf(f, f, ss);
+          }
+          st = __builtin_amdgcn_mfma_f32_32x32x16_bf16(xh, p_lo, st, 0, 0, 0);
+          st = __builtin_amdgcn_mfma_f32_32x32x16_bf16(xl, p_mid, st, 0, 0, 0);
+          st = __builtin_amdgcn_mfma_f32_32x32x16_bf16(xh, p_mid, st, 0, 0, 0);
+          st = __builtin_amdgcn_mfma_f32_32x32x16_bf16(xl, p_hi, st, 0, 0, 0);
+          st = __builtin_amdgcn_mfma_f32_32x32x16_bf16(xh, p_hi, st, 0, 0, 0);
+        } else {
+          const bf16x8 av = __builtin_bit_cast(bf16x8, d);
+          // smallest part first: the step sum sees the corrections before the bulk
+          st = __builtin_amdgcn_mfma_f32_32x32x16_bf16(av, p_lo, st, 0, 0, 0);
+          st = __builtin_amdgcn_mfma_f32_32x32x16_bf16(av, p_mid, st, 0, 0, 0);
+          st = __builtin_amdgcn_mfma_f32_32x32x16_bf16(av, p_hi, st, 0, 0, 0);
+#pragma unroll
+          for (int c = 0; c < 4; ++c) {
+            const float lo_ = __uint_as_float(d[c] << 16);
+            const float hi_ = __uint_as_float(d[c] & 0xffff0000u);
+            ss = fmaf(lo_, lo_, ss);
+            ss_hi = fmaf(hi_, hi_, ss_hi);
+          }
         }
       }
     }
@@ -649,9 +678,10 @@ inline hipError_t launch_dynw_bwd_wide(const TX* x, const float* phi, const floa
   return hipGetLastError();
 }
 
-// The wide pass for many bf16 rows (the standalone op at R = tokens), both
-// products on MFMA (v_mfma_f32_32x32x16_bf16; fragment layout above):
-//   grad_x [R, K]  = G [R, 24] phi^T [24, K] + coef [R] x      (bf16 out)
+// The wide pass for many bf16 or fp16 rows (the standalone op at R = tokens),
+// both products on MFMA (v_mfma_f32_32x32x16_bf16; fragment layout above; fp16
+// x is split exactly into bf16 hi + lo for grad_phi):
+//   grad_x [R, K]  = G [R, 24] phi^T [24, K] + coef [R] x      (x's dtype out)
 //   grad_phi [K, 24] = x^T [K, R] G [R, 24]                      (f32, per chunk)
 // with G = grad_raw = rowbuf[r][0:24] and coef = rowbuf[r][24].  A workgroup
 // of kBwdWaves waves owns kBwdCols = 32 * kBwdWaves columns (wave w: the
@@ -705,11 +735,11 @@ __device__ __forceinline__ u32x2 lds_read_tr16(const __bf16* p) {
   return __builtin_bit_cast(u32x2, __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(p)));
 }
 
-template <int NW = kBwdWaves, int MINW = kBwdMinWaves>
-__global__ __launch_bounds__(64 * NW, MINW) void dynw_bwd_mfma_kernel(const __bf16* __restrict__ x,
+template <typename TX, int NW = kBwdWaves, int MINW = kBwdMinWaves>
+__global__ __launch_bounds__(64 * NW, MINW) void dynw_bwd_mfma_kernel(const TX* __restrict__ x,
                                                                     const float* __restrict__ phi,
                                                                     const float* __restrict__ rowbuf,
-                                                                    __bf16* __restrict__ gx, float* __restrict__ gphi,
+                                                                    TX* __restrict__ gx, float* __restrict__ gphi,
                                                                     float* __restrict__ gphi_part,
                                                                     float* __restrict__ bias_part,
                                                                     float* __restrict__ gbias,
@@ -725,6 +755,9 @@ __global__ __launch_bounds__(64 * NW, MINW) void dynw_bwd_mfma_kernel(const __bf
   constexpr int GRPP = kBwdThreads / 8;        // G rows per pass (8 lanes per 32-float row)
   constexpr int NG = TR / GRPP > 0 ? TR / GRPP : 1;
   static_assert(TR % XRPP == 0 && (TR % GRPP == 0 || GRPP >= TR), "block shape");
+  constexpr bool kXF16 = __is_same(TX, _Float16);
+  static_assert(kXF16 || __is_same(TX, __bf16), "x is bf16 or fp16");
+  // The x and grad_x tiles hold TX values; the G planes are bf16.
   __shared__ __attribute__((aligned(16))) __bf16 xs[TR * kBwdXPitch];
   __shared__ __attribute__((aligned(16))) __bf16 gxs[TR * kBwdXPitch];
   __shared__ __attribute__((aligned(16))) __bf16 ghi[TR * kBwdGPitch];
@@ -764,8 +797,8 @@ __global__ __launch_bounds__(64 * NW, MINW) void dynw_bwd_mfma_kernel(const __bf
   // before each block's staging hold for a path without them, so it waited for the next
   // block's loads as well.)
   const int64_t nrows = r_end - r_beg;
-  const Span<__bf16, true> xsp(x + r_beg * K, nrows * K);
-  const Span<__bf16, true> gxsp(gx ? gx + r_beg * K : x, gx ? nrows * K : 0);
+  const Span<TX, true> xsp(x + r_beg * K, nrows * K);
+  const Span<TX, true> gxsp(gx ? gx + r_beg * K : x, gx ? nrows * K : 0);
   const Span<float, true> gsp(rowbuf + r_beg * kRow, nrows * kRow);
   constexpr uint32_t kOobBf16 = 0x40000000u, kOobF32 = 0x20000000u;  // 2^31 bytes
   const int xr = threadIdx.x / XLPR;
@@ -781,7 +814,7 @@ __global__ __launch_bounds__(64 * NW, MINW) void dynw_bwd_mfma_kernel(const __bf
   };
   auto load_block = [&](int64_t b, u32x4 (&xv)[NX], f32x4 (&gv)[NG]) {
 #pragma unroll
-    for (int i = 0; i < NX; ++i) xv[i] = xsp.load16<true>(xoff(b, i));
+    for (int i = 0; i < NX; ++i) xv[i] = xsp.template load16<true>(xoff(b, i));
 #pragma unroll
     for (int j = 0; j < NG; ++j)
       gv[j] = __builtin_bit_cast(
@@ -863,11 +896,28 @@ __global__ __launch_bounds__(64 * NW, MINW) void dynw_bwd_mfma_kernel(const __bf
 #pragma unroll
       for (int hh = 0; hh < NH; ++hh) d[hh] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(bhi[js], ghv[hh][js], d[hh], 0, 0, 0);
     }
-    // grad_phi += x^T G over the steps (one chain, in step order).
+    // grad_phi += x^T G over the steps (one chain, in step order).  fp16 x splits exactly
+    // into bf16 hi + lo (|lo| <= 2^-9 |x|); x_lo * G_lo (2^-18 of x G, the size of G's own
+    // split residual) is dropped.
 #pragma unroll
     for (int st = 0; st < NST; ++st) {
-      dphi = __builtin_amdgcn_mfma_f32_32x32x16_bf16(pa[st], pbl[st], dphi, 0, 0, 0);
-      dphi = __builtin_amdgcn_mfma_f32_32x32x16_bf16(pa[st], pbh[st], dphi, 0, 0, 0);
+      if constexpr (kXF16) {
+        const f16x8 hv = __builtin_bit_cast(f16x8, pa[st]);
+        bf16x8 xh, xl;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+          const float f = (float)hv[j];
+          const __bf16 h = (__bf16)f;
+          xh[j] = h;
+          xl[j] = (__bf16)(f - (float)h);  // exact
+        }
+        dphi = __builtin_amdgcn_mfma_f32_32x32x16_bf16(xh, pbl[st], dphi, 0, 0, 0);
+        dphi = __builtin_amdgcn_mfma_f32_32x32x16_bf16(xl, pbh[st], dphi, 0, 0, 0);
+        dphi = __builtin_amdgcn_mfma_f32_32x32x16_bf16(xh, pbh[st], dphi, 0, 0, 0);
+      } else {
+        dphi = __builtin_amdgcn_mfma_f32_32x32x16_bf16(pa[st], pbl[st], dphi, 0, 0, 0);
+        dphi = __builtin_amdgcn_mfma_f32_32x32x16_bf16(pa[st], pbh[st], dphi, 0, 0, 0);
+      }
     }
     // Epilogue: lane l holds row l % 32 of its half, columns 32 wave + 8 q + 4 (l / 32) + 0..3
     // in d[hh][4 q ..].
@@ -878,18 +928,19 @@ __global__ __launch_bounds__(64 * NW, MINW) void dynw_bwd_mfma_kernel(const __bf
 #pragma unroll
       for (int q = 0; q < 4; ++q) {
         const int cc = 32 * wave + 8 * q + 4 * (lane >> 5);
-        const bf16x4 x4 = *reinterpret_cast<const bf16x4*>(&xs[row * kBwdXPitch + cc]);
-        bf16x4 o4;
+        typedef TX tx4 __attribute__((ext_vector_type(4)));
+        const tx4 x4 = *reinterpret_cast<const tx4*>(&xs[row * kBwdXPitch + cc]);
+        tx4 o4;
 #pragma unroll
-        for (int r = 0; r < 4; ++r) o4[r] = (__bf16)(d[hh][4 * q + r] + c * (float)x4[r]);
-        *reinterpret_cast<bf16x4*>(&gxs[row * kBwdXPitch + cc]) = o4;
+        for (int r = 0; r < 4; ++r) o4[r] = (TX)(d[hh][4 * q + r] + c * (float)x4[r]);
+        *reinterpret_cast<tx4*>(&gxs[row * kBwdXPitch + cc]) = o4;
       }
     }
     __syncthreads();
     // grad_x tile out: rows xr + XRPP i, 16 bytes at column xc (no grad_x: an empty span).
 #pragma unroll
     for (int i = 0; i < NX; ++i)
-      gxsp.store16<true>(xoff(b, i), *reinterpret_cast<const u32x4*>(&gxs[(xr + XRPP * i) * kBwdXPitch + xc]));
+      gxsp.template store16<true>(xoff(b, i), *reinterpret_cast<const u32x4*>(&gxs[(xr + XRPP * i) * kBwdXPitch + xc]));
     // No barrier here: every read of xs / ghi / glo / cf in this block came
     // before the barrier above, and gxs is next written after the next
     // block's first barrier, which waits for these reads.

@@ -204,7 +204,10 @@ def test_add_residual_forward_backward(dtype, bo_dtype, shape):
                                         # MFMA forward with rows in bulk: 9 chunks, the last one step
                                         # long (seven of its eight waves' slices past K), a last row
                                         # range of 11 tiles (an odd count, the last one partial)
-                                        (21845, 8208, torch.bfloat16)])
+                                        (21845, 8208, torch.bfloat16),
+                                        # fp16 rows on the MFMA kernels (x split into two bf16 parts)
+                                        (1000, 4096, torch.float16), (257, 3008, torch.float16),
+                                        (4096, 16384, torch.float16), (21845, 8208, torch.float16)])
 def test_dynamic_weights_forward_backward(R, K, xdtype):
     import mhc
 
@@ -235,19 +238,23 @@ def test_dynamic_weights_forward_backward(R, K, xdtype):
         # grad_x is formed in fp32 (on MFMA from split bf16 operands for R >= 64) and rounded
         # once to bf16: within half a bf16 ulp, 2^-9, of the largest element.
         assert rel_err(to_np(leaves[0].grad), gx) < 4e-3
+    if xdtype == torch.float16:
+        # likewise rounded once to fp16: half an fp16 ulp is 2^-12 of the largest element
+        assert rel_err(to_np(leaves[0].grad), gx) < 5e-4
     assert rel_err(to_np(leaves[1].grad), gphi) < 1e-4
     assert rel_err(to_np(leaves[2].grad), gbias) < 1e-4
     assert rel_err(np.array([a.grad.item() for a in leaves[3:]]), np.array(ga)) < 1e-4
 
 
-@pytest.mark.parametrize("R,K", [(1000, 4096), (257, 3008), (21845, 8208)])
-def test_dynamic_weights_mfma_paths_are_deterministic(R, K):
+@pytest.mark.parametrize("R,K,xdtype", [(1000, 4096, torch.bfloat16), (257, 3008, torch.bfloat16),
+                                        (21845, 8208, torch.bfloat16), (1000, 4096, torch.float16)])
+def test_dynamic_weights_mfma_paths_are_deterministic(R, K, xdtype):
     """The MFMA projection adds its waves' tile results and the K chunks in a fixed order, and the
     backward's grad_phi / bias partials likewise: two calls give the same bits."""
     import mhc
 
     g = gen(8)
-    x = randn((R, K), g, torch.bfloat16, scale=1 / 64)
+    x = randn((R, K), g, xdtype, scale=1 / 64)
     phi = randn((K, 24), g, scale=0.02)
     bias = randn((24,), g, scale=0.1)
     alphas = [torch.tensor([v], device=DEV) for v in (0.1, 0.2, 0.3)]
