@@ -32,10 +32,11 @@ static DynPlan dyn_plan(int64_t R, int64_t K) {
 
 static size_t align256(size_t v) { return (v + 255) & ~(size_t)255; }
 
-// MFMA plan for bf16 / fp16 x with many rows (dynw_mfma_kernel): K chunks of
-// kMfmaChunkSteps steps (1024 k), and row ranges of whole 32-row tiles so that
-// about kMfmaTargetWg workgroups run, one per CU (the kernel's LDS allows one).
-// At R = K = 16384: 16 chunks x 16 ranges of 1024 rows.
+// MFMA plan for x with many rows (dynw_mfma_kernel): K chunks of
+// mfma_steps(esize) * kMfmaWaves steps (1024 k for 16-bit x, 512 k for fp32),
+// and row ranges of whole 32-row tiles so that about kMfmaTargetWg workgroups
+// run, one per CU (the kernel's LDS allows one).
+// At R = K = 16384, 16-bit x: 16 chunks x 16 ranges of 1024 rows.
 constexpr int64_t kMfmaMinRows = 64;
 constexpr int64_t kMfmaTargetWg = 256;
 
@@ -47,21 +48,22 @@ struct MfmaPlan {
   size_t part_bytes;
 };
 
-static bool mfma_shape_ok(int64_t R, int64_t K) {
-  return R >= kMfmaMinRows && K > 0 && K % 16 == 0 && span_ok(32 * K, 2) && span_ok(K * kOut, 4);
+static bool mfma_shape_ok(int64_t R, int64_t K, int esize) {
+  return R >= kMfmaMinRows && K > 0 && K % 16 == 0 && span_ok(32 * K, esize) && span_ok(K * kOut, 4);
 }
 
-static MfmaPlan mfma_plan(int64_t R, int64_t K) {
+static MfmaPlan mfma_plan(int64_t R, int64_t K, int esize) {
   MfmaPlan p;
+  const int64_t chunk_steps = (int64_t)kMfmaWaves * mfma_steps(esize);
   p.nsteps = K / 16;
-  p.nK = (int)((p.nsteps + kMfmaChunkSteps - 1) / kMfmaChunkSteps);
+  p.nK = (int)((p.nsteps + chunk_steps - 1) / chunk_steps);
   if (p.nK < 1) p.nK = 1;
   const int64_t tiles = (R + 31) / 32;
   int64_t ngr = (kMfmaTargetWg + p.nK - 1) / p.nK;
   if (ngr > tiles) ngr = tiles;
   if (ngr < 1) ngr = 1;
   int64_t tpw = (tiles + ngr - 1) / ngr;
-  while (tpw > 1 && !span_ok(32 * tpw * K, 2)) tpw = (tpw + 1) / 2;
+  while (tpw > 1 && !span_ok(32 * tpw * K, esize)) tpw = (tpw + 1) / 2;
   p.rows_per_wg = 32 * tpw;
   p.ngr = (int)((R + p.rows_per_wg - 1) / p.rows_per_wg);
   p.part_bytes = align256((size_t)R * p.nK * kPart * sizeof(float));
@@ -78,10 +80,11 @@ extern "C" size_t mhc_dynamic_weights_workspace_bytes(int64_t R, int64_t K) {
   if (R <= 0) return 0;
   const DynPlan p = dyn_plan(R, K);
   size_t need = align256((size_t)R * p.nK * kPart * sizeof(float));
-  if (mfma_shape_ok(R, K)) {
-    const MfmaPlan m = mfma_plan(R, K);
-    if (m.part_bytes > need) need = m.part_bytes;
-  }
+  for (int esize : {2, 4})
+    if (mfma_shape_ok(R, K, esize)) {
+      const MfmaPlan m = mfma_plan(R, K, esize);
+      if (m.part_bytes > need) need = m.part_bytes;
+    }
   return need;
 }
 
@@ -105,17 +108,16 @@ extern "C" int mhc_dynamic_weights_forward(const void* x, int dtype_x, const flo
   hipStream_t st = (hipStream_t)stream;
   float* part = (float*)workspace;
   int nK = 0;
-  if ((dtype_x == MHC_DTYPE_BF16 || dtype_x == MHC_DTYPE_F16) && mfma_shape_ok(R, K) && aligned16(x)) {
-    // bf16 / fp16 rows in bulk: the projection on MFMA (HBM-bound instead of VALU-bound).
-    const MfmaPlan m = mfma_plan(R, K);
+  const int esize = dtype_x == MHC_DTYPE_F32 ? 4 : 2;
+  if (mfma_shape_ok(R, K, esize) && aligned16(x)) {
+    // rows in bulk: the projection on MFMA (HBM-bound instead of VALU-bound).
+    const MfmaPlan m = mfma_plan(R, K, esize);
     const dim3 grid((unsigned)m.ngr, (unsigned)m.nK);
-    if (dtype_x == MHC_DTYPE_BF16)
-      dynw_mfma_kernel<__bf16><<<grid, 64 * kMfmaWaves, 0, st>>>((const __bf16*)x, phi, part, R, K, m.nK,
-                                                                 m.rows_per_wg);
-    else
-      dynw_mfma_kernel<_Float16><<<grid, 64 * kMfmaWaves, 0, st>>>((const _Float16*)x, phi, part, R, K, m.nK,
-                                                                   m.rows_per_wg);
-    if (int rc = hip_status(hipGetLastError(), "dynamic_weights_forward mfma launch")) return rc;
+    int rc = MHC_DISPATCH_DTYPE(dtype_x, [&] {
+      dynw_mfma_kernel<T><<<grid, 64 * kMfmaWaves, 0, st>>>((const T*)x, phi, part, R, K, m.nK, m.rows_per_wg);
+      return hip_status(hipGetLastError(), "dynamic_weights_forward mfma launch");
+    });
+    if (rc) return rc;
     nK = m.nK;
   } else {
     const DynPlan p = dyn_plan(R, K);

@@ -131,24 +131,31 @@ typedef float f32x16 __attribute__((ext_vector_type(16)));
 // K % 16 == 0, a 16-byte aligned x, and rows_per_wg * K * 2 and K * 24 * 4
 // bytes under 2^31.
 constexpr int kMfmaWaves = 8;                             // waves per workgroup (2 per SIMD)
-constexpr int kMfmaSteps = 8;                             // 16-k steps per wave slice
-constexpr int kMfmaChunkSteps = kMfmaWaves * kMfmaSteps;  // steps per K chunk
+constexpr int kMfmaSteps = 8;                             // 16-k steps per wave slice (16-bit x)
+constexpr int kMfmaChunkSteps = kMfmaWaves * kMfmaSteps;  // steps per K chunk (16-bit x)
+// fp32 x: half the steps per slice, so that a slice is still 256 bytes of a row
+// and the LDS tiles keep their size
+__host__ __device__ constexpr int mfma_steps(int esize) { return esize == 4 ? kMfmaSteps / 2 : kMfmaSteps; }
 constexpr int kMfmaRedCols = kPart;                       // 24 dot products and the sum of squares
 constexpr int kMfmaRedPitch = 36;                         // floats per (wave, column): 32 rows + pad
 
-template <typename TX, int NW = kMfmaWaves, int S = kMfmaSteps>
+template <typename TX, int NW = kMfmaWaves, int S = mfma_steps(sizeof(TX))>
 __global__ __launch_bounds__(64 * NW, 2) void dynw_mfma_kernel(const TX* __restrict__ x,
                                                              const float* __restrict__ phi,
                                                              float* __restrict__ part, int64_t R, int64_t K, int nK,
                                                              int64_t rows_per_wg) {
   constexpr int kThr = 64 * NW;
-  constexpr int L = 2 * S;      // 16-byte chunks of a row in the wave's slice
-  constexpr int RPL = 64 / L;   // rows per load instruction
-  constexpr int NL = 32 / RPL;  // loads per lane per tile
+  constexpr int E = (int)sizeof(TX);
+  constexpr int VE = 16 / E;     // elements per 16-byte chunk
+  constexpr int CPF = 8 / VE;    // chunks per 8-element fragment
+  constexpr int L = S * E;       // 16-byte chunks of a row in the wave's slice (S * 16 elements)
+  constexpr int RPL = 64 / L;    // rows per load instruction
+  constexpr int NL = 32 / RPL;   // loads per lane per tile
   static_assert(64 % L == 0 && 32 % RPL == 0, "slice shape");
   constexpr int kRedWave = kMfmaRedCols * kMfmaRedPitch;
   constexpr bool kXF16 = __is_same(TX, _Float16);
-  static_assert(kXF16 || __is_same(TX, __bf16), "x is bf16 or fp16");
+  constexpr bool kXF32 = __is_same(TX, float);
+  static_assert(kXF16 || kXF32 || __is_same(TX, __bf16), "x is bf16, fp16 or fp32");
   __shared__ __attribute__((aligned(16))) u32x4 xt[NW][32 * L];
   __shared__ __attribute__((aligned(16))) float red[2][NW * kRedWave];
   const int wave = threadIdx.x >> 6;
@@ -181,8 +188,8 @@ __global__ __launch_bounds__(64 * NW, 2) void dynw_mfma_kernel(const TX* __restr
   const int64_t ntile = (rend - rbeg + 31) / 32;
   const Span<TX, true> xs(x + rbeg * K, (rend - rbeg) * K);
   const int lr = lane / L, lc = lane % L;
-  // element offset of load j of tile t: (32 t + RPL j + lr) K + 16 s0 + 8 lc (past K: never used)
-  const uint32_t lbase = (uint32_t)(lr * K + 16 * s0 + 8 * lc);
+  // element offset of load j of tile t: (32 t + RPL j + lr) K + 16 s0 + VE lc (past K: never used)
+  const uint32_t lbase = (uint32_t)(lr * K + 16 * s0 + VE * lc);
   u32x4* tile = xt[wave];
   u32x4 a[2][NL];
   auto aload = [&](int64_t t, u32x4 (&d)[NL]) {
@@ -211,11 +218,36 @@ __global__ __launch_bounds__(64 * NW, 2) void dynw_mfma_kernel(const TX* __restr
 #pragma unroll
     for (int i = 0; i < S; ++i) {
       if (i < nvalid) {
-        const u32x4 d = tile[fr * L + ((2 * i + half) ^ (fr & (L - 1)))];
+        const u32x4 d = tile[fr * L + ((CPF * (2 * i + half)) ^ (fr & (L - 1)))];
         const bf16x8 p_hi = __builtin_bit_cast(bf16x8, bf[i][0]);
         const bf16x8 p_mid = __builtin_bit_cast(bf16x8, bf[i][1]);
         const bf16x8 p_lo = __builtin_bit_cast(bf16x8, bf[i][2]);
-        if constexpr (kXF16) {
+        if constexpr (kXF32) {
+          // fp32 x: each value splits exactly into bf16 hi + mid + lo (24 significant
+          // bits, 8 per part).  Six products, smallest first; those below 2^-18 of
+          // x phi (x_mid * phi_lo, x_lo * phi_mid, x_lo * phi_lo: 2^-27 and less,
+          // the size of phi's own split residual) are dropped.
+          const u32x4 d1 = tile[fr * L + ((CPF * (2 * i + half) + 1) ^ (fr & (L - 1)))];
+          bf16x8 xh, xm, xl;
+#pragma unroll
+          for (int j = 0; j < 8; ++j) {
+            const float v = __uint_as_float(j < 4 ? d[j] : d1[j - 4]);
+            const __bf16 h = (__bf16)v;
+            const float r1 = v - (float)h;  // exact
+            const __bf16 m = (__bf16)r1;
+            xh[j] = h;
+            xm[j] = m;
+            xl[j] = (__bf16)(r1 - (float)m);  // exact
+            if (j & 1) ss_hi = fmaf(v, v, ss_hi);
+            else ss = fmaf(v, v, ss);
+          }
+          st = __builtin_amdgcn_mfma_f32_32x32x16_bf16(xh, p_lo, st, 0, 0, 0);
+          st = __builtin_amdgcn_mfma_f32_32x32x16_bf16(xm, p_mid, st, 0, 0, 0);
+          st = __builtin_amdgcn_mfma_f32_32x32x16_bf16(xl, p_hi, st, 0, 0, 0);
+          st = __builtin_amdgcn_mfma_f32_32x32x16_bf16(xh, p_mid, st, 0, 0, 0);
+          st = __builtin_amdgcn_mfma_f32_32x32x16_bf16(xm, p_hi, st, 0, 0, 0);
+          st = __builtin_amdgcn_mfma_f32_32x32x16_bf16(xh, p_hi, st, 0, 0, 0);
+        } else if constexpr (kXF16) {
           // fp16 x: each value splits exactly into bf16 hi + lo (11 significant bits,
           // 8 in hi, the rest in lo, |lo| <= 2^-9 |x|; bf16 keeps fp32's exponent
           // range).  Five products, smallest first; x_lo * phi_lo (2^-27 of x phi,

@@ -207,7 +207,13 @@ def test_add_residual_forward_backward(dtype, bo_dtype, shape):
                                         (21845, 8208, torch.bfloat16),
                                         # fp16 rows on the MFMA kernels (x split into two bf16 parts)
                                         (1000, 4096, torch.float16), (257, 3008, torch.float16),
-                                        (4096, 16384, torch.float16), (21845, 8208, torch.float16)])
+                                        (4096, 16384, torch.float16), (21845, 8208, torch.float16),
+                                        # fp32 rows on the MFMA projection (x in three bf16 parts,
+                                        # 512-k chunks): a last chunk of 28 steps (the last wave's
+                                        # slice past K), one step, a one-step last chunk
+                                        (1000, 4096, torch.float32), (257, 3008, torch.float32),
+                                        (65, 16, torch.float32), (21845, 8208, torch.float32),
+                                        (4096, 16384, torch.float32)])
 def test_dynamic_weights_forward_backward(R, K, xdtype):
     import mhc
 
@@ -247,7 +253,8 @@ def test_dynamic_weights_forward_backward(R, K, xdtype):
 
 
 @pytest.mark.parametrize("R,K,xdtype", [(1000, 4096, torch.bfloat16), (257, 3008, torch.bfloat16),
-                                        (21845, 8208, torch.bfloat16), (1000, 4096, torch.float16)])
+                                        (21845, 8208, torch.bfloat16), (1000, 4096, torch.float16),
+                                        (1000, 4096, torch.float32)])
 def test_dynamic_weights_mfma_paths_are_deterministic(R, K, xdtype):
     """The MFMA projection adds its waves' tile results and the K chunks in a fixed order, and the
     backward's grad_phi / bias partials likewise: two calls give the same bits."""
