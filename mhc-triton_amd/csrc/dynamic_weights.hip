@@ -161,7 +161,7 @@ static WidePlan wide_plan(int64_t R, int64_t K) {
   return p;
 }
 
-// Row chunks of the MFMA backward (dynw_bwd_mfma_kernel): one 8-wave workgroup
+// Row chunks of the MFMA backward (dynw_bwd_mfma_kernel, any x dtype): one 8-wave workgroup
 // fits a CU, so about kMfmaTargetWg workgroups, each walking a long chunk: its
 // pipeline fills and drains once per chunk, and fewer chunks leave fewer grad_phi
 // partials.  At R = K = 16384, 4 chunks of 4096 rows (256 workgroups) took
@@ -234,8 +234,8 @@ extern "C" int mhc_dynamic_weights_backward(const void* x, int dtype_x, const fl
   if (int rc = hip_status(hipGetLastError(), "dynamic_weights_backward rows launch")) return rc;
   const bool phi_vec = aligned16(phi);
   const WidePlan w = wide_plan(R, K);
-  const bool mfma_ok = (dtype_x == MHC_DTYPE_BF16 || dtype_x == MHC_DTYPE_F16) && R >= kMfmaMinRows && K % 8 == 0 &&
-                       aligned16(x) && (!grad_x || aligned16(grad_x));
+  const int esize = dtype_x == MHC_DTYPE_F32 ? 4 : 2;
+  const bool mfma_ok = R >= kMfmaMinRows && K % (16 / esize) == 0 && aligned16(x) && (!grad_x || aligned16(grad_x));
   // the row chunks of the pass that runs (the MFMA plan has at most w.nR)
   const WidePlan pl = mfma_ok ? mfma_bwd_plan(R, K, w) : w;
   char* split_ws = (char*)workspace + align256((size_t)R * kRow * sizeof(float));
@@ -243,20 +243,17 @@ extern "C" int mhc_dynamic_weights_backward(const void* x, int dtype_x, const fl
   float* bias_part = nullptr;  // MFMA path, split rows: per-chunk grad_bias / grad_alpha records
   int rc;
   // (the kernel's buffer spans reach up to four blocks past a chunk's rows)
-  if (mfma_ok && span_ok((pl.RC + 4 * kBwdRows) * K, 2) && span_ok((pl.RC + 4 * kBwdRows) * kRow, 4)) {
-    // bf16 / fp16 rows in bulk: grad_x and grad_phi on MFMA.
+  if (mfma_ok && span_ok((pl.RC + 4 * kBwdRows) * K, esize) && span_ok((pl.RC + 4 * kBwdRows) * kRow, 4)) {
+    // rows in bulk: grad_x and grad_phi on MFMA.
     if (pl.nR > 1 && (grad_bias || grad_alpha))
       bias_part = (float*)(split_ws + align256((size_t)w.nR * K * kOut * sizeof(float)));
     const dim3 grid((unsigned)((K + 32 * kBwdWaves - 1) / (32 * kBwdWaves)), (unsigned)pl.nR);
-    if (dtype_x == MHC_DTYPE_BF16)
-      dynw_bwd_mfma_kernel<__bf16><<<grid, 64 * kBwdWaves, 0, st>>>(
-          (const __bf16*)x, phi, rowbuf, (__bf16*)grad_x, grad_phi, gphi_part, bias_part, grad_bias, grad_alpha, R, K,
-          pl.RC);
-    else
-      dynw_bwd_mfma_kernel<_Float16><<<grid, 64 * kBwdWaves, 0, st>>>(
-          (const _Float16*)x, phi, rowbuf, (_Float16*)grad_x, grad_phi, gphi_part, bias_part, grad_bias, grad_alpha,
-          R, K, pl.RC);
-    rc = hip_status(hipGetLastError(), "dynamic_weights_backward mfma launch");
+    rc = MHC_DISPATCH_DTYPE(dtype_x, [&] {
+      dynw_bwd_mfma_kernel<T><<<grid, 64 * kBwdWaves, 0, st>>>((const T*)x, phi, rowbuf, (T*)grad_x, grad_phi,
+                                                               gphi_part, bias_part, grad_bias, grad_alpha, R, K,
+                                                               pl.RC);
+      return hip_status(hipGetLastError(), "dynamic_weights_backward mfma launch");
+    });
   } else {
     rc = MHC_DISPATCH_DTYPE(dtype_x, [&] {
       return hip_status(launch_dynw_bwd_wide<T, T>((const T*)x, phi, rowbuf, (T*)grad_x, grad_phi, gphi_part,

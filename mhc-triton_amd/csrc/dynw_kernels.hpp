@@ -90,9 +90,9 @@ __global__ __launch_bounds__(kThreads) void dynw_partial_kernel(const TX* __rest
 }
 
 // ---------------------------------------------------------------------------
-// MFMA projection for many bf16 or fp16 rows (the standalone op at R = tokens):
-// the [R, K] x [K, 24] product on v_mfma_f32_32x32x16_bf16 (fp16 x is split
-// exactly into two bf16 parts in registers).  Fragment layout of
+// MFMA projection for many rows (the standalone op at R = tokens): the
+// [R, K] x [K, 24] product on v_mfma_f32_32x32x16_bf16 (fp16 x is split
+// exactly into two bf16 parts in registers, fp32 x into three).  Fragment layout of
 // that instruction (gfx950, checked on the device):
 //   A: lane l, element j -> A[l % 32][8 (l / 32) + j]          (x rows)
 //   B: lane l, element j -> B[8 (l / 32) + j][l % 32]          (phi columns)
@@ -710,9 +710,9 @@ inline hipError_t launch_dynw_bwd_wide(const TX* x, const float* phi, const floa
   return hipGetLastError();
 }
 
-// The wide pass for many bf16 or fp16 rows (the standalone op at R = tokens),
-// both products on MFMA (v_mfma_f32_32x32x16_bf16; fragment layout above; fp16
-// x is split exactly into bf16 hi + lo for grad_phi):
+// The wide pass for many rows (the standalone op at R = tokens), both products
+// on MFMA (v_mfma_f32_32x32x16_bf16; fragment layout above; fp16 x is split
+// exactly into bf16 hi + lo for grad_phi, fp32 x into hi + mid):
 //   grad_x [R, K]  = G [R, 24] phi^T [24, K] + coef [R] x      (x's dtype out)
 //   grad_phi [K, 24] = x^T [K, R] G [R, 24]                      (f32, per chunk)
 // with G = grad_raw = rowbuf[r][0:24] and coef = rowbuf[r][24].  A workgroup
@@ -779,19 +779,24 @@ __global__ __launch_bounds__(64 * NW, MINW) void dynw_bwd_mfma_kernel(const TX* 
                                                                     int64_t RC) {
   constexpr int kBwdThreads = 64 * NW;
   constexpr int kBwdCols = 32 * NW;            // columns per workgroup
-  constexpr int kBwdXPitch = kBwdCols + 8;     // bf16 per padded LDS row of the x / grad_x tiles
+  constexpr int E = (int)sizeof(TX);
+  constexpr int VE = 16 / E;                   // x elements per 16-byte vector
+  constexpr int kBwdXPitch = kBwdCols + VE;    // elements per padded LDS row of the x / grad_x tiles
   constexpr int TR = kBwdRows;
-  constexpr int XLPR = kBwdCols / 8;           // lanes per x row (16 bytes each)
+  constexpr int XLPR = kBwdCols / VE;          // lanes per x row (16 bytes each)
   constexpr int XRPP = kBwdThreads / XLPR;     // x rows per pass of the workgroup
   constexpr int NX = TR / XRPP;                // 16-byte x vectors per lane per block
   constexpr int GRPP = kBwdThreads / 8;        // G rows per pass (8 lanes per 32-float row)
   constexpr int NG = TR / GRPP > 0 ? TR / GRPP : 1;
   static_assert(TR % XRPP == 0 && (TR % GRPP == 0 || GRPP >= TR), "block shape");
   constexpr bool kXF16 = __is_same(TX, _Float16);
-  static_assert(kXF16 || __is_same(TX, __bf16), "x is bf16 or fp16");
-  // The x and grad_x tiles hold TX values; the G planes are bf16.
-  __shared__ __attribute__((aligned(16))) __bf16 xs[TR * kBwdXPitch];
-  __shared__ __attribute__((aligned(16))) __bf16 gxs[TR * kBwdXPitch];
+  constexpr bool kXF32 = __is_same(TX, float);
+  static_assert(kXF16 || kXF32 || __is_same(TX, __bf16), "x is bf16, fp16 or fp32");
+  // Blocks of loads in flight: fp32 blocks are twice the bytes in the same registers.
+  constexpr int A = kXF32 ? 1 : kBwdAhead;
+  // The x and grad_x tiles hold TX values (fp32: 2 x 66.5 KiB of LDS); the G planes are bf16.
+  __shared__ __attribute__((aligned(16))) TX xs[TR * kBwdXPitch];
+  __shared__ __attribute__((aligned(16))) TX gxs[TR * kBwdXPitch];
   __shared__ __attribute__((aligned(16))) __bf16 ghi[TR * kBwdGPitch];
   __shared__ __attribute__((aligned(16))) __bf16 glo[TR * kBwdGPitch];
   __shared__ float cf[TR];
@@ -832,9 +837,9 @@ __global__ __launch_bounds__(64 * NW, MINW) void dynw_bwd_mfma_kernel(const TX* 
   const Span<TX, true> xsp(x + r_beg * K, nrows * K);
   const Span<TX, true> gxsp(gx ? gx + r_beg * K : x, gx ? nrows * K : 0);
   const Span<float, true> gsp(rowbuf + r_beg * kRow, nrows * kRow);
-  constexpr uint32_t kOobBf16 = 0x40000000u, kOobF32 = 0x20000000u;  // 2^31 bytes
+  constexpr uint32_t kOobX = 0x80000000u / E, kOobF32 = 0x20000000u;  // 2^31 bytes
   const int xr = threadIdx.x / XLPR;
-  const int xc = (threadIdx.x % XLPR) * 8;
+  const int xc = (threadIdx.x % XLPR) * VE;
   const bool xcol_ok = k0 + xc < K;
   const int grow = threadIdx.x >> 3;
   const int gcol = (threadIdx.x & 7) * 4;
@@ -842,7 +847,7 @@ __global__ __launch_bounds__(64 * NW, MINW) void dynw_bwd_mfma_kernel(const TX* 
   const bool gld_ok = g_ok && gcol < 28;
   // element offsets in the spans of row i of this lane in block b
   auto xoff = [&](int64_t b, int i) -> uint32_t {
-    return xcol_ok ? (uint32_t)((TR * b + xr + XRPP * i) * K + k0 + xc) : kOobBf16;
+    return xcol_ok ? (uint32_t)((TR * b + xr + XRPP * i) * K + k0 + xc) : kOobX;
   };
   auto load_block = [&](int64_t b, u32x4 (&xv)[NX], f32x4 (&gv)[NG]) {
 #pragma unroll
@@ -885,22 +890,32 @@ __global__ __launch_bounds__(64 * NW, MINW) void dynw_bwd_mfma_kernel(const TX* 
       }
     }
     __syncthreads();
-    load_block(b + kBwdAhead, xv, gv);  // in flight during the compute below
+    load_block(b + A, xv, gv);  // in flight during the compute below
     // grad_phi operands for the block's 16-row steps, read before the grad_x work so that their
     // LDS latency overlaps it.  A = x^T (lane l: column 32 wave + l % 32, rows
-    // 16 st + 8 (l / 32) + e), B = G (same rows, j = l % 32).
+    // 16 st + 8 (l / 32) + e), B = G (same rows, j = l % 32).  16-bit x comes through the
+    // transpose read; fp32 x as eight 4-byte reads per step (consecutive lanes, consecutive
+    // columns).
     constexpr int NST = TR / 16;
     bf16x8 pa[NST], pbh[NST], pbl[NST];
+    float pa32[kXF32 ? NST : 1][8];
 #pragma unroll
     for (int st = 0; st < NST; ++st) {
       const int rb = 16 * st + tr_row;
-      const u32x2 x0 = lds_read_tr16(&xs[rb * kBwdXPitch + 32 * wave + tr_col]);
-      const u32x2 x1 = lds_read_tr16(&xs[(rb + 4) * kBwdXPitch + 32 * wave + tr_col]);
+      if constexpr (kXF32) {
+#pragma unroll
+        for (int e = 0; e < 8; ++e)
+          pa32[st][e] = xs[(16 * st + 8 * (lane >> 5) + e) * kBwdXPitch + 32 * wave + (lane & 31)];
+      } else {
+        const u32x2 x0 = lds_read_tr16(reinterpret_cast<const __bf16*>(&xs[rb * kBwdXPitch + 32 * wave + tr_col]));
+        const u32x2 x1 =
+            lds_read_tr16(reinterpret_cast<const __bf16*>(&xs[(rb + 4) * kBwdXPitch + 32 * wave + tr_col]));
+        pa[st] = __builtin_bit_cast(bf16x8, u32x4{x0[0], x0[1], x1[0], x1[1]});
+      }
       const u32x2 h0 = lds_read_tr16(&ghi[rb * kBwdGPitch + tr_col]);
       const u32x2 h1 = lds_read_tr16(&ghi[(rb + 4) * kBwdGPitch + tr_col]);
       const u32x2 q0 = lds_read_tr16(&glo[rb * kBwdGPitch + tr_col]);
       const u32x2 q1 = lds_read_tr16(&glo[(rb + 4) * kBwdGPitch + tr_col]);
-      pa[st] = __builtin_bit_cast(bf16x8, u32x4{x0[0], x0[1], x1[0], x1[1]});
       pbh[st] = __builtin_bit_cast(bf16x8, u32x4{h0[0], h0[1], h1[0], h1[1]});
       pbl[st] = __builtin_bit_cast(bf16x8, u32x4{q0[0], q0[1], q1[0], q1[1]});
     }
@@ -933,7 +948,21 @@ __global__ __launch_bounds__(64 * NW, MINW) void dynw_bwd_mfma_kernel(const TX* 
     // split residual) is dropped.
 #pragma unroll
     for (int st = 0; st < NST; ++st) {
-      if constexpr (kXF16) {
+      if constexpr (kXF32) {
+        // fp32 x: bf16 hi + mid parts (x_lo * G_hi and x_mid * G_lo, 2^-18 of x G, are dropped
+        // as above)
+        bf16x8 xh, xm;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+          const float v = pa32[st][j];
+          const __bf16 h = (__bf16)v;
+          xh[j] = h;
+          xm[j] = (__bf16)(v - (float)h);
+        }
+        dphi = __builtin_amdgcn_mfma_f32_32x32x16_bf16(xh, pbl[st], dphi, 0, 0, 0);
+        dphi = __builtin_amdgcn_mfma_f32_32x32x16_bf16(xm, pbh[st], dphi, 0, 0, 0);
+        dphi = __builtin_amdgcn_mfma_f32_32x32x16_bf16(xh, pbh[st], dphi, 0, 0, 0);
+      } else if constexpr (kXF16) {
         const f16x8 hv = __builtin_bit_cast(f16x8, pa[st]);
         bf16x8 xh, xl;
 #pragma unroll
@@ -977,10 +1006,8 @@ __global__ __launch_bounds__(64 * NW, MINW) void dynw_bwd_mfma_kernel(const TX* 
     // before the barrier above, and gxs is next written after the next
     // block's first barrier, which waits for these reads.
   };
-  // Blocks rotate through kBwdAhead register sets, each refilled with the block kBwdAhead
-  // ahead; the loop runs a multiple of kBwdAhead blocks (those past the chunk read zeros and
-  // store nothing).
-  constexpr int A = kBwdAhead;
+  // Blocks rotate through A register sets, each refilled with the block A ahead; the loop
+  // runs a multiple of A blocks (those past the chunk read zeros and store nothing).
   u32x4 xv[A][NX];
   f32x4 gv[A][NG];
   const int64_t nblk = (nrows + TR - 1) / TR;

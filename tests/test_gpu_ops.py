@@ -208,9 +208,10 @@ def test_add_residual_forward_backward(dtype, bo_dtype, shape):
                                         # fp16 rows on the MFMA kernels (x split into two bf16 parts)
                                         (1000, 4096, torch.float16), (257, 3008, torch.float16),
                                         (4096, 16384, torch.float16), (21845, 8208, torch.float16),
-                                        # fp32 rows on the MFMA projection (x in three bf16 parts,
-                                        # 512-k chunks): a last chunk of 28 steps (the last wave's
-                                        # slice past K), one step, a one-step last chunk
+                                        # fp32 rows on the MFMA kernels (x in three bf16 parts
+                                        # forward, 512-k chunks): a last chunk of 28 steps (the last
+                                        # wave's slice past K), one step, a one-step last chunk;
+                                        # backward column blocks of 16 and 192 columns
                                         (1000, 4096, torch.float32), (257, 3008, torch.float32),
                                         (65, 16, torch.float32), (21845, 8208, torch.float32),
                                         (4096, 16384, torch.float32)])
@@ -238,6 +239,9 @@ def test_dynamic_weights_forward_backward(R, K, xdtype):
     # result for H_res.  Outputs from bf16/fp16 x may be 2e-2 off; hold them to 5e-5.
     assert rel_err(to_np(H_res), orr) < (1e-5 if xdtype == torch.float32 else 5e-5)
     gx, gphi, gbias, ga = O.dynamic_weights_backward(*args, to_np(gp), to_np(gq), to_np(gr), 20, 1e-6)
+    print(f"dynamic weights R={R} K={K} {xdtype}: H_res {rel_err(to_np(H_res), orr):.2e} "
+          f"grad_x {rel_err(to_np(leaves[0].grad), gx):.2e} grad_phi {rel_err(to_np(leaves[1].grad), gphi):.2e}",
+          flush=True)
     assert leaves[0].grad.dtype == xdtype
     assert rel_err(to_np(leaves[0].grad), gx) < GTOL[xdtype]
     if xdtype == torch.bfloat16:
