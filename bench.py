@@ -399,6 +399,21 @@ def _ops_leg(n: int = 20, warm: int = 3) -> dict:
 
     # x read by the forward, x read and grad_x written by the backward
     rec("dynamic_weights_fwd+bwd R=16384 K=16384 bf16", timed(fwd_bwd), 3 * T * 4 * D * e)
+    del xt, xl
+    # the same op on fp16 and fp32 rows (the MFMA kernels split x into bf16 parts in registers)
+    for dt, tag in ((torch.float16, "f16"), (torch.float32, "f32")):
+        xd = torch.randn((T, 4 * D), generator=g, device=dev).to(dt)
+        nb = T * 4 * D * xd.element_size()
+        rec(f"dynamic_weights_fwd R=16384 K=16384 {tag}",
+            timed(lambda: K.fused_dynamic_weights_forward(xd, phi, bias, *al)), nb)
+        xdl = xd.clone().requires_grad_(True)
+
+        def fwd_bwd_d():
+            o = mhc.fused_dynamic_weights(xdl, phl, bias, *al)
+            torch.autograd.grad(o, [xdl, phl], gs)
+
+        rec(f"dynamic_weights_fwd+bwd R=16384 K=16384 {tag}", timed(fwd_bwd_d), 3 * nb)
+        del xd, xdl
     return out
 
 
