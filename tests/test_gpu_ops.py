@@ -214,7 +214,10 @@ def test_add_residual_forward_backward(dtype, bo_dtype, shape):
                                         # backward column blocks of 16 and 192 columns
                                         (1000, 4096, torch.float32), (257, 3008, torch.float32),
                                         (65, 16, torch.float32), (21845, 8208, torch.float32),
-                                        (4096, 16384, torch.float32)])
+                                        (4096, 16384, torch.float32),
+                                        # K % 16 = 8: the VALU projection forward, the MFMA backward
+                                        # with a last column block of 232 columns
+                                        (100, 1000, torch.float32), (100, 1000, torch.float16)])
 def test_dynamic_weights_forward_backward(R, K, xdtype):
     import mhc
 
