@@ -128,8 +128,8 @@ typedef float f32x16 __attribute__((ext_vector_type(16)));
 // squares [24], which the VALU forms from the A fragments alongside the MFMAs
 // (v_dot2_f32_bf16 would take a quarter of the instructions, but its sums are
 // not fp32-accurate: H_pre moved by 6e-3 relative at K = 4096).  Requires
-// K % 16 == 0, a 16-byte aligned x, and rows_per_wg * K * 2 and K * 24 * 4
-// bytes under 2^31.
+// K % 16 == 0, a 16-byte aligned x, and rows_per_wg * K * sizeof(x) and
+// K * 24 * 4 bytes under 2^31.
 constexpr int kMfmaWaves = 8;                             // waves per workgroup (2 per SIMD)
 constexpr int kMfmaSteps = 8;                             // 16-k steps per wave slice (16-bit x)
 constexpr int kMfmaChunkSteps = kMfmaWaves * kMfmaSteps;  // steps per K chunk (16-bit x)
@@ -744,8 +744,8 @@ inline hipError_t launch_dynw_bwd_wide(const TX* x, const float* phi, const floa
 // 4096 rows (one workgroup per CU), 200 us with 16 chunks of 1024; with 16
 // chunks, copies of it without the grad_x stores took 168 us and without the
 // MFMA work 181 us, against 170 us for a plain copy of the same strips
-// (1024 workgroups).  Requires K % 8 == 0 and
-// 16-byte aligned x and grad_x.  Grid (K / kBwdCols column blocks, row
+// (1024 workgroups).  Requires K a multiple of 16 bytes of x (8 elements of
+// 16-bit x, 4 of fp32) and 16-byte aligned x and grad_x.  Grid (K / kBwdCols column blocks, row
 // chunks); outputs as dynw_bwd_wide_kernel: grad_phi direct with one chunk,
 // else per-chunk partials.  Column block 0 of each row chunk also sums the
 // chunk's grad_bias / grad_alpha records after its main loop: into gbias /
