@@ -198,7 +198,8 @@ def _stream_ceiling(tokens: int, row_bytes: int, caps=(0, 2, 3, 4, 6, 8), reps: 
 
 
 DYNW_FWD_MODES = {0: "loads only", 1: "+ LDS staging and fragment reads", 2: "+ one workgroup barrier per tile",
-                  3: "+ split-K records (32 rows x 25 floats per tile and K chunk)"}
+                  3: "+ split-K records (32 rows x 25 floats per tile and K chunk)",
+                  4: "+ the same records chunk-major, stored as 16-byte vectors"}
 DYNW_BWD_MODES = {0: "read only", 1: "copy (each vector stored back in place to grad_x)",
                   2: "copy through LDS tiles with two barriers per block",
                   3: "copy through LDS tiles doubled by block parity, both blocks of a pair stored together"}

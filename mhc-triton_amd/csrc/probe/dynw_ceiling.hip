@@ -14,6 +14,7 @@
 //        the kernel lays them out) and come back in fragment order
 //   2  + one workgroup barrier per tile
 //   3  + the split-K records: 32 rows x 25 floats per tile and K chunk
+//   4  as 3 with the records chunk-major and stored as 16-byte vectors
 // Backward (dynw_bwd_mfma_kernel's pattern): grid (256-column blocks, row
 // chunks), 8 waves; each workgroup walks its rows in 64-row blocks of
 // 512-byte strips, two blocks of loads in flight:
@@ -83,7 +84,7 @@ __global__ __launch_bounds__(kFwdThreads, 2) void dynw_fwd_pattern_kernel(const 
 #pragma unroll
       for (int i = 0; i < kFwdSteps; ++i) acc ^= tile[fr * kL + ((2 * i + half) ^ (fr & (kL - 1)))];
       if constexpr (MODE >= 2) __syncthreads();
-      if constexpr (MODE >= 3) {
+      if constexpr (MODE == 3) {
         const float v = (float)(acc.x & 0xffu);
 #pragma unroll
         for (int q = 0; q < (32 * mhc::kPart + kFwdThreads - 1) / kFwdThreads; ++q) {
@@ -93,6 +94,18 @@ __global__ __launch_bounds__(kFwdThreads, 2) void dynw_fwd_pattern_kernel(const 
             const int64_t r = rbeg + 32 * t + row;
             if (r < rend) part[(r * nK + kc) * mhc::kPart + c] = v;
           }
+        }
+      } else if constexpr (MODE == 4) {
+        // the same records chunk-major ([chunk][row][25]: a tile's 32 records are 800
+        // consecutive floats), each of 200 threads storing 16 bytes
+        const float v = (float)(acc.x & 0xffu);
+        constexpr int kVec = 32 * mhc::kPart / 4;
+        if (threadIdx.x < kVec) {
+          const int64_t r0 = rbeg + 32 * t;
+          const int64_t nrec = rend - r0 < 32 ? rend - r0 : 32;
+          if (4 * threadIdx.x + 4 <= nrec * mhc::kPart)  // whole vectors inside the range only
+            *reinterpret_cast<mhc::f32x4*>(part + ((int64_t)kc * R + r0) * mhc::kPart + 4 * threadIdx.x) =
+                mhc::f32x4{v, v, v, v};
         }
       }
     }
@@ -236,7 +249,7 @@ extern "C" int mhc_probe_dynw(int pattern, int mode, const void* x, void* out, i
   unsigned* s = (unsigned*)sink;
   if (pattern == 0) {
     const int nK = (int)((K / 16 + kFwdWaves * kFwdSteps - 1) / (kFwdWaves * kFwdSteps));
-    if (mode == 3 && !out) return 1;
+    if (mode >= 3 && !out) return 1;
     const dim3 grid((unsigned)((R + rows - 1) / rows), (unsigned)nK);
     const __bf16* xb = (const __bf16*)x;
     float* p = (float*)out;
@@ -245,6 +258,7 @@ extern "C" int mhc_probe_dynw(int pattern, int mode, const void* x, void* out, i
       case 1: dynw_fwd_pattern_kernel<1><<<grid, kFwdThreads, kFwdLds, st>>>(xb, p, R, K, nK, rows, s); break;
       case 2: dynw_fwd_pattern_kernel<2><<<grid, kFwdThreads, kFwdLds, st>>>(xb, p, R, K, nK, rows, s); break;
       case 3: dynw_fwd_pattern_kernel<3><<<grid, kFwdThreads, kFwdLds, st>>>(xb, p, R, K, nK, rows, s); break;
+      case 4: dynw_fwd_pattern_kernel<4><<<grid, kFwdThreads, kFwdLds, st>>>(xb, p, R, K, nK, rows, s); break;
       default: return 1;
     }
   } else if (pattern == 1) {

@@ -94,9 +94,10 @@ def test_dynw_backward_probe_copies_every_strip(mode, R, K, rows):
     assert torch.equal(gx.view(torch.int32).reshape(R, K // 8, 4), want)
 
 
+@pytest.mark.parametrize("mode", [3, 4])
 @pytest.mark.parametrize("R,K,rows", [(1000, 2048, 320), (96, 1040, 64)])
-def test_dynw_forward_probe_writes_every_record(R, K, rows):
-    """The forward pattern's mode 3 writes one 25-float record per row and K chunk, as the
+def test_dynw_forward_probe_writes_every_record(mode, R, K, rows):
+    """The forward pattern's modes 3 and 4 write one 25-float record per row and K chunk, as the
     projection kernel does: its tile loop covers every row of every range."""
     lib = ctypes.CDLL(PROBE)
     fn = lib.mhc_probe_dynw
@@ -106,7 +107,7 @@ def test_dynw_forward_probe_writes_every_record(R, K, rows):
     x = torch.ones((R, K), device="cuda", dtype=torch.bfloat16)
     part = torch.full((R * nK * 25,), float("nan"), device="cuda")
     sink = torch.zeros(256, dtype=torch.int32, device="cuda")
-    assert fn(0, 3, x.data_ptr(), part.data_ptr(), R, K, rows, sink.data_ptr(),
+    assert fn(0, mode, x.data_ptr(), part.data_ptr(), R, K, rows, sink.data_ptr(),
               torch.cuda.current_stream().cuda_stream) == 0
     torch.cuda.synchronize()
     assert not part.isnan().any()
