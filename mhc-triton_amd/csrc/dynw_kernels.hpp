@@ -91,9 +91,10 @@ __global__ __launch_bounds__(kThreads) void dynw_partial_kernel(const TX* __rest
 
 // ---------------------------------------------------------------------------
 // MFMA projection for many rows (the standalone op at R = tokens): the
-// [R, K] x [K, 24] product on v_mfma_f32_32x32x16_bf16 (fp16 x is split
-// exactly into two bf16 parts in registers, fp32 x into three).  Fragment layout of
-// that instruction (gfx950, checked on the device):
+// [R, K] x [K, 24] product on v_mfma_f32_32x32x16_bf16 (fp32 x is split
+// exactly into three bf16 parts in registers; fp16 x goes through
+// v_mfma_f32_32x32x16_f16 against a scaled two-part phi, below).  Fragment
+// layout of these instructions (gfx950, checked on the device):
 //   A: lane l, element j -> A[l % 32][8 (l / 32) + j]          (x rows)
 //   B: lane l, element j -> B[8 (l / 32) + j][l % 32]          (phi columns)
 //   D: lane l, element i -> D[8 (i / 4) + 4 (l / 32) + i % 4][l % 32]
@@ -185,6 +186,7 @@ __global__ __launch_bounds__(64 * NW, 2) void dynw_mfma_kernel(const TX* __restr
       }
   }
   u32x4 bf[S][3];  // filled below, while the first tiles' loads are in flight
+  float unscale = 1.f;  // fp16 x: 1 / s of this lane's column (below)
   const int64_t ntile = (rend - rbeg + 31) / 32;
   const Span<TX, true> xs(x + rbeg * K, (rend - rbeg) * K);
   const int lr = lane / L, lc = lane % L;
@@ -211,9 +213,9 @@ __global__ __launch_bounds__(64 * NW, 2) void dynw_mfma_kernel(const TX* __restr
   // Tile t: its fragments from the wave's LDS tile, the chain, and the wave's
   // results into red[buf]; then the workgroup adds the NW records of each output.
   auto tile_compute = [&](int64_t t, int buf) {
-    f32x16 st;
+    f32x16 st, st2;  // st2: the fp16 path's p2 products
 #pragma unroll
-    for (int i = 0; i < 16; ++i) st[i] = 0.f;
+    for (int i = 0; i < 16; ++i) st[i] = st2[i] = 0.f;
     float ss = 0.f, ss_hi = 0.f;
 #pragma unroll
     for (int i = 0; i < S; ++i) {
@@ -248,26 +250,16 @@ __global__ __launch_bounds__(64 * NW, 2) void dynw_mfma_kernel(const TX* __restr
           st = __builtin_amdgcn_mfma_f32_32x32x16_bf16(xm, p_hi, st, 0, 0, 0);
           st = __builtin_amdgcn_mfma_f32_32x32x16_bf16(xh, p_hi, st, 0, 0, 0);
         } else if constexpr (kXF16) {
-          // fp16 x: each value splits exactly into bf16 hi + lo (11 significant bits,
-          // 8 in hi, the rest in lo, |lo| <= 2^-9 |x|; bf16 keeps fp32's exponent
-          // range).  Five products, smallest first; x_lo * phi_lo (2^-27 of x phi,
-          // the size of phi's own split residual) is dropped.
+          // fp16 x: x as loaded against the two scaled fp16 parts of phi
           const f16x8 hv = __builtin_bit_cast(f16x8, d);
-          bf16x8 xh, xl;
+          st2 = __builtin_amdgcn_mfma_f32_32x32x16_f16(hv, __builtin_bit_cast(f16x8, bf[i][1]), st2, 0, 0, 0);
+          st = __builtin_amdgcn_mfma_f32_32x32x16_f16(hv, __builtin_bit_cast(f16x8, bf[i][0]), st, 0, 0, 0);
 #pragma unroll
           for (int j = 0; j < 8; ++j) {
             const float f = (float)hv[j];
-            const __bf16 h = (__bf16)f;
-            xh[j] = h;
-            xl[j] = (__bf16)(f - (float)h);  // exact
             if (j & 1) ss_hi = fmaf(f, f, ss_hi);
             else ss = fmaf(f, f, ss);
           }
-          st = __builtin_amdgcn_mfma_f32_32x32x16_bf16(xh, p_lo, st, 0, 0, 0);
-          st = __builtin_amdgcn_mfma_f32_32x32x16_bf16(xl, p_mid, st, 0, 0, 0);
-          st = __builtin_amdgcn_mfma_f32_32x32x16_bf16(xh, p_mid, st, 0, 0, 0);
-          st = __builtin_amdgcn_mfma_f32_32x32x16_bf16(xl, p_hi, st, 0, 0, 0);
-          st = __builtin_amdgcn_mfma_f32_32x32x16_bf16(xh, p_hi, st, 0, 0, 0);
         } else {
           const bf16x8 av = __builtin_bit_cast(bf16x8, d);
           // smallest part first: the step sum sees the corrections before the bulk
@@ -283,6 +275,10 @@ __global__ __launch_bounds__(64 * NW, 2) void dynw_mfma_kernel(const TX* __restr
           }
         }
       }
+    }
+    if constexpr (kXF16) {  // x (p1 + 2^-11 p2) / s, exact scalings
+#pragma unroll
+      for (int i = 0; i < 16; ++i) st[i] = fmaf(st2[i], 1.f / 2048.f, st[i]) * unscale;
     }
     float* rw = red[buf] + wave * kRedWave;
     // lane l holds column l % 32, rows 8 q + 4 (l / 32) + 0..3 in st[4 q .. 4 q + 3]
@@ -327,7 +323,41 @@ __global__ __launch_bounds__(64 * NW, 2) void dynw_mfma_kernel(const TX* __restr
   aload(1, a[1]);
   __builtin_amdgcn_sched_barrier(0);
   // phi in three bf16 parts, phi = hi + mid + lo + O(2^-27 |phi|), while the
-  // first two tiles' loads are in flight
+  // first two tiles' loads are in flight.  fp16 x instead: the f16 MFMA takes x
+  // as it is, and phi goes in as two fp16 parts of its column scaled by a power
+  // of two, s phi = p1 + 2^-11 p2 + O(2^-22 |s phi|), with s chosen per wave
+  // slice and column so that the column's largest |s phi| lies in [2^14, 2^15)
+  // (no fp16 overflow); the two products accumulate apart and meet, unscaled,
+  // at the end of each tile.
+  if constexpr (kXF16) {
+    float mx = 0.f;
+#pragma unroll
+    for (int i = 0; i < S; ++i)
+#pragma unroll
+      for (int j = 0; j < 8; ++j) mx = fmaxf(mx, fabsf(__uint_as_float(pv[i][j])));
+    mx = fmaxf(mx, __shfl_xor(mx, 32, 64));  // lanes l and l + 32 hold one column
+    int ex = 0;
+    if (mx > 0.f) frexpf(mx, &ex);  // mx in [2^(ex-1), 2^ex)
+    // s = 2^(15 - ex), held to 2^126 so that s and 1 / s stay finite and normal
+    // (a column below 2^-111 then scales into [2^-112, 2^15), still fp16 normals
+    // down to 2^-126 of its largest entry)
+    const int es = mx > 0.f ? min(15 - ex, 126) : 0;
+    const float sc = ldexpf(1.f, es);
+    unscale = ldexpf(1.f, -es);
+#pragma unroll
+    for (int i = 0; i < S; ++i) {
+      f16x8 p1, p2;
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        const float v = __uint_as_float(pv[i][j]) * sc;  // exact
+        const _Float16 h = (_Float16)v;
+        p1[j] = h;
+        p2[j] = (_Float16)((v - (float)h) * 2048.f);  // v - h exact
+      }
+      bf[i][0] = __builtin_bit_cast(u32x4, p1);
+      bf[i][1] = __builtin_bit_cast(u32x4, p2);
+    }
+  } else {
 #pragma unroll
   for (int i = 0; i < S; ++i) {
     bf16x8 hi, mid, lo;
@@ -344,6 +374,7 @@ __global__ __launch_bounds__(64 * NW, 2) void dynw_mfma_kernel(const TX* __restr
     bf[i][0] = __builtin_bit_cast(u32x4, hi);
     bf[i][1] = __builtin_bit_cast(u32x4, mid);
     bf[i][2] = __builtin_bit_cast(u32x4, lo);
+  }
   }
   for (int64_t t = 0; t < ntile; t += 2) {
     astage(a[0]);

@@ -283,6 +283,37 @@ def test_dynamic_weights_mfma_paths_are_deterministic(R, K, xdtype):
         assert torch.equal(a, b)
 
 
+@pytest.mark.parametrize("xdtype", [torch.float16, torch.bfloat16, torch.float32])
+def test_dynamic_weights_projection_over_a_wide_phi_range(xdtype):
+    """The MFMA projection (aux[:, :24] = x phi) per column, against float64, for phi columns
+    far outside fp16's range (1e5), far below it (1e-9, and for fp16 x 1e-36), all zero, and
+    N(0, 0.02): the fp16 path scales each column by a power of two before splitting it into
+    fp16 parts, the bf16 / fp32 paths split it into bf16 parts (fp32's exponent range)."""
+    from mhc import _kernels as K_
+
+    R, K = 256, 2048
+    g = gen(11)
+    x = randn((R, K), g, xdtype, scale=1 / 64)
+    phi = randn((K, 24), g, scale=0.02)
+    phi[:, 0] *= 5e6
+    phi[:, 1] *= 5e-8
+    phi[:, 2] = 0.0
+    phi[::7, 3] *= 1e4  # one column with a few large entries among ordinary ones
+    if xdtype == torch.float16:
+        phi[:, 4] *= 5e-35  # largest entry near 2^-118: the scale is held at 2^126
+    bias = randn((24,), g, scale=0.1)
+    alphas = [torch.tensor([v], device=DEV) for v in (0.1, 0.2, 0.3)]
+    *_, aux = K_.fused_dynamic_weights_forward(x, phi, bias, *alphas, return_aux=True)
+    raw = to_np(x) @ to_np(phi)
+    got = to_np(aux[:, :24])
+    errs = [rel_err(got[:, j], raw[:, j]) for j in range(24) if j != 2]
+    print(f"{xdtype}: worst column error {max(errs):.2e}", flush=True)
+    assert max(errs) < 1e-5
+    assert np.all(got[:, 2] == 0.0)
+    ss = (to_np(x) ** 2).sum(axis=1)
+    assert rel_err(1.0 / to_np(aux[:, 24]) ** 2, ss / K + 1e-6) < 1e-5
+
+
 def test_dynamic_weights_default_init_sgn_zero():
     """phi = 0 with the module's default bias: scaled_res has 12 exact zeros,
     whose gradient follows torch (sgn(0) = 0)."""
