@@ -34,6 +34,7 @@ from __future__ import annotations
 import argparse
 import json
 import os
+import statistics
 import sys
 import time
 
@@ -213,7 +214,6 @@ def _dynw_ceiling(R: int = 16384, K: int = 16384, reps: int = 10, warm: int = 2,
     probes and the launchers alternate in rounds and each figure is the median over rounds; a
     rocprofv3 kernel trace of this run splits the launchers' time into their kernels."""
     import ctypes
-    import statistics
 
     import torch
 
@@ -321,9 +321,11 @@ def _calibrate_copy() -> int:
 
 def _ops_leg(n: int = 20, warm: int = 3) -> dict:
     """Each low-level op alone, timed with HIP events on torch's current stream
-    (the stream the kernels run on): mean time per call and the fraction of
-    8 TB/s its algorithmic bytes reach.  Inputs are resident before timing;
-    gradient calls use torch.autograd.grad, so nothing accumulates between calls."""
+    (the stream the kernels run on): time per call (the median of three blocks of
+    ``n`` calls, each block's mean, so that a stretch of lowered clocks on the box
+    moves one block, not the figure) and the fraction of 8 TB/s its algorithmic
+    bytes reach.  Inputs are resident before timing; gradient calls use
+    torch.autograd.grad, so nothing accumulates between calls."""
     import torch
 
     import mhc
@@ -334,21 +336,24 @@ def _ops_leg(n: int = 20, warm: int = 3) -> dict:
     g = torch.Generator(device=dev)
     g.manual_seed(0)
 
-    def timed(fn, calls=n):
+    def timed(fn, calls=n, blocks=3):
         for _ in range(warm):
             fn()
         torch.cuda.synchronize()
-        a = torch.cuda.Event(enable_timing=True)
-        b = torch.cuda.Event(enable_timing=True)
-        # a bounded spin kernel ahead of the first event keeps the GPU busy while the host
-        # queues the first calls, so the host's start-up latency stays out of the interval
-        torch.cuda._sleep(1 << 20)
-        a.record()
-        for _ in range(calls):
-            fn()
-        b.record()
-        torch.cuda.synchronize()
-        return a.elapsed_time(b) / calls * 1e3  # us
+        per_block = []
+        for _ in range(blocks):
+            a = torch.cuda.Event(enable_timing=True)
+            b = torch.cuda.Event(enable_timing=True)
+            # a bounded spin kernel ahead of the first event keeps the GPU busy while the host
+            # queues the first calls, so the host's start-up latency stays out of the interval
+            torch.cuda._sleep(1 << 20)
+            a.record()
+            for _ in range(calls):
+                fn()
+            b.record()
+            torch.cuda.synchronize()
+            per_block.append(a.elapsed_time(b) / calls * 1e3)  # us
+        return statistics.median(per_block)
 
     out = {}
 
@@ -401,7 +406,8 @@ def _ops_leg(n: int = 20, warm: int = 3) -> dict:
     # x read by the forward, x read and grad_x written by the backward
     rec("dynamic_weights_fwd+bwd R=16384 K=16384 bf16", timed(fwd_bwd), 3 * T * 4 * D * e)
     del xt, xl
-    # the same op on fp16 and fp32 rows (the MFMA kernels split x into bf16 parts in registers)
+    # the same op on fp16 and fp32 rows (MFMA kernels: fp16 forward on the f16 MFMA, the rest
+    # with x split into bf16 parts in registers)
     for dt, tag in ((torch.float16, "f16"), (torch.float32, "f32")):
         xd = torch.randn((T, 4 * D), generator=g, device=dev).to(dt)
         nb = T * 4 * D * xd.element_size()
@@ -667,8 +673,6 @@ def _cpu_leg(cfg, reps: int = 3, seq: int | None = None):
     fp32-upcast (the reference's own torch path raises on bf16 H with fp32 weights,
     _torch_baseline.py:136,141).  One warm-up run, then the median of `reps` runs, as the
     reference's benchmark times its large cases.  `seq` shortens the sequence (tests only)."""
-    import statistics
-
     import torch
 
     from oracle import torch_path
