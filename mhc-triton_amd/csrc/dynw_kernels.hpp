@@ -109,6 +109,20 @@ __global__ __launch_bounds__(kThreads) void dynw_partial_kernel(const TX* __rest
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 
+// a and b rounded to bf16 in one v_cvt_pk_bf16_f32 (a in the low half), and
+// what that leaves of each, exactly: a = bf16(a) + ra.  Taking the rounded
+// values back out of the packed word (a shift, a mask) keeps the compiler from
+// converting each value again on its own to subtract it.
+__device__ __forceinline__ uint32_t bf16_pair(float a, float b) {
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2{a, b}, bf16x2));
+}
+__device__ __forceinline__ uint32_t bf16_pair(float a, float b, float& ra, float& rb) {
+  const uint32_t p = bf16_pair(a, b);
+  ra = a - __uint_as_float(p << 16);
+  rb = b - __uint_as_float(p & 0xffff0000u);
+  return p;
+}
+
 // Forward projection on MFMA, K-slice form.  A workgroup of NW waves owns a
 // K chunk of NW * S steps and a range of rows; wave w owns the chunk's steps
 // w S .. w S + S - 1 (S * 32 bytes of each row) and keeps that slice's phi
@@ -230,19 +244,21 @@ __global__ __launch_bounds__(64 * NW, 2) void dynw_mfma_kernel(const TX* __restr
           // x phi (x_mid * phi_lo, x_lo * phi_mid, x_lo * phi_lo: 2^-27 and less,
           // the size of phi's own split residual) are dropped.
           const u32x4 d1 = tile[fr * L + ((CPF * (2 * i + half) + 1) ^ (fr & (L - 1)))];
-          bf16x8 xh, xm, xl;
+          u32x4 ph, pm, pl;
 #pragma unroll
-          for (int j = 0; j < 8; ++j) {
-            const float v = __uint_as_float(j < 4 ? d[j] : d1[j - 4]);
-            const __bf16 h = (__bf16)v;
-            const float r1 = v - (float)h;  // exact
-            const __bf16 m = (__bf16)r1;
-            xh[j] = h;
-            xm[j] = m;
-            xl[j] = (__bf16)(r1 - (float)m);  // exact
-            if (j & 1) ss_hi = fmaf(v, v, ss_hi);
-            else ss = fmaf(v, v, ss);
+          for (int c = 0; c < 4; ++c) {
+            const float a = __uint_as_float(c < 2 ? d[2 * c] : d1[2 * c - 4]);
+            const float b = __uint_as_float(c < 2 ? d[2 * c + 1] : d1[2 * c - 3]);
+            float ra, rb, la, lb;
+            ph[c] = bf16_pair(a, b, ra, rb);    // ra, rb exact
+            pm[c] = bf16_pair(ra, rb, la, lb);  // la, lb exact
+            pl[c] = bf16_pair(la, lb);          // exact: at most 8 significant bits left
+            ss = fmaf(a, a, ss);
+            ss_hi = fmaf(b, b, ss_hi);
           }
+          const bf16x8 xh = __builtin_bit_cast(bf16x8, ph);
+          const bf16x8 xm = __builtin_bit_cast(bf16x8, pm);
+          const bf16x8 xl = __builtin_bit_cast(bf16x8, pl);
           st = __builtin_amdgcn_mfma_f32_32x32x16_bf16(xh, p_lo, st, 0, 0, 0);
           st = __builtin_amdgcn_mfma_f32_32x32x16_bf16(xm, p_mid, st, 0, 0, 0);
           st = __builtin_amdgcn_mfma_f32_32x32x16_bf16(xl, p_hi, st, 0, 0, 0);
@@ -982,27 +998,29 @@ __global__ __launch_bounds__(64 * NW, MINW) void dynw_bwd_mfma_kernel(const TX* 
       if constexpr (kXF32) {
         // fp32 x: bf16 hi + mid parts (x_lo * G_hi and x_mid * G_lo, 2^-18 of x G, are dropped
         // as above)
-        bf16x8 xh, xm;
+        u32x4 ph, pm;
 #pragma unroll
-        for (int j = 0; j < 8; ++j) {
-          const float v = pa32[st][j];
-          const __bf16 h = (__bf16)v;
-          xh[j] = h;
-          xm[j] = (__bf16)(v - (float)h);
+        for (int c = 0; c < 4; ++c) {
+          float ra, rb;
+          ph[c] = bf16_pair(pa32[st][2 * c], pa32[st][2 * c + 1], ra, rb);
+          pm[c] = bf16_pair(ra, rb);
         }
+        const bf16x8 xh = __builtin_bit_cast(bf16x8, ph);
+        const bf16x8 xm = __builtin_bit_cast(bf16x8, pm);
         dphi = __builtin_amdgcn_mfma_f32_32x32x16_bf16(xh, pbl[st], dphi, 0, 0, 0);
         dphi = __builtin_amdgcn_mfma_f32_32x32x16_bf16(xm, pbh[st], dphi, 0, 0, 0);
         dphi = __builtin_amdgcn_mfma_f32_32x32x16_bf16(xh, pbh[st], dphi, 0, 0, 0);
       } else if constexpr (kXF16) {
         const f16x8 hv = __builtin_bit_cast(f16x8, pa[st]);
-        bf16x8 xh, xl;
+        u32x4 ph, pl;
 #pragma unroll
-        for (int j = 0; j < 8; ++j) {
-          const float f = (float)hv[j];
-          const __bf16 h = (__bf16)f;
-          xh[j] = h;
-          xl[j] = (__bf16)(f - (float)h);  // exact
+        for (int c = 0; c < 4; ++c) {
+          float ra, rb;
+          ph[c] = bf16_pair((float)hv[2 * c], (float)hv[2 * c + 1], ra, rb);
+          pl[c] = bf16_pair(ra, rb);  // exact
         }
+        const bf16x8 xh = __builtin_bit_cast(bf16x8, ph);
+        const bf16x8 xl = __builtin_bit_cast(bf16x8, pl);
         dphi = __builtin_amdgcn_mfma_f32_32x32x16_bf16(xh, pbl[st], dphi, 0, 0, 0);
         dphi = __builtin_amdgcn_mfma_f32_32x32x16_bf16(xl, pbh[st], dphi, 0, 0, 0);
         dphi = __builtin_amdgcn_mfma_f32_32x32x16_bf16(xh, pbh[st], dphi, 0, 0, 0);
