@@ -923,16 +923,15 @@ __global__ __launch_bounds__(64 * NW, MINW) void dynw_bwd_mfma_kernel(const TX* 
 #pragma unroll
       for (int jj = 0; jj < NG; ++jj) {
         const int gr = grow + GRPP * jj;
-        bf16x4 h4, l4;
+        u32x2 h4, l4;
 #pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          const float v = gcol < kOut ? gv[jj][e] : 0.f;
-          const __bf16 h = (__bf16)v;
-          h4[e] = h;
-          l4[e] = (__bf16)(v - (float)h);
+        for (int c = 0; c < 2; ++c) {
+          float ra, rb;
+          h4[c] = bf16_pair(gcol < kOut ? gv[jj][2 * c] : 0.f, gcol < kOut ? gv[jj][2 * c + 1] : 0.f, ra, rb);
+          l4[c] = bf16_pair(ra, rb);
         }
-        *reinterpret_cast<bf16x4*>(&ghi[gr * kBwdGPitch + gcol]) = h4;
-        *reinterpret_cast<bf16x4*>(&glo[gr * kBwdGPitch + gcol]) = l4;
+        *reinterpret_cast<u32x2*>(&ghi[gr * kBwdGPitch + gcol]) = h4;
+        *reinterpret_cast<u32x2*>(&glo[gr * kBwdGPitch + gcol]) = l4;
         if (gcol == kOut) cf[gr] = gv[jj][0];
       }
     }
