@@ -67,11 +67,11 @@ ALGO_UNITS = {True: (18, 24), False: (14, 19)}
 # rocprofv3 counter passes over this bench (`--pmc FETCH_SIZE`, then
 # `--pmc WRITE_SIZE`), each scaled by what the counter reads for a 512 MiB
 # device copy (`bench.py --calibrate-copy`: FETCH_SIZE x2.0, WRITE_SIZE x1.0 on
-# MI355X).  Measured at commit de1782b on the kernel as built there (unchanged
-# since); algorithmic bytes 9 D e T: config3 1,207,959,552 (+0.018%), config4
+# MI355X).  Measured at commit TRAFFIC_COMMIT on the kernel as built there;
+# algorithmic bytes 9 D e T: config3 1,207,959,552 (+0.018%), config4
 # 1,056,964,608 (+0.018%), config5 1,207,959,552 (+0.012%).
-MEASURED_TRAFFIC = {"config3": 1208171969, "config4": 1057150466, "config5": 1208101031}
-TRAFFIC_COMMIT = "de1782b"
+MEASURED_TRAFFIC = {"config3": 1208180457, "config4": 1057155147, "config5": 1208107132}
+TRAFFIC_COMMIT = "bd0c8b8"
 
 # Best fraction of 8 TB/s that a kernel of the closure forward's launch shape
 # reaches when it only moves the same 5:4 read / write mix (4 H rows + bo read,
