@@ -275,6 +275,10 @@ extern "C" int mhc_dynamic_weights_backward(const void* x, int dtype_x, const fl
 namespace mhc {
 
 constexpr int kPoolUN = 4;  // rows in flight per lane in colsum_kernel
+// Sequences up to this length take colsum_direct_kernel (one launch, the same
+// bits): at such lengths the pass is a few microseconds of latency, and the
+// second launch and the column-partial round trip are most of it.
+constexpr int64_t kPoolDirectRows = 8;
 
 template <typename T, int W, bool PROJ>
 static int launch_meanpool(const T* H, float* x, const float* phi, float* projpart, float* colpart, int64_t B,
@@ -284,6 +288,12 @@ static int launch_meanpool(const T* H, float* x, const float* phi, float* projpa
   const bool phi_vec = phi ? aligned16(phi) : false;
   for (int64_t b0 = 0; b0 < B; b0 += kMaxGridY) {
     const int64_t nb = (B - b0) < kMaxGridY ? (B - b0) : kMaxGridY;
+    if (S <= kPoolDirectRows) {
+      colsum_direct_kernel<T, PROJ><<<dim3((unsigned)p.nrc, (unsigned)nb), kThreads, 0, st>>>(
+          H, x, phi, projpart, S, K, p.SC, inv_S, b0, phi_vec);
+      if (int rc = hip_status(hipGetLastError(), "mean_pool direct launch")) return rc;
+      continue;
+    }
     // The first half of each S chunk with nt loads, the second half plain: in
     // the layer, branch_input reads H next and finds the chunk tails in the
     // memory-side cache (colsum + branch_input: -4 us at config-3 size, -6 us

@@ -1230,6 +1230,49 @@ __global__ __launch_bounds__(kThreads) void colsum_reduce_kernel(const float* __
   }
 }
 
+// Short sequences (the decode regime): the two kernels above in one launch.
+// One thread per column sums H[b, s, c] over the same S chunks of SC rows, in
+// the same order, as colsum_kernel and colsum_reduce_kernel do (each chunk from
+// zero, then the chunk sums in chunk order, then the 1/S scale), so x and the
+// projection partials come out bit for bit as on the two-kernel path; what
+// goes is the column-partial round trip and one dependent launch.
+template <typename T, bool PROJ>
+__global__ __launch_bounds__(kThreads) void colsum_direct_kernel(const T* __restrict__ H, float* __restrict__ x,
+                                                                 const float* __restrict__ phi,
+                                                                 float* __restrict__ projpart, int64_t S, int64_t K,
+                                                                 int64_t SC, float inv_S, int64_t b0, bool phi_vec) {
+  __shared__ float red[(kThreads / 16) * kPart];
+  const int64_t b = b0 + blockIdx.y;
+  const int64_t c = (int64_t)blockIdx.x * kThreads + threadIdx.x;
+  float pv[kPart];
+#pragma unroll
+  for (int j = 0; j < kPart; ++j) pv[j] = 0.f;
+  if (c < K) {
+    const T* p = H + b * S * K + c;
+    float v = 0.f;
+    for (int64_t s0 = 0; s0 < S; s0 += SC) {
+      const int64_t s1 = s0 + SC < S ? s0 + SC : S;
+      float a = 0.f;
+#pragma unroll 4
+      for (int64_t s = s0; s < s1; ++s) a += to_f32(p[s * K]);
+      v += a;
+    }
+    v *= inv_S;
+    x[b * K + c] = v;
+    if constexpr (PROJ) {
+      float ph[kOut];
+      load_phi_row(phi, c, phi_vec, ph);
+#pragma unroll
+      for (int j = 0; j < kOut; ++j) pv[j] = v * ph[j];
+      pv[kOut] = v * v;
+    }
+  }
+  if constexpr (PROJ) {
+    const float tot = block_sum_rows<kPart>(pv, red);
+    if (threadIdx.x < kPart) projpart[(b * gridDim.x + blockIdx.x) * kPart + threadIdx.x] = tot;
+  }
+}
+
 // Launch plan of the two mean-pool kernels; depends only on the shape, so
 // workspace sizes can be queried without a device.
 struct PoolPlan {

@@ -108,6 +108,17 @@ def test_unfused_dynamic_fp32():
     check_layer(hc, H, bo, dHn, dbi, 1e-5, 1e-4, 1e-4)
 
 
+@pytest.mark.parametrize("B,S,D,dtype", [(1, 1, 4096, torch.bfloat16), (3, 2, 100, torch.bfloat16),
+                                         (64, 1, 256, torch.float32), (2, 8, 448, torch.float16),
+                                         (4, 7, 96, torch.float32), (2, 9, 64, torch.bfloat16)])
+def test_short_sequences(B, S, D, dtype):
+    """Decode-like sequence lengths: S up to 8 takes the single-launch mean-pool
+    (colsum_direct_kernel), S = 9 the two-kernel one; dynamic fused weights, phi ~ N(0, 0.02)."""
+    hc, H, bo, dHn, dbi = make_case(B, S, D, dtype, phi_std=0.02)
+    tol = 1e-5 if dtype == torch.float32 else 2e-2
+    check_layer(hc, H, bo, dHn, dbi, tol, 1e-4 if dtype == torch.float32 else 2e-2, 1e-4)
+
+
 def test_ragged_dim_bf16():
     """D not a multiple of the 8-element vector: the scalar-path kernels."""
     hc, H, bo, dHn, dbi = make_case(3, 17, 100, torch.bfloat16, phi_std=0.02)
