@@ -140,6 +140,24 @@ extern "C" int mhc_dynamic_weights_forward(const void* x, int dtype_x, const flo
   return hip_status(hipGetLastError(), "dynamic_weights_forward finalize launch");
 }
 
+namespace mhc {
+
+// The layer path at many batches: x [R, K] fp32 (the pooled rows) projected on the MFMA kernel
+// into the partial records part[R][nK][25], as the op does for rows in bulk.
+bool dynw_project_rows_ok(int64_t R, int64_t K, const float* x) {
+  return mfma_shape_ok(R, K, 4) && aligned16(x);
+}
+
+int dynw_project_rows(const float* x, const float* phi, float* part, int64_t R, int64_t K, int* nK, hipStream_t st) {
+  const MfmaPlan m = mfma_plan(R, K, 4);
+  dynw_mfma_kernel<float><<<dim3((unsigned)m.ngr, (unsigned)m.nK), 64 * kMfmaWaves, 0, st>>>(x, phi, part, R, K,
+                                                                                         m.nK, m.rows_per_wg);
+  *nK = m.nK;
+  return hip_status(hipGetLastError(), "layer projection mfma launch");
+}
+
+}  // namespace mhc
+
 // Row chunks of the backward's wide pass: one chunk for a batch's worth of
 // rows; for many rows about 1024 workgroups, at least 64 rows each.
 struct WidePlan {
@@ -182,13 +200,63 @@ static WidePlan mfma_bwd_plan(int64_t R, int64_t K, const WidePlan& w) {
   }
 }
 
+namespace mhc {
+
+// Workspace of dynw_grad_pass with split rows: the grad_phi chunk partials, and the grad_bias /
+// grad_alpha chunk records (none with one chunk).
+size_t dynw_grad_split_bytes(int64_t R, int64_t K) {
+  const WidePlan w = wide_plan(R, K);
+  if (w.nR <= 1) return 0;
+  return align256((size_t)w.nR * K * kOut * sizeof(float)) + align256((size_t)w.nR * 27 * sizeof(float));
+}
+
+// grad_x, grad_phi, grad_bias and grad_alpha from the per-row records rowbuf [R][kRow] that
+// dynw_bwd_rows_kernel wrote: rows in bulk on the MFMA kernel, else the VALU wide pass, in row
+// chunks whose grad_phi / bias partials dynw_gphi_reduce_kernel then adds in chunk order.
+// split_ws holds dynw_grad_split_bytes(R, K) bytes.
+int dynw_grad_pass(const void* x, int dtype_x, const float* phi, const float* rowbuf, void* grad_x, float* grad_phi,
+                   float* grad_bias, float* grad_alpha, int64_t R, int64_t K, char* split_ws, hipStream_t st) {
+  const bool phi_vec = aligned16(phi);
+  const WidePlan w = wide_plan(R, K);
+  const int esize = dtype_x == MHC_DTYPE_F32 ? 4 : 2;
+  const bool mfma_ok = R >= kMfmaMinRows && K % (16 / esize) == 0 && aligned16(x) && (!grad_x || aligned16(grad_x));
+  // the row chunks of the pass that runs (the MFMA plan has at most w.nR)
+  const WidePlan pl = mfma_ok ? mfma_bwd_plan(R, K, w) : w;
+  float* gphi_part = (pl.nR > 1 && grad_phi) ? (float*)split_ws : nullptr;
+  float* bias_part = nullptr;  // MFMA path, split rows: per-chunk grad_bias / grad_alpha records
+  int rc;
+  // (the kernel's buffer spans reach up to four blocks past a chunk's rows)
+  if (mfma_ok && span_ok((pl.RC + 4 * kBwdRows) * K, esize) && span_ok((pl.RC + 4 * kBwdRows) * kRow, 4)) {
+    // rows in bulk: grad_x and grad_phi on MFMA.
+    if (pl.nR > 1 && (grad_bias || grad_alpha))
+      bias_part = (float*)(split_ws + align256((size_t)w.nR * K * kOut * sizeof(float)));
+    const dim3 grid((unsigned)((K + 32 * kBwdWaves - 1) / (32 * kBwdWaves)), (unsigned)pl.nR);
+    rc = MHC_DISPATCH_DTYPE(dtype_x, [&] {
+      dynw_bwd_mfma_kernel<T><<<grid, 64 * kBwdWaves, 0, st>>>((const T*)x, phi, rowbuf, (T*)grad_x, grad_phi,
+                                                               gphi_part, bias_part, grad_bias, grad_alpha, R, K,
+                                                               pl.RC);
+      return hip_status(hipGetLastError(), "dynamic_weights_backward mfma launch");
+    });
+  } else {
+    rc = MHC_DISPATCH_DTYPE(dtype_x, [&] {
+      return hip_status(launch_dynw_bwd_wide<T, T>((const T*)x, phi, rowbuf, (T*)grad_x, grad_phi, gphi_part,
+                                                   grad_bias, grad_alpha, R, K, pl.RC, (unsigned)pl.nR, phi_vec, st),
+                        "dynamic_weights_backward wide launch");
+    });
+  }
+  if (rc || (!gphi_part && !bias_part)) return rc;
+  const int64_t n = gphi_part ? K * kOut : 0;
+  const int64_t nt = n + (bias_part ? 27 : 0);
+  dynw_gphi_reduce_kernel<><<<dim3((unsigned)((nt + kThreads - 1) / kThreads)), kThreads, 0, st>>>(
+      gphi_part, grad_phi, n, pl.nR, bias_part, grad_bias, grad_alpha);
+  return hip_status(hipGetLastError(), "dynamic_weights_backward grad_phi reduce launch");
+}
+
+}  // namespace mhc
+
 extern "C" size_t mhc_dynamic_weights_backward_workspace_bytes(int64_t R, int64_t K) {
   if (R <= 0) return 0;
-  const WidePlan w = wide_plan(R, K);
-  size_t need = align256((size_t)R * kRow * sizeof(float));
-  // split rows: the grad_phi chunk partials, and the grad_bias / grad_alpha chunk records
-  if (w.nR > 1) need += align256((size_t)w.nR * K * kOut * sizeof(float)) + align256((size_t)w.nR * 27 * sizeof(float));
-  return need;
+  return align256((size_t)R * kRow * sizeof(float)) + dynw_grad_split_bytes(R, K);
 }
 
 extern "C" int mhc_dynamic_weights_backward(const void* x, int dtype_x, const float* phi, const float* bias,
@@ -232,41 +300,8 @@ extern "C" int mhc_dynamic_weights_backward(const void* x, int dtype_x, const fl
       aux, P, InRow{H_pre, 4}, InRow{grad_H_pre, 4}, InRow{grad_H_post, 4}, InRow{grad_H_res, 16}, nullptr, 0,
       rowbuf, R, K, iters, eps);
   if (int rc = hip_status(hipGetLastError(), "dynamic_weights_backward rows launch")) return rc;
-  const bool phi_vec = aligned16(phi);
-  const WidePlan w = wide_plan(R, K);
-  const int esize = dtype_x == MHC_DTYPE_F32 ? 4 : 2;
-  const bool mfma_ok = R >= kMfmaMinRows && K % (16 / esize) == 0 && aligned16(x) && (!grad_x || aligned16(grad_x));
-  // the row chunks of the pass that runs (the MFMA plan has at most w.nR)
-  const WidePlan pl = mfma_ok ? mfma_bwd_plan(R, K, w) : w;
-  char* split_ws = (char*)workspace + align256((size_t)R * kRow * sizeof(float));
-  float* gphi_part = (pl.nR > 1 && grad_phi) ? (float*)split_ws : nullptr;
-  float* bias_part = nullptr;  // MFMA path, split rows: per-chunk grad_bias / grad_alpha records
-  int rc;
-  // (the kernel's buffer spans reach up to four blocks past a chunk's rows)
-  if (mfma_ok && span_ok((pl.RC + 4 * kBwdRows) * K, esize) && span_ok((pl.RC + 4 * kBwdRows) * kRow, 4)) {
-    // rows in bulk: grad_x and grad_phi on MFMA.
-    if (pl.nR > 1 && (grad_bias || grad_alpha))
-      bias_part = (float*)(split_ws + align256((size_t)w.nR * K * kOut * sizeof(float)));
-    const dim3 grid((unsigned)((K + 32 * kBwdWaves - 1) / (32 * kBwdWaves)), (unsigned)pl.nR);
-    rc = MHC_DISPATCH_DTYPE(dtype_x, [&] {
-      dynw_bwd_mfma_kernel<T><<<grid, 64 * kBwdWaves, 0, st>>>((const T*)x, phi, rowbuf, (T*)grad_x, grad_phi,
-                                                               gphi_part, bias_part, grad_bias, grad_alpha, R, K,
-                                                               pl.RC);
-      return hip_status(hipGetLastError(), "dynamic_weights_backward mfma launch");
-    });
-  } else {
-    rc = MHC_DISPATCH_DTYPE(dtype_x, [&] {
-      return hip_status(launch_dynw_bwd_wide<T, T>((const T*)x, phi, rowbuf, (T*)grad_x, grad_phi, gphi_part,
-                                                   grad_bias, grad_alpha, R, K, pl.RC, (unsigned)pl.nR, phi_vec, st),
-                        "dynamic_weights_backward wide launch");
-    });
-  }
-  if (rc || (!gphi_part && !bias_part)) return rc;
-  const int64_t n = gphi_part ? K * kOut : 0;
-  const int64_t nt = n + (bias_part ? 27 : 0);
-  dynw_gphi_reduce_kernel<><<<dim3((unsigned)((nt + kThreads - 1) / kThreads)), kThreads, 0, st>>>(
-      gphi_part, grad_phi, n, pl.nR, bias_part, grad_bias, grad_alpha);
-  return hip_status(hipGetLastError(), "dynamic_weights_backward grad_phi reduce launch");
+  return dynw_grad_pass(x, dtype_x, phi, rowbuf, grad_x, grad_phi, grad_bias, grad_alpha, R, K,
+                        (char*)workspace + align256((size_t)R * kRow * sizeof(float)), st);
 }
 
 // ---------------------------------------------------------------------------
@@ -289,8 +324,12 @@ static int launch_meanpool(const T* H, float* x, const float* phi, float* projpa
   for (int64_t b0 = 0; b0 < B; b0 += kMaxGridY) {
     const int64_t nb = (B - b0) < kMaxGridY ? (B - b0) : kMaxGridY;
     if (S <= kPoolDirectRows) {
-      colsum_direct_kernel<T, PROJ><<<dim3((unsigned)p.nrc, (unsigned)nb), kThreads, 0, st>>>(
-          H, x, phi, projpart, S, K, p.SC, inv_S, b0, phi_vec);
+      if (!PROJ && W > 1 && aligned16(x))
+        colsum_direct_vec_kernel<T, W><<<dim3((unsigned)p.ncc, (unsigned)nb), kThreads, 0, st>>>(
+            H, x, S, K, p.SC, inv_S, b0);
+      else
+        colsum_direct_kernel<T, PROJ><<<dim3((unsigned)p.nrc, (unsigned)nb), kThreads, 0, st>>>(
+            H, x, phi, projpart, S, K, p.SC, inv_S, b0, phi_vec);
       if (int rc = hip_status(hipGetLastError(), "mean_pool direct launch")) return rc;
       continue;
     }

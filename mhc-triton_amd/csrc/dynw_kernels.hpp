@@ -1273,6 +1273,40 @@ __global__ __launch_bounds__(kThreads) void colsum_direct_kernel(const T* __rest
   }
 }
 
+// The same without the projection, W columns per lane through 16-byte loads (a
+// workgroup per 256 W columns of a batch instead of per 256: at B = 4096, S = 1,
+// D = 4096 the one-column form launched 262,144 workgroups); the per-column sums
+// are the same operations, so the bits are too.
+template <typename T, int W>
+__global__ __launch_bounds__(kThreads) void colsum_direct_vec_kernel(const T* __restrict__ H, float* __restrict__ x,
+                                                                     int64_t S, int64_t K, int64_t SC, float inv_S,
+                                                                     int64_t b0) {
+  const int64_t b = b0 + blockIdx.y;
+  const int64_t c = ((int64_t)blockIdx.x * kThreads + threadIdx.x) * W;
+  if (c >= K) return;
+  const T* p = H + b * S * K + c;
+  float v[W];
+#pragma unroll
+  for (int e = 0; e < W; ++e) v[e] = 0.f;
+  for (int64_t s0 = 0; s0 < S; s0 += SC) {
+    const int64_t s1 = s0 + SC < S ? s0 + SC : S;
+    float a[W];
+#pragma unroll
+    for (int e = 0; e < W; ++e) a[e] = 0.f;
+    for (int64_t s = s0; s < s1; ++s) {
+      float f[W];
+      ld<T, W>(p + s * K, f);
+#pragma unroll
+      for (int e = 0; e < W; ++e) a[e] += f[e];
+    }
+#pragma unroll
+    for (int e = 0; e < W; ++e) v[e] += a[e];
+  }
+#pragma unroll
+  for (int e = 0; e < W; ++e) v[e] *= inv_S;
+  st<float, W>(x + b * K + c, v);
+}
+
 // Launch plan of the two mean-pool kernels; depends only on the shape, so
 // workspace sizes can be queried without a device.
 struct PoolPlan {

@@ -25,6 +25,23 @@ int add_residual_backward_any(const void* dhn, int dtype_h, const void* bo, int 
 int mean_pool_any(const void* H, int dtype, float* x, const float* phi, float* projpart, float* colpart,
                   int64_t B, int64_t S, int64_t D, int* nrc, hipStream_t st);
 size_t mean_pool_colpart_bytes(int dtype, int64_t B, int64_t S, int64_t D);
+bool dynw_project_rows_ok(int64_t R, int64_t K, const float* x);
+int dynw_project_rows(const float* x, const float* phi, float* part, int64_t R, int64_t K, int* nK, hipStream_t st);
+size_t dynw_grad_split_bytes(int64_t R, int64_t K);
+int dynw_grad_pass(const void* x, int dtype_x, const float* phi, const float* rowbuf, void* grad_x, float* grad_phi,
+                   float* grad_bias, float* grad_alpha, int64_t R, int64_t K, char* split_ws, hipStream_t st);
+
+// Batches from which the dynamic weights of the layer run as the op runs them for rows in bulk.
+// Below them the batch is a handful of rows: the projection folds into the mean-pool's reduce
+// (which re-reads phi for every batch) and the backward runs one row chunk on the VALU, whose
+// latency is what counts there.  At B = 4096, S = 1, D = 4096 the folded projection took 397 us
+// and the one-chunk backward 1842 us.  Measured crossovers (graph-replayed steps at D = 4096):
+// the backward on the MFMA kernel in row chunks wins from 64 batches on (fwd+bwd 69 -> 59 us at
+// B = 64, 2504 -> 622 us at B = 4096); the projection of the pooled rows on the MFMA kernel, after
+// a mean-pool without it, only from 512 on (forward 72 -> 63 us at B = 512, 457 -> 329 us at
+// B = 4096; 28 against 23 us at B = 64).
+constexpr int64_t kLayerBulkRows = 64;
+constexpr int64_t kLayerBulkProjRows = 512;
 
 constexpr int kLU = 1;   // items per lane per tile, streaming passes
 constexpr int kLRU = 2;  // items per lane per tile, the reduction-only pass B
@@ -40,6 +57,7 @@ struct LayerWs {
   size_t dres;       // [B][16]
   size_t rowbuf;     // [B][52]
   size_t gx;         // [B][4D]
+  size_t grad_split; // B >= kLayerBulkRows: the weights backward's row-chunk partials
   size_t total;
 };
 
@@ -57,6 +75,7 @@ static LayerWs layer_ws(int64_t B, int64_t S, int64_t D, int dtype) {
   w.dres = o;      o += al((size_t)B * 16 * sizeof(float));
   w.rowbuf = o;    o += al((size_t)B * kRow * sizeof(float));
   w.gx = o;        o += al((size_t)B * 4 * D * sizeof(float));
+  w.grad_split = o; o += B >= kLayerBulkRows ? al(dynw_grad_split_bytes(B, 4 * D)) : 0;
   w.total = o;
   return w;
 }
@@ -274,10 +293,22 @@ static int layer_dynamic_forward_run(const void* H, int dtype, const float* phi,
                                      const LayerWs& L, char* wsb, hipStream_t st) {
   float* part = (float*)(wsb + L.pool_part);
   int nK = 0;
-  if (int rc = mean_pool_any(H, dtype, x, phi, part, (float*)(wsb + L.colpart), B, S, D, &nK, st)) return rc;
+  const int64_t K = 4 * D;
   DynParams P{H_pre_base, H_post_base, H_res_base, alpha_pre, alpha_post, alpha_res};
+  if (B >= kLayerBulkProjRows && dynw_project_rows_ok(B, K, x)) {
+    // many batches: the mean-pool alone, then the pooled rows' projection on MFMA (its
+    // records fit the projection-partial region: K / 512 chunks against K / 256)
+    if (int rc = mean_pool_any(H, dtype, x, nullptr, nullptr, (float*)(wsb + L.colpart), B, S, D, nullptr, st))
+      return rc;
+    if (int rc = dynw_project_rows(x, phi, part, B, K, &nK, st)) return rc;
+    dynw_finalize_rows_kernel<><<<dim3((unsigned)((B + kFinRowsWg - 1) / kFinRowsWg)), kThreads, 0, st>>>(
+        part, nK, B, K, P, OutRow{w, kOut}, OutRow{w + 4, kOut}, OutRow{w + 8, kOut}, aux, iters, eps);
+    if (int rc = hip_status(hipGetLastError(), "layer finalize launch")) return rc;
+    return branch_input_any(H, dtype, w, branch_input, B, S, D, st);
+  }
+  if (int rc = mean_pool_any(H, dtype, x, phi, part, (float*)(wsb + L.colpart), B, S, D, &nK, st)) return rc;
   dynw_finalize_kernel<><<<dim3((unsigned)((B + 3) / 4)), kThreads, 0, st>>>(
-      part, nK, B, 4 * D, P, OutRow{w, kOut}, OutRow{w + 4, kOut}, OutRow{w + 8, kOut}, aux, iters, eps);
+      part, nK, B, K, P, OutRow{w, kOut}, OutRow{w + 4, kOut}, OutRow{w + 8, kOut}, aux, iters, eps);
   if (int rc = hip_status(hipGetLastError(), "layer finalize launch")) return rc;
   return branch_input_any(H, dtype, w, branch_input, B, S, D, st);
 }
@@ -469,10 +500,14 @@ extern "C" int mhc_layer_dynamic_backward(const void* H, int dtype, const void* 
       aux, P, InRow{w, kOut}, InRow{nullptr, 0}, InRow{dH_post, 4}, InRow{nullptr, 0}, part, (int)nblk, rowbuf, B,
       K, iters, eps);
   if ((rc = hip_status(hipGetLastError(), "layer weights backward rows launch"))) return rc;
-  if ((rc = hip_status(launch_dynw_bwd_wide<float, float>(x, phi, rowbuf, dH ? gx : nullptr, grad_phi, nullptr,
-                                                          grad_bias, grad_alpha, B, K, B, 1u, aligned16(phi), st),
-                       "layer weights backward wide launch")))
-    return rc;
+  if (B >= kLayerBulkRows)
+    rc = dynw_grad_pass(x, MHC_DTYPE_F32, phi, rowbuf, dH ? gx : nullptr, grad_phi, grad_bias, grad_alpha, B, K,
+                        wsb + L.grad_split, st);
+  else
+    rc = hip_status(launch_dynw_bwd_wide<float, float>(x, phi, rowbuf, dH ? gx : nullptr, grad_phi, nullptr,
+                                                       grad_bias, grad_alpha, B, K, B, 1u, aligned16(phi), st),
+                    "layer weights backward wide launch");
+  if (rc) return rc;
   if (!dH || S * D == 0) return MHC_OK;
   // Pass C: dH.
   return MHC_DISPATCH_DTYPE(dtype, [&] { return dh_dispatch<T>(d_branch_input, dH_new, gx, w, dH, B, S, D, st); });

@@ -117,14 +117,17 @@ def test_stream_ops_past_2p31_elements():
         del win
 
 
+LAYER_WINDOWS = [slice(0, 64), slice(1, 65)]  # 2^31 elements each: indices below 2^31
+
+
 def test_layer_step_past_2p31_elements():
     """A dynamic HyperConnection step (mean-pool projection, weights, mix, closure and every
-    gradient) on 65 batches against windows of 48.  The forward (the mean-pool's S split is the
-    same for 48 and 65 batches at this shape) and d_branch_output match bit for bit.  dH is the
-    exception by design: pass B spreads each batch's dH_pre / dH_res sums over a number of
-    workgroups that depends on the batch count, so the weight gradients, and with them the
-    mean-pool term grad_x / S inside dH, differ in their last fp32 bits; a few dH elements then
-    round to the neighbouring bf16 value."""
+    gradient, the weights backward on the MFMA kernel) on 65 batches against windows of 64.  The
+    forward (the mean-pool's S split is the same for 64 and 65 batches at this shape) and
+    d_branch_output match bit for bit.  dH is the exception by design: pass B
+    spreads each batch's dH_pre / dH_res sums over a number of workgroups that depends on the
+    batch count, so the weight gradients, and with them the mean-pool term grad_x / S inside dH,
+    differ in their last fp32 bits; a few dH elements then round to the neighbouring bf16 value."""
     import mhc
 
     assert B * S * 4 * D > 2 ** 31
@@ -147,7 +150,7 @@ def test_layer_step_past_2p31_elements():
 
     big, big_p = run(slice(None))
     torch.cuda.synchronize()
-    for sl in WINDOWS:
+    for sl in LAYER_WINDOWS:
         win, _ = run(sl)
         for k, v in win.items():
             what = f"{k} batches {sl.start}..{sl.stop - 1}"
@@ -157,18 +160,19 @@ def test_layer_step_past_2p31_elements():
             got = big[k][sl]
             flips = (got != v).float().mean().item()
             # one bf16 step of the larger of the two values (2^(e - 7) for magnitudes in
-            # [2^e, 2^(e+1))), and 1e-6 of the tensor's largest value for values near zero
+            # [2^e, 2^(e+1))), plus 1e-4 of the tensor's largest value (the fp32 gradient
+            # tolerance) for values near zero, whose steps are finer than the fp32 differences
             a, w = got.float(), v.float()
             m = torch.maximum(a.abs(), w.abs())
             step = torch.exp2(torch.floor(torch.log2(m.clamp_min(1e-30))) - 7)
-            over = ((a - w).abs() > step + 1e-6 * w.abs().max()).sum().item()
+            over = ((a - w).abs() > step + 1e-4 * w.abs().max()).sum().item()
             print(f"{what}: {flips:.2e} of the elements differ, {over} by more than one bf16 step",
                   flush=True)
             assert flips < 1e-3 and over == 0, (what, flips, over)
             del a, w, m, step
         del win
     # parameter gradients: the sum over all batches, from two windows that split them
-    _, p0 = run(slice(0, 48))
-    _, p1 = run(slice(48, 65))
+    _, p0 = run(slice(0, 64))
+    _, p1 = run(slice(64, 65))
     for n, v in big_p.items():
         _close(f"grad {n}", v, p0[n] + p1[n], 1e-5)

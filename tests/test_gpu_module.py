@@ -110,10 +110,14 @@ def test_unfused_dynamic_fp32():
 
 @pytest.mark.parametrize("B,S,D,dtype", [(1, 1, 4096, torch.bfloat16), (3, 2, 100, torch.bfloat16),
                                          (64, 1, 256, torch.float32), (2, 8, 448, torch.float16),
-                                         (4, 7, 96, torch.float32), (2, 9, 64, torch.bfloat16)])
+                                         (4, 7, 96, torch.float32), (2, 9, 64, torch.bfloat16),
+                                         (200, 3, 128, torch.bfloat16), (512, 1, 128, torch.float32),
+                                         (600, 2, 64, torch.bfloat16), (515, 12, 32, torch.float16)])
 def test_short_sequences(B, S, D, dtype):
-    """Decode-like sequence lengths: S up to 8 takes the single-launch mean-pool
-    (colsum_direct_kernel), S = 9 the two-kernel one; dynamic fused weights, phi ~ N(0, 0.02)."""
+    """Decode-like sequence lengths and batches of many sequences: S up to 8 takes the
+    single-launch mean-pool (colsum_direct_kernel), S = 9 and 12 the two-kernel one; from 64
+    batches the weights backward runs on the MFMA kernel in row chunks, from 512 the pooled
+    rows' projection too.  Dynamic fused weights, phi ~ N(0, 0.02)."""
     hc, H, bo, dHn, dbi = make_case(B, S, D, dtype, phi_std=0.02)
     tol = 1e-5 if dtype == torch.float32 else 2e-2
     check_layer(hc, H, bo, dHn, dbi, tol, 1e-4 if dtype == torch.float32 else 2e-2, 1e-4)
