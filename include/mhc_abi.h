@@ -192,7 +192,9 @@ int mhc_mean_pool(const void* H, int dtype, float* x, int64_t B, int64_t S, int6
 /* Dynamic layer forward (module.py:119-139 + 177): mean-pool, Eq. 14-19
  * with bias = [H_pre_base, H_post_base, H_res_base], then branch_input.
  * Outputs: branch_input [B,S,D] (dtype), x [B,4D] f32, w [B,24] f32,
- * aux [B,25] f32. */
+ * aux [B,25] f32.  x (the pooled rows, an input of the backward) may be NULL
+ * when no backward follows: the pooled rows are then not kept (and at S = 1
+ * with many batches not formed at all). */
 int mhc_layer_dynamic_forward(const void* H, int dtype, const float* phi,
                               const float* H_pre_base, const float* H_post_base,
                               const float* H_res_base, const float* alpha_pre,
@@ -219,7 +221,10 @@ int mhc_layer_dynamic_forward(const void* H, int dtype, const float* phi,
  * on one GPU (on different streams) race; serialise them.  The array's address
  * is looked up on the first call on each GPU and kept for the process: once
  * this entry point has run on a GPU, do not call it there again after
- * hipDeviceReset (which unloads the code object the address points into). */
+ * hipDeviceReset (which unloads the code object the address points into).
+ * With x NULL at 512 batches or more and S > 1 its weights can differ in their
+ * last bits from the workspace entry's: it has no room to keep the pooled rows
+ * for their projection, and folds the projection into the mean-pool instead. */
 int mhc_layer_dynamic_forward_noalloc(const void* H, int dtype, const float* phi,
                                       const float* H_pre_base, const float* H_post_base,
                                       const float* H_res_base, const float* alpha_pre,

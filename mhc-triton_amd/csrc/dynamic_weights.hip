@@ -142,18 +142,22 @@ extern "C" int mhc_dynamic_weights_forward(const void* x, int dtype_x, const flo
 
 namespace mhc {
 
-// The layer path at many batches: x [R, K] fp32 (the pooled rows) projected on the MFMA kernel
-// into the partial records part[R][nK][25], as the op does for rows in bulk.
-bool dynw_project_rows_ok(int64_t R, int64_t K, const float* x) {
-  return mfma_shape_ok(R, K, 4) && aligned16(x);
+// The layer path at many batches: rows x [R, K] (the pooled rows in fp32, or at S = 1 H's own
+// rows) projected on the MFMA kernel into the partial records part[R][nK][25], as the op does
+// for rows in bulk.
+bool dynw_project_rows_ok(int64_t R, int64_t K, const void* x, int dtype) {
+  return mfma_shape_ok(R, K, dtype == MHC_DTYPE_F32 ? 4 : 2) && aligned16(x);
 }
 
-int dynw_project_rows(const float* x, const float* phi, float* part, int64_t R, int64_t K, int* nK, hipStream_t st) {
-  const MfmaPlan m = mfma_plan(R, K, 4);
-  dynw_mfma_kernel<float><<<dim3((unsigned)m.ngr, (unsigned)m.nK), 64 * kMfmaWaves, 0, st>>>(x, phi, part, R, K,
-                                                                                         m.nK, m.rows_per_wg);
+int dynw_project_rows(const void* x, int dtype, const float* phi, float* part, int64_t R, int64_t K, int* nK,
+                      hipStream_t st) {
+  const MfmaPlan m = mfma_plan(R, K, dtype == MHC_DTYPE_F32 ? 4 : 2);
   *nK = m.nK;
-  return hip_status(hipGetLastError(), "layer projection mfma launch");
+  return MHC_DISPATCH_DTYPE(dtype, [&] {
+    dynw_mfma_kernel<T><<<dim3((unsigned)m.ngr, (unsigned)m.nK), 64 * kMfmaWaves, 0, st>>>(
+        (const T*)x, phi, part, R, K, m.nK, m.rows_per_wg);
+    return hip_status(hipGetLastError(), "layer projection mfma launch");
+  });
 }
 
 }  // namespace mhc

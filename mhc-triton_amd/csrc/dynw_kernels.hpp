@@ -1215,7 +1215,7 @@ __global__ __launch_bounds__(kThreads) void colsum_reduce_kernel(const float* __
 #pragma unroll 8
     for (int k = 0; k < nS; ++k) v += p[(int64_t)k * K];
     v *= inv_S;
-    x[b * K + c] = v;
+    if (x) x[b * K + c] = v;  // with the projection x is optional (nothing reads it after a no-grad forward)
     if constexpr (PROJ) {
       float ph[kOut];
       load_phi_row(phi, c, phi_vec, ph);
@@ -1258,7 +1258,7 @@ __global__ __launch_bounds__(kThreads) void colsum_direct_kernel(const T* __rest
       v += a;
     }
     v *= inv_S;
-    x[b * K + c] = v;
+    if (x) x[b * K + c] = v;  // with the projection x is optional (nothing reads it after a no-grad forward)
     if constexpr (PROJ) {
       float ph[kOut];
       load_phi_row(phi, c, phi_vec, ph);

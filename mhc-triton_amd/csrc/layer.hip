@@ -25,8 +25,9 @@ int add_residual_backward_any(const void* dhn, int dtype_h, const void* bo, int 
 int mean_pool_any(const void* H, int dtype, float* x, const float* phi, float* projpart, float* colpart,
                   int64_t B, int64_t S, int64_t D, int* nrc, hipStream_t st);
 size_t mean_pool_colpart_bytes(int dtype, int64_t B, int64_t S, int64_t D);
-bool dynw_project_rows_ok(int64_t R, int64_t K, const float* x);
-int dynw_project_rows(const float* x, const float* phi, float* part, int64_t R, int64_t K, int* nK, hipStream_t st);
+bool dynw_project_rows_ok(int64_t R, int64_t K, const void* x, int dtype);
+int dynw_project_rows(const void* x, int dtype, const float* phi, float* part, int64_t R, int64_t K, int* nK,
+                      hipStream_t st);
 size_t dynw_grad_split_bytes(int64_t R, int64_t K);
 int dynw_grad_pass(const void* x, int dtype_x, const float* phi, const float* rowbuf, void* grad_x, float* grad_phi,
                    float* grad_bias, float* grad_alpha, int64_t R, int64_t K, char* split_ws, hipStream_t st);
@@ -276,7 +277,7 @@ static int layer_dynamic_forward_args(const char* who, const void* H, const floa
   if (B == 0) return MHC_OK;
   const bool nz = S * D != 0;  // bulk tensors may be empty (null) when S * D == 0
   if ((nz && (!H || !branch_input)) || !phi || !H_pre_base || !H_post_base || !H_res_base || !alpha_pre ||
-      !alpha_post || !alpha_res || !x || !w || !aux) {
+      !alpha_post || !alpha_res || !w || !aux) {
     set_error("%s: null pointer", who);
     return MHC_ERR_ARG;
   }
@@ -290,17 +291,27 @@ static int layer_dynamic_forward_run(const void* H, int dtype, const float* phi,
                                      const float* H_post_base, const float* H_res_base, const float* alpha_pre,
                                      const float* alpha_post, const float* alpha_res, void* branch_input, float* x,
                                      float* w, float* aux, int64_t B, int64_t S, int64_t D, int iters, float eps,
-                                     const LayerWs& L, char* wsb, hipStream_t st) {
+                                     const LayerWs& L, char* wsb, bool full_ws, hipStream_t st) {
   float* part = (float*)(wsb + L.pool_part);
   int nK = 0;
   const int64_t K = 4 * D;
   DynParams P{H_pre_base, H_post_base, H_res_base, alpha_pre, alpha_post, alpha_res};
-  if (B >= kLayerBulkProjRows && dynw_project_rows_ok(B, K, x)) {
-    // many batches: the mean-pool alone, then the pooled rows' projection on MFMA (its
-    // records fit the projection-partial region: K / 512 chunks against K / 256)
-    if (int rc = mean_pool_any(H, dtype, x, nullptr, nullptr, (float*)(wsb + L.colpart), B, S, D, nullptr, st))
+  // Many batches: the mean-pool alone, then the pooled rows' projection on MFMA (its records
+  // fit the projection-partial region: at most K / 512 chunks against K / 256).  At S = 1 the
+  // pooled rows are H's own rows, projected as they are (half the bytes of the f32 rows in
+  // 16-bit H), and the f32 copy is written only for a backward that asks for it.  For S > 1
+  // without x (no backward follows) the pooled rows go to the workspace's grad_x region, so
+  // that the weights come out as with x; only a caller without the full workspace (the
+  // allocation-free entry) then takes the folded projection below.
+  const bool s1 = S == 1 && dynw_project_rows_ok(B, K, H, dtype);
+  float* xp = x ? x : (full_ws ? (float*)(wsb + L.gx) : nullptr);
+  if (B >= kLayerBulkProjRows && (s1 || (xp && dynw_project_rows_ok(B, K, xp, MHC_DTYPE_F32)))) {
+    if (x || !s1)
+      if (int rc = mean_pool_any(H, dtype, xp, nullptr, nullptr, (float*)(wsb + L.colpart), B, S, D, nullptr, st))
+        return rc;
+    if (int rc = s1 ? dynw_project_rows(H, dtype, phi, part, B, K, &nK, st)
+                    : dynw_project_rows(xp, MHC_DTYPE_F32, phi, part, B, K, &nK, st))
       return rc;
-    if (int rc = dynw_project_rows(x, phi, part, B, K, &nK, st)) return rc;
     dynw_finalize_rows_kernel<><<<dim3((unsigned)((B + kFinRowsWg - 1) / kFinRowsWg)), kThreads, 0, st>>>(
         part, nK, B, K, P, OutRow{w, kOut}, OutRow{w + 4, kOut}, OutRow{w + 8, kOut}, aux, iters, eps);
     if (int rc = hip_status(hipGetLastError(), "layer finalize launch")) return rc;
@@ -326,7 +337,7 @@ extern "C" int mhc_layer_dynamic_forward(const void* H, int dtype, const float* 
   if (B == 0) return MHC_OK;
   LAYER_WS_CHECK("layer_dynamic_forward");
   return layer_dynamic_forward_run(H, dtype, phi, H_pre_base, H_post_base, H_res_base, alpha_pre, alpha_post,
-                                   alpha_res, branch_input, x, w, aux, B, S, D, iters, eps, L, wsb,
+                                   alpha_res, branch_input, x, w, aux, B, S, D, iters, eps, L, wsb, true,
                                    (hipStream_t)stream);
 }
 
@@ -394,7 +405,7 @@ extern "C" int mhc_layer_dynamic_forward_noalloc(const void* H, int dtype, const
   char* wsb = nullptr;
   if (int rc = scratch_on_current_device(&wsb)) return rc;
   return layer_dynamic_forward_run(H, dtype, phi, H_pre_base, H_post_base, H_res_base, alpha_pre, alpha_post,
-                                   alpha_res, branch_input, x, w, aux, B, S, D, iters, eps, L, wsb,
+                                   alpha_res, branch_input, x, w, aux, B, S, D, iters, eps, L, wsb, false,
                                    (hipStream_t)stream);
 }
 

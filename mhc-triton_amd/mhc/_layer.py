@@ -60,15 +60,16 @@ def _in_h_dtype(t: Optional[torch.Tensor], H: torch.Tensor) -> Optional[torch.Te
 # ---------------------------------------------------------------------------
 
 def dynamic_forward(H, phi, H_pre_base, H_post_base, H_res_base, alpha_pre, alpha_post, alpha_res,
-                    iters: int, eps: float):
-    """mhc_layer_dynamic_forward: H -> (branch_input, x [B,4D] f32, w [B,24] f32, aux [B,25] f32)."""
+                    iters: int, eps: float, keep_x: bool = True):
+    """mhc_layer_dynamic_forward: H -> (branch_input, x [B,4D] f32, w [B,24] f32, aux [B,25] f32).
+    Without keep_x (no backward follows) x is None and the pooled rows are not kept."""
     B, S, _, D = H.shape
     dev = _lib.require_gpu(H, phi)
     H = H.contiguous()
     params = [_f32(t) for t in (phi, H_pre_base, H_post_base, H_res_base,
                                 alpha_pre.reshape(1), alpha_post.reshape(1), alpha_res.reshape(1))]
     bi = torch.empty(B, S, D, device=dev, dtype=H.dtype)
-    x = torch.empty(B, 4 * D, device=dev, dtype=torch.float32)
+    x = torch.empty(B, 4 * D, device=dev, dtype=torch.float32) if keep_x else None
     w = torch.empty(B, 24, device=dev, dtype=torch.float32)
     aux = torch.empty(B, 25, device=dev, dtype=torch.float32)
     lib = _lib.load()
@@ -76,7 +77,7 @@ def dynamic_forward(H, phi, H_pre_base, H_post_base, H_res_base, alpha_pre, alph
     ws = _ws(lib, B, S, D, code, dev)
     with _lib.on_device(dev):
         _lib.check(lib.mhc_layer_dynamic_forward(
-            H.data_ptr(), code, *[p.data_ptr() for p in params], bi.data_ptr(), x.data_ptr(), w.data_ptr(),
+            H.data_ptr(), code, *[p.data_ptr() for p in params], bi.data_ptr(), _lib.ptr(x), w.data_ptr(),
             aux.data_ptr(), B, S, D, int(iters), float(eps), *_wsargs(ws), _lib.stream(dev)),
             "layer_dynamic_forward")
     return bi, x, w, aux
@@ -252,9 +253,11 @@ class _DynamicLayer(torch.autograd.Function):
 
     @staticmethod
     def forward(ctx, H, phi, H_pre_base, H_post_base, H_res_base, alpha_pre, alpha_post, alpha_res,
-                iters: int, eps: float):
+                iters: int, eps: float, keep_x: bool):
         params = (phi, H_pre_base, H_post_base, H_res_base, alpha_pre, alpha_post, alpha_res)
-        bi, x, w, aux = dynamic_forward(H, *params, iters, eps)
+        # the pooled rows x serve only the backward: the caller drops them when no gradient can
+        # reach this node (ctx.needs_input_grad reflects requires_grad even under torch.no_grad)
+        bi, x, w, aux = dynamic_forward(H, *params, iters, eps, keep_x=keep_x)
         ctx.save_for_backward(H, x, w, aux, *params)
         ctx.iters = iters
         ctx.eps = eps
@@ -264,9 +267,12 @@ class _DynamicLayer(torch.autograd.Function):
     @staticmethod
     def backward(ctx, d_bi, d_w, d_link, d_post):
         H, x, w, aux, *params = ctx.saved_tensors
+        if x is None:
+            raise RuntimeError("mhc: backward through a dynamic layer forward that kept no pooled rows "
+                               "(it ran where no gradient could reach it)")
         dH, gphi, gbias, galpha = dynamic_backward(H, d_bi, d_link, d_post, *params, x, w, aux,
                                                    ctx.iters, ctx.eps, need_dH=ctx.needs_input_grad[0])
-        return (dH, *_dynamic_param_grads(params, gphi, gbias, galpha), None, None)
+        return (dH, *_dynamic_param_grads(params, gphi, gbias, galpha), None, None, None)
 
 
 def _dynamic_param_grads(params, gphi, gbias, galpha):

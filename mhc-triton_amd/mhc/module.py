@@ -181,9 +181,14 @@ class HyperConnection(nn.Module):
             bi, w, link, post_link = _layer._StaticLayer.apply(H, self.H_pre_base, self.H_post_base,
                                                                self.H_res_base, self.sinkhorn_iters)
         elif self.use_fused_weights:
+            # a forward no gradient can reach (inference, or nothing requiring grad) keeps no pooled rows
+            keep_x = torch.is_grad_enabled() and (H.requires_grad or any(p.requires_grad for p in (
+                self.phi, self.H_pre_base, self.H_post_base, self.H_res_base, self.alpha_pre, self.alpha_post,
+                self.alpha_res)))
             bi, w, link, post_link = _layer._DynamicLayer.apply(H, self.phi, self.H_pre_base, self.H_post_base,
                                                                 self.H_res_base, self.alpha_pre, self.alpha_post,
-                                                                self.alpha_res, self.sinkhorn_iters, self.eps)
+                                                                self.alpha_res, self.sinkhorn_iters, self.eps,
+                                                                keep_x)
         else:
             x, h_link, bi_link, w_link = _layer._PoolNode.apply(H)
             bi, w, link, post_link = _layer._GenericLayer.apply(h_link, self._unfused_weights_from(x), bi_link,

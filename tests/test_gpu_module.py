@@ -123,6 +123,26 @@ def test_short_sequences(B, S, D, dtype):
     check_layer(hc, H, bo, dHn, dbi, tol, 1e-4 if dtype == torch.float32 else 2e-2, 1e-4)
 
 
+@pytest.mark.parametrize("B,S,D,dtype", [(600, 1, 128, torch.bfloat16), (520, 3, 64, torch.bfloat16),
+                                         (8, 4, 256, torch.float32), (3, 20, 96, torch.bfloat16),
+                                         (512, 1, 64, torch.float16)])
+def test_no_grad_forward_matches_grad_forward(B, S, D, dtype):
+    """A forward no gradient reaches keeps no pooled rows x (at S = 1 with many batches it never
+    forms them: the projection reads H's rows); branch_input and the closure's H_new come out
+    bit for bit as in a forward that keeps x for a backward."""
+    hc, H, bo, _, _ = make_case(B, S, D, dtype, phi_std=0.02)
+    bi, add = hc(H.clone().requires_grad_(True))
+    Hn = add(bo)
+    with torch.no_grad():
+        bi0, add0 = hc(H)
+        Hn0 = add0(bo)
+    assert torch.equal(bi0, bi.detach()) and torch.equal(Hn0, Hn.detach())
+    # and the no-grad forward against the oracle
+    obi, oHn, _ = O.layer_forward(params_np(hc), to_np(H), to_np(bo), True, True, hc.sinkhorn_iters, hc.eps)
+    tol = 1e-5 if dtype == torch.float32 else 2e-2
+    assert rel_err(to_np(bi0), obi) < tol and rel_err(to_np(Hn0), oHn) < tol
+
+
 def test_ragged_dim_bf16():
     """D not a multiple of the 8-element vector: the scalar-path kernels."""
     hc, H, bo, dHn, dbi = make_case(3, 17, 100, torch.bfloat16, phi_std=0.02)
