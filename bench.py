@@ -5,6 +5,7 @@
     python bench.py --ops        # the low-level ops one by one (one JSON line)
     python bench.py --readme     # the reference's own benchmark table, same workloads
     python bench.py --dynw-ceiling   # access-pattern ceilings of the MFMA dynamic-weights kernels
+    python bench.py --decode     # short sequences, from 1 to 4096 of them: HIP-graph step latency
 
 One "step" is the HyperConnection layer's forward and backward over one
 synthetic batch, exactly as a transformer block uses it:
@@ -108,6 +109,10 @@ def _parse():
                     help="time probe kernels with the access patterns of the MFMA dynamic-weights kernels "
                          "(forward and backward, R = K = 16384 bf16), adding the kernels' costs one at a time, "
                          "and the op itself in the same run")
+    ap.add_argument("--decode", action="store_true",
+                    help="time the dynamic layer at short sequences (S = 1 and 8, B from 1 to 4096, dim 4096 "
+                         "bf16) as replayed HIP graphs: the no-grad forward with the closure, and forward + "
+                         "backward, and exit")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="only run 3 plain device copies of 512 MiB (the known-size kernel that scales "
                          "rocprofv3 FETCH_SIZE / WRITE_SIZE readings into bytes) and exit")
@@ -317,6 +322,72 @@ def _calibrate_copy() -> int:
     print(json.dumps({"calibration": "device copy", "bytes_read": COPY_BYTES, "bytes_written": COPY_BYTES,
                       "launches": 3}), flush=True)
     return 0
+
+
+def _decode_leg(D: int = 4096, reps: int = 5, calls: int = 30) -> dict:
+    """The dynamic HyperConnection layer at short sequences (decode, batched decode, short-sequence
+    training), each step captured in a HIP graph and replayed `calls` times, `reps` times over:
+    the median per-replay wall time of the no-grad forward with its closure (what a serving loop
+    runs) and of the forward + backward.  Replays are launch-bound at the small shapes, so the
+    figure is latency, not bandwidth; `frac` is the algorithmic bytes (18 D e per token forward,
+    42 with the backward) over the time, against 8 TB/s."""
+    import torch
+
+    import mhc
+
+    out = {}
+    for B, S in ((1, 1), (8, 1), (64, 1), (512, 1), (4096, 1), (64, 8), (512, 8)):
+        torch.manual_seed(0)
+        hc = mhc.HyperConnection(D).to("cuda")
+        with torch.no_grad():
+            hc.phi.normal_(0.0, 0.02)
+        params = list(hc.parameters())
+        H = torch.randn(B, S, 4, D, device="cuda").bfloat16().requires_grad_(True)
+        bo = torch.randn(B, S, D, device="cuda").bfloat16().requires_grad_(True)
+        dHn = torch.randn(B, S, 4, D, device="cuda").bfloat16()
+        dbi = torch.randn(B, S, D, device="cuda").bfloat16()
+
+        def fwd():
+            with torch.no_grad():
+                bi, add = hc(H)
+                return add(bo)
+
+        def step():
+            H.grad = None
+            bo.grad = None
+            for p in params:
+                p.grad = None
+            bi, add = hc(H)
+            torch.autograd.backward([add(bo), bi], [dHn, dbi])
+
+        rec = {}
+        for name, fn, units in (("fwd_nograd", fwd, 18), ("fwd_bwd", step, 42)):
+            side = torch.cuda.Stream()
+            side.wait_stream(torch.cuda.current_stream())
+            with torch.cuda.stream(side):
+                for _ in range(3):
+                    fn()
+            torch.cuda.current_stream().wait_stream(side)
+            torch.cuda.synchronize()
+            g = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(g):
+                fn()
+            for _ in range(5):
+                g.replay()
+            torch.cuda.synchronize()
+            ts = []
+            for _ in range(reps):
+                t0 = time.perf_counter()
+                for _ in range(calls):
+                    g.replay()
+                torch.cuda.synchronize()
+                ts.append((time.perf_counter() - t0) / calls * 1e6)
+            us = statistics.median(ts)
+            nbytes = units * D * 2 * B * S
+            rec[name] = {"us": round(us, 1), "hbm_frac": round(nbytes / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4)}
+            del g
+        out[f"B={B} S={S}"] = rec
+    return out
 
 
 def _ops_leg(n: int = 20, warm: int = 3) -> dict:
@@ -785,6 +856,11 @@ def main() -> int:
     _lib.load()  # fails loudly when the HIP library is not built
     if args.ops:
         print(json.dumps({"ops": _ops_leg(), "unit": "us per call", "peak_GBps": HBM_PEAK_GBS,
+                          "device": torch.cuda.get_device_name(0)}), flush=True)
+        return 0
+    if args.decode:
+        print(json.dumps({"decode": _decode_leg(), "unit": "us per replayed step", "dim": 4096, "dtype": "bf16",
+                          "layer": "HyperConnection(dynamic=True), phi ~ N(0, 0.02)",
                           "device": torch.cuda.get_device_name(0)}), flush=True)
         return 0
     if args.readme:
