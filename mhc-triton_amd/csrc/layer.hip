@@ -57,7 +57,8 @@ struct LayerWs {
   size_t dpre;       // [B][4]
   size_t dres;       // [B][16]
   size_t rowbuf;     // [B][52]
-  size_t gx;         // [B][4D]
+  size_t gx;         // [B][4D] grad of the pooled rows (backward); a forward without x at many
+                     // batches and S > 1 keeps its pooled rows here
   size_t grad_split; // B >= kLayerBulkRows: the weights backward's row-chunk partials
   size_t total;
 };
