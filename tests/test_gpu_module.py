@@ -112,12 +112,15 @@ def test_unfused_dynamic_fp32():
                                          (64, 1, 256, torch.float32), (2, 8, 448, torch.float16),
                                          (4, 7, 96, torch.float32), (2, 9, 64, torch.bfloat16),
                                          (200, 3, 128, torch.bfloat16), (512, 1, 128, torch.float32),
-                                         (600, 2, 64, torch.bfloat16), (515, 12, 32, torch.float16)])
+                                         (600, 2, 64, torch.bfloat16), (515, 12, 32, torch.float16),
+                                         (520, 1, 99, torch.bfloat16), (70, 2, 99, torch.float32)])
 def test_short_sequences(B, S, D, dtype):
     """Decode-like sequence lengths and batches of many sequences: S up to 8 takes the
     single-launch mean-pool (colsum_direct_kernel), S = 9 and 12 the two-kernel one; from 64
     batches the weights backward runs on the MFMA kernel in row chunks, from 512 the pooled
-    rows' projection too.  Dynamic fused weights, phi ~ N(0, 0.02)."""
+    rows' projection too; D = 99 (4D % 16 = 12) keeps the folded projection and the scalar
+    mean-pool, with the backward's MFMA pass on ragged column blocks.  Dynamic fused weights,
+    phi ~ N(0, 0.02)."""
     hc, H, bo, dHn, dbi = make_case(B, S, D, dtype, phi_std=0.02)
     tol = 1e-5 if dtype == torch.float32 else 2e-2
     check_layer(hc, H, bo, dHn, dbi, tol, 1e-4 if dtype == torch.float32 else 2e-2, 1e-4)
@@ -125,7 +128,7 @@ def test_short_sequences(B, S, D, dtype):
 
 @pytest.mark.parametrize("B,S,D,dtype", [(600, 1, 128, torch.bfloat16), (520, 3, 64, torch.bfloat16),
                                          (8, 4, 256, torch.float32), (3, 20, 96, torch.bfloat16),
-                                         (512, 1, 64, torch.float16)])
+                                         (512, 1, 64, torch.float16), (530, 1, 99, torch.bfloat16)])
 def test_no_grad_forward_matches_grad_forward(B, S, D, dtype):
     """A forward no gradient reaches keeps no pooled rows x (at S = 1 with many batches it never
     forms them: the projection reads H's rows); branch_input and the closure's H_new come out
