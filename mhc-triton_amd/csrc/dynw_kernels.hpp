@@ -352,6 +352,7 @@ __global__ __launch_bounds__(64 * NW, 2) void dynw_mfma_kernel(const TX* __restr
 #pragma unroll
       for (int j = 0; j < 8; ++j) mx = fmaxf(mx, fabsf(__uint_as_float(pv[i][j])));
     mx = fmaxf(mx, __shfl_xor(mx, 32, 64));  // lanes l and l + 32 hold one column
+    mx = fminf(mx, 0x1.fffffep127f);          // an infinite phi gets a finite exponent (and NaN products)
     int ex = 0;
     if (mx > 0.f) frexpf(mx, &ex);  // mx in [2^(ex-1), 2^ex)
     // s = 2^(15 - ex), held to 2^126 so that s and 1 / s stay finite and normal
