@@ -1294,6 +1294,7 @@ __global__ __launch_bounds__(kThreads) void colsum_direct_vec_kernel(const T* __
     float a[W];
 #pragma unroll
     for (int e = 0; e < W; ++e) a[e] = 0.f;
+#pragma unroll 4
     for (int64_t s = s0; s < s1; ++s) {
       float f[W];
       ld<T, W>(p + s * K, f);
