@@ -327,8 +327,14 @@ static int launch_meanpool(const T* H, float* x, const float* phi, float* projpa
   const bool phi_vec = phi ? aligned16(phi) : false;
   for (int64_t b0 = 0; b0 < B; b0 += kMaxGridY) {
     const int64_t nb = (B - b0) < kMaxGridY ? (B - b0) : kMaxGridY;
-    if (S <= kPoolDirectRows) {
-      if (!PROJ && W > 1 && aligned16(x))
+    // Without the projection, the single launch also serves lengths up to 64 that the plan does
+    // not split (one S chunk: enough batches fill the GPU), where the column partials would be x
+    // itself (B = 4096, S = 16: 563 -> 419 us; B = 512, S = 64: 242 -> 232).  Longer ones keep
+    // colsum_kernel, whose streaming loads read them faster (B = 48, S = 256: 69 against 71 us).
+    const bool direct_vec =
+        !PROJ && W > 1 && aligned16(x) && (S <= kPoolDirectRows || (p.nS == 1 && S <= 64));
+    if (direct_vec || S <= kPoolDirectRows) {
+      if (direct_vec)
         colsum_direct_vec_kernel<T, W><<<dim3((unsigned)p.ncc, (unsigned)nb), kThreads, 0, st>>>(
             H, x, S, K, p.SC, inv_S, b0);
       else

@@ -342,10 +342,12 @@ def test_mean_pool_matches_oracle():
     from mhc._kernels import mean_pool
 
     g = gen(7)
-    # S <= 8: the single-launch form (colsum_direct_kernel); longer: column sums + reduce
+    # S <= 8, or up to 64 in one S chunk: the single-launch form (colsum_direct_vec_kernel, or
+    # colsum_direct_kernel for unaligned rows); longer or split: column sums + reduce
     for dtype, shape in [(torch.float32, (2, 128, 4, 512)), (torch.bfloat16, (3, 77, 4, 100)),
                          (torch.float16, (1, 300, 4, 64)), (torch.bfloat16, (5, 1, 4, 1024)),
-                         (torch.float32, (2, 8, 4, 96)), (torch.float16, (3, 3, 4, 50))]:
+                         (torch.float32, (2, 8, 4, 96)), (torch.float16, (3, 3, 4, 50)),
+                         (torch.bfloat16, (200, 20, 4, 1024)), (torch.float32, (400, 64, 4, 128))]:
         H = randn(shape, g, dtype)
         x = mean_pool(H)
         assert x.dtype == torch.float32
