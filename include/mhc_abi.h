@@ -193,8 +193,9 @@ int mhc_mean_pool(const void* H, int dtype, float* x, int64_t B, int64_t S, int6
  * with bias = [H_pre_base, H_post_base, H_res_base], then branch_input.
  * Outputs: branch_input [B,S,D] (dtype), x [B,4D] f32, w [B,24] f32,
  * aux [B,25] f32.  x (the pooled rows, an input of the backward) may be NULL
- * when no backward follows: the pooled rows are then not kept (and at S = 1
- * with many batches not formed at all). */
+ * when no backward follows, and at S = 1 whatever follows (the backward then
+ * reads H's rows): the pooled rows are then not kept (and at S = 1 with many
+ * batches not formed at all). */
 int mhc_layer_dynamic_forward(const void* H, int dtype, const float* phi,
                               const float* H_pre_base, const float* H_post_base,
                               const float* H_res_base, const float* alpha_pre,
@@ -284,7 +285,9 @@ int mhc_layer_add_backward(const void* dH_new, int dtype_h, const void* branch_o
 /* Dynamic layer backward: given d_bi [B,S,D], dH_new [B,S,4,D] (NULL when
  * H_new received no gradient) and dH_post [B,4] f32 from the closure backward,
  * writes dH [B,S,4,D] (NULL to skip) and the f32 parameter gradients
- * grad_phi [4D,24], grad_bias [24] (pre, post, res), grad_alpha [3]. */
+ * grad_phi [4D,24], grad_bias [24] (pre, post, res), grad_alpha [3].  x is the
+ * forward's pooled rows; at S = 1 it may be NULL (the forward then need not
+ * write it): the pooled rows are H's own rows, read from H. */
 int mhc_layer_dynamic_backward(const void* H, int dtype, const void* d_branch_input,
                                const void* dH_new, const float* dH_post,
                                const float* phi, const float* H_pre_base,

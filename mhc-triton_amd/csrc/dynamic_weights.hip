@@ -189,8 +189,9 @@ static WidePlan wide_plan(int64_t R, int64_t K) {
 // partials.  At R = K = 16384, 4 chunks of 4096 rows (256 workgroups) took
 // 179-181 us against 199-203 us for 16 (1024 workgroups) and 223-224 us for 32.
 // Never more chunks than the wide plan w (whose workspace holds the partials);
-// chunks are split further while a chunk's buffer spans would pass 2^31 bytes.
-static WidePlan mfma_bwd_plan(int64_t R, int64_t K, const WidePlan& w) {
+// chunks are split further while a chunk's buffer spans (esize-byte x or grad_x
+// elements) would pass 2^31 bytes.
+static WidePlan mfma_bwd_plan(int64_t R, int64_t K, const WidePlan& w, int esize) {
   const int64_t ncb = (K + 32 * kBwdWaves - 1) / (32 * kBwdWaves);
   int64_t nr = (kMfmaTargetWg + ncb - 1) / ncb;
   if (nr > w.nR) nr = w.nR;
@@ -199,7 +200,7 @@ static WidePlan mfma_bwd_plan(int64_t R, int64_t K, const WidePlan& w) {
     p.RC = (R + nr - 1) / nr;
     p.nR = (int)((R + p.RC - 1) / p.RC);
     const int64_t span_rows = p.RC + 4 * kBwdRows;
-    if (nr >= w.nR || (span_ok(span_rows * K, 2) && span_ok(span_rows * kRow, 4))) return nr >= w.nR ? w : p;
+    if (nr >= w.nR || (span_ok(span_rows * K, esize) && span_ok(span_rows * kRow, 4))) return nr >= w.nR ? w : p;
     nr = 2 * nr < w.nR ? 2 * nr : w.nR;
   }
 }
@@ -217,35 +218,53 @@ size_t dynw_grad_split_bytes(int64_t R, int64_t K) {
 // grad_x, grad_phi, grad_bias and grad_alpha from the per-row records rowbuf [R][kRow] that
 // dynw_bwd_rows_kernel wrote: rows in bulk on the MFMA kernel, else the VALU wide pass, in row
 // chunks whose grad_phi / bias partials dynw_gphi_reduce_kernel then adds in chunk order.
+// grad_x is in x's dtype, or f32 with gx_f32 (the layer at S = 1 passes H's rows as x).
 // split_ws holds dynw_grad_split_bytes(R, K) bytes.
-int dynw_grad_pass(const void* x, int dtype_x, const float* phi, const float* rowbuf, void* grad_x, float* grad_phi,
-                   float* grad_bias, float* grad_alpha, int64_t R, int64_t K, char* split_ws, hipStream_t st) {
+int dynw_grad_pass(const void* x, int dtype_x, const float* phi, const float* rowbuf, void* grad_x, bool gx_f32,
+                   float* grad_phi, float* grad_bias, float* grad_alpha, int64_t R, int64_t K, char* split_ws,
+                   hipStream_t st) {
   const bool phi_vec = aligned16(phi);
   const WidePlan w = wide_plan(R, K);
   const int esize = dtype_x == MHC_DTYPE_F32 ? 4 : 2;
+  const int span_esize = gx_f32 && grad_x ? 4 : esize;  // the wider of x and grad_x
   const bool mfma_ok = R >= kMfmaMinRows && K % (16 / esize) == 0 && aligned16(x) && (!grad_x || aligned16(grad_x));
   // the row chunks of the pass that runs (the MFMA plan has at most w.nR)
-  const WidePlan pl = mfma_ok ? mfma_bwd_plan(R, K, w) : w;
+  const WidePlan pl = mfma_ok ? mfma_bwd_plan(R, K, w, span_esize) : w;
   float* gphi_part = (pl.nR > 1 && grad_phi) ? (float*)split_ws : nullptr;
   float* bias_part = nullptr;  // MFMA path, split rows: per-chunk grad_bias / grad_alpha records
   int rc;
   // (the kernel's buffer spans reach up to four blocks past a chunk's rows)
-  if (mfma_ok && span_ok((pl.RC + 4 * kBwdRows) * K, esize) && span_ok((pl.RC + 4 * kBwdRows) * kRow, 4)) {
+  if (mfma_ok && span_ok((pl.RC + 4 * kBwdRows) * K, span_esize) && span_ok((pl.RC + 4 * kBwdRows) * kRow, 4)) {
     // rows in bulk: grad_x and grad_phi on MFMA.
     if (pl.nR > 1 && (grad_bias || grad_alpha))
       bias_part = (float*)(split_ws + align256((size_t)w.nR * K * kOut * sizeof(float)));
     const dim3 grid((unsigned)((K + 32 * kBwdWaves - 1) / (32 * kBwdWaves)), (unsigned)pl.nR);
+    // Chunks of one 64-row block load it alone: with 16-bit x and grad_x, loads of the next
+    // block (out of range) in flight as well cost 1.3-2.2 us at R = 64-256, K = 16384; from two
+    // blocks on the two ahead time alike, from six (R = 1536) they win by 1.6-2.6 us.
     rc = MHC_DISPATCH_DTYPE(dtype_x, [&] {
-      dynw_bwd_mfma_kernel<T><<<grid, 64 * kBwdWaves, 0, st>>>((const T*)x, phi, rowbuf, (T*)grad_x, grad_phi,
-                                                               gphi_part, bias_part, grad_bias, grad_alpha, R, K,
-                                                               pl.RC);
+      if (gx_f32)
+        dynw_bwd_mfma_kernel<T, float><<<grid, 64 * kBwdWaves, 0, st>>>(
+            (const T*)x, phi, rowbuf, (float*)grad_x, grad_phi, gphi_part, bias_part, grad_bias, grad_alpha, R, K,
+            pl.RC);
+      else if (pl.RC <= kBwdRows)
+        dynw_bwd_mfma_kernel<T, T, 1><<<grid, 64 * kBwdWaves, 0, st>>>(
+            (const T*)x, phi, rowbuf, (T*)grad_x, grad_phi, gphi_part, bias_part, grad_bias, grad_alpha, R, K,
+            pl.RC);
+      else
+        dynw_bwd_mfma_kernel<T><<<grid, 64 * kBwdWaves, 0, st>>>((const T*)x, phi, rowbuf, (T*)grad_x, grad_phi,
+                                                                 gphi_part, bias_part, grad_bias, grad_alpha, R,
+                                                                 K, pl.RC);
       return hip_status(hipGetLastError(), "dynamic_weights_backward mfma launch");
     });
   } else {
     rc = MHC_DISPATCH_DTYPE(dtype_x, [&] {
-      return hip_status(launch_dynw_bwd_wide<T, T>((const T*)x, phi, rowbuf, (T*)grad_x, grad_phi, gphi_part,
-                                                   grad_bias, grad_alpha, R, K, pl.RC, (unsigned)pl.nR, phi_vec, st),
-                        "dynamic_weights_backward wide launch");
+      const hipError_t e =
+          gx_f32 ? launch_dynw_bwd_wide<T, float>((const T*)x, phi, rowbuf, (float*)grad_x, grad_phi, gphi_part,
+                                                  grad_bias, grad_alpha, R, K, pl.RC, (unsigned)pl.nR, phi_vec, st)
+                 : launch_dynw_bwd_wide<T, T>((const T*)x, phi, rowbuf, (T*)grad_x, grad_phi, gphi_part, grad_bias,
+                                              grad_alpha, R, K, pl.RC, (unsigned)pl.nR, phi_vec, st);
+      return hip_status(e, "dynamic_weights_backward wide launch");
     });
   }
   if (rc || (!gphi_part && !bias_part)) return rc;
@@ -304,7 +323,7 @@ extern "C" int mhc_dynamic_weights_backward(const void* x, int dtype_x, const fl
       aux, P, InRow{H_pre, 4}, InRow{grad_H_pre, 4}, InRow{grad_H_post, 4}, InRow{grad_H_res, 16}, nullptr, 0,
       rowbuf, R, K, iters, eps);
   if (int rc = hip_status(hipGetLastError(), "dynamic_weights_backward rows launch")) return rc;
-  return dynw_grad_pass(x, dtype_x, phi, rowbuf, grad_x, grad_phi, grad_bias, grad_alpha, R, K,
+  return dynw_grad_pass(x, dtype_x, phi, rowbuf, grad_x, false, grad_phi, grad_bias, grad_alpha, R, K,
                         (char*)workspace + align256((size_t)R * kRow * sizeof(float)), st);
 }
 

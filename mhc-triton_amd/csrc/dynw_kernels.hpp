@@ -815,11 +815,12 @@ __device__ __forceinline__ u32x2 lds_read_tr16(const __bf16* p) {
   return __builtin_bit_cast(u32x2, __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(p)));
 }
 
-template <typename TX, int NW = kBwdWaves, int MINW = kBwdMinWaves>
+template <typename TX, typename TG = TX, int AH = (sizeof(TX) == 4 || sizeof(TG) == 4) ? 1 : kBwdAhead,
+          int NW = kBwdWaves, int MINW = kBwdMinWaves>
 __global__ __launch_bounds__(64 * NW, MINW) void dynw_bwd_mfma_kernel(const TX* __restrict__ x,
                                                                     const float* __restrict__ phi,
                                                                     const float* __restrict__ rowbuf,
-                                                                    TX* __restrict__ gx, float* __restrict__ gphi,
+                                                                    TG* __restrict__ gx, float* __restrict__ gphi,
                                                                     float* __restrict__ gphi_part,
                                                                     float* __restrict__ bias_part,
                                                                     float* __restrict__ gbias,
@@ -834,17 +835,30 @@ __global__ __launch_bounds__(64 * NW, MINW) void dynw_bwd_mfma_kernel(const TX* 
   constexpr int XLPR = kBwdCols / VE;          // lanes per x row (16 bytes each)
   constexpr int XRPP = kBwdThreads / XLPR;     // x rows per pass of the workgroup
   constexpr int NX = TR / XRPP;                // 16-byte x vectors per lane per block
+  // grad_x is written in TG: x's type, or f32 from 16-bit x (the layer at S = 1 reads H's rows
+  // as x and keeps grad_x in f32 for pass C); same tile walk with TG's vector width
+  constexpr int EG = (int)sizeof(TG);
+  constexpr int VEG = 16 / EG;
+  constexpr int kBwdGXPitch = kBwdCols + VEG;  // elements per padded LDS row of the grad_x tile
+  constexpr int XLPRG = kBwdCols / VEG;
+  constexpr int XRPPG = kBwdThreads / XLPRG;
+  constexpr int NXG = TR / XRPPG;
+  static_assert(TR % XRPPG == 0 && (__is_same(TG, TX) || __is_same(TG, float)), "grad_x tile");
   constexpr int GRPP = kBwdThreads / 8;        // G rows per pass (8 lanes per 32-float row)
   constexpr int NG = TR / GRPP > 0 ? TR / GRPP : 1;
   static_assert(TR % XRPP == 0 && (TR % GRPP == 0 || GRPP >= TR), "block shape");
   constexpr bool kXF16 = __is_same(TX, _Float16);
   constexpr bool kXF32 = __is_same(TX, float);
   static_assert(kXF16 || kXF32 || __is_same(TX, __bf16), "x is bf16, fp16 or fp32");
-  // Blocks of loads in flight: fp32 blocks are twice the bytes in the same registers.
-  constexpr int A = kXF32 ? 1 : kBwdAhead;
-  // The x and grad_x tiles hold TX values (fp32: 2 x 66.5 KiB of LDS); the G planes are bf16.
+  // Blocks of loads in flight (AH): by default one for fp32 x, whose blocks are twice the bytes in
+  // the same registers, and for an f32 grad_x from 16-bit x (layer backward at S = 1, D = 4096:
+  // 32.2 -> 30.0 us at 64 rows, the same at 1024 and 4096 rows), else kBwdAhead; the launcher
+  // takes one for chunks of a single block.
+  constexpr int A = AH;
+  static_assert(A >= 1 && A <= kBwdAhead, "blocks ahead");
+  // The x and grad_x tiles hold TX and TG values (fp32: 2 x 66.5 KiB of LDS); the G planes are bf16.
   __shared__ __attribute__((aligned(16))) TX xs[TR * kBwdXPitch];
-  __shared__ __attribute__((aligned(16))) TX gxs[TR * kBwdXPitch];
+  __shared__ __attribute__((aligned(16))) TG gxs[TR * kBwdGXPitch];
   __shared__ __attribute__((aligned(16))) __bf16 ghi[TR * kBwdGPitch];
   __shared__ __attribute__((aligned(16))) __bf16 glo[TR * kBwdGPitch];
   __shared__ float cf[TR];
@@ -883,9 +897,9 @@ __global__ __launch_bounds__(64 * NW, MINW) void dynw_bwd_mfma_kernel(const TX* 
   // block's loads as well.)
   const int64_t nrows = r_end - r_beg;
   const Span<TX, true> xsp(x + r_beg * K, nrows * K);
-  const Span<TX, true> gxsp(gx ? gx + r_beg * K : x, gx ? nrows * K : 0);
+  const Span<TG, true> gxsp(gx ? gx + r_beg * K : reinterpret_cast<const TG*>(x), gx ? nrows * K : 0);
   const Span<float, true> gsp(rowbuf + r_beg * kRow, nrows * kRow);
-  constexpr uint32_t kOobX = 0x80000000u / E, kOobF32 = 0x20000000u;  // 2^31 bytes
+  constexpr uint32_t kOobX = 0x80000000u / E, kOobG = 0x80000000u / EG, kOobF32 = 0x20000000u;  // 2^31 bytes
   const int xr = threadIdx.x / XLPR;
   const int xc = (threadIdx.x % XLPR) * VE;
   const bool xcol_ok = k0 + xc < K;
@@ -896,6 +910,12 @@ __global__ __launch_bounds__(64 * NW, MINW) void dynw_bwd_mfma_kernel(const TX* 
   // element offsets in the spans of row i of this lane in block b
   auto xoff = [&](int64_t b, int i) -> uint32_t {
     return xcol_ok ? (uint32_t)((TR * b + xr + XRPP * i) * K + k0 + xc) : kOobX;
+  };
+  const int gxr = threadIdx.x / XLPRG;
+  const int gxc = (threadIdx.x % XLPRG) * VEG;
+  const bool gxcol_ok = k0 + gxc < K;
+  auto goff = [&](int64_t b, int i) -> uint32_t {
+    return gxcol_ok ? (uint32_t)((TR * b + gxr + XRPPG * i) * K + k0 + gxc) : kOobG;
   };
   auto load_block = [&](int64_t b, u32x4 (&xv)[NX], f32x4 (&gv)[NG]) {
 #pragma unroll
@@ -1039,18 +1059,20 @@ __global__ __launch_bounds__(64 * NW, MINW) void dynw_bwd_mfma_kernel(const TX* 
       for (int q = 0; q < 4; ++q) {
         const int cc = 32 * wave + 8 * q + 4 * (lane >> 5);
         typedef TX tx4 __attribute__((ext_vector_type(4)));
+        typedef TG tg4 __attribute__((ext_vector_type(4)));
         const tx4 x4 = *reinterpret_cast<const tx4*>(&xs[row * kBwdXPitch + cc]);
-        tx4 o4;
+        tg4 o4;
 #pragma unroll
-        for (int r = 0; r < 4; ++r) o4[r] = (TX)(d[hh][4 * q + r] + c * (float)x4[r]);
-        *reinterpret_cast<tx4*>(&gxs[row * kBwdXPitch + cc]) = o4;
+        for (int r = 0; r < 4; ++r) o4[r] = (TG)(d[hh][4 * q + r] + c * (float)x4[r]);
+        *reinterpret_cast<tg4*>(&gxs[row * kBwdGXPitch + cc]) = o4;
       }
     }
     __syncthreads();
-    // grad_x tile out: rows xr + XRPP i, 16 bytes at column xc (no grad_x: an empty span).
+    // grad_x tile out: rows gxr + XRPPG i, 16 bytes at column gxc (no grad_x: an empty span).
 #pragma unroll
-    for (int i = 0; i < NX; ++i)
-      gxsp.template store16<true>(xoff(b, i), *reinterpret_cast<const u32x4*>(&gxs[(xr + XRPP * i) * kBwdXPitch + xc]));
+    for (int i = 0; i < NXG; ++i)
+      gxsp.template store16<true>(goff(b, i),
+                                  *reinterpret_cast<const u32x4*>(&gxs[(gxr + XRPPG * i) * kBwdGXPitch + gxc]));
     // No barrier here: every read of xs / ghi / glo / cf in this block came
     // before the barrier above, and gxs is next written after the next
     // block's first barrier, which waits for these reads.

@@ -29,8 +29,9 @@ bool dynw_project_rows_ok(int64_t R, int64_t K, const void* x, int dtype);
 int dynw_project_rows(const void* x, int dtype, const float* phi, float* part, int64_t R, int64_t K, int* nK,
                       hipStream_t st);
 size_t dynw_grad_split_bytes(int64_t R, int64_t K);
-int dynw_grad_pass(const void* x, int dtype_x, const float* phi, const float* rowbuf, void* grad_x, float* grad_phi,
-                   float* grad_bias, float* grad_alpha, int64_t R, int64_t K, char* split_ws, hipStream_t st);
+int dynw_grad_pass(const void* x, int dtype_x, const float* phi, const float* rowbuf, void* grad_x, bool gx_f32,
+                   float* grad_phi, float* grad_bias, float* grad_alpha, int64_t R, int64_t K, char* split_ws,
+                   hipStream_t st);
 
 // Batches from which the dynamic weights of the layer run as the op runs them for rows in bulk.
 // Below them the batch is a handful of rows: the projection folds into the mean-pool's reduce
@@ -488,7 +489,7 @@ extern "C" int mhc_layer_dynamic_backward(const void* H, int dtype, const void* 
   if (B == 0) return MHC_OK;
   const bool nz = S * D != 0;  // bulk tensors may be empty (null) when S * D == 0
   if ((nz && (!H || !d_branch_input)) || !phi || !H_pre_base || !H_post_base || !H_res_base || !alpha_pre ||
-      !alpha_post || !alpha_res || !x || !w || !aux) {
+      !alpha_post || !alpha_res || (!x && S != 1) || !w || !aux) {
     set_error("layer_dynamic_backward: null pointer");
     return MHC_ERR_ARG;
   }
@@ -512,13 +513,19 @@ extern "C" int mhc_layer_dynamic_backward(const void* H, int dtype, const void* 
       aux, P, InRow{w, kOut}, InRow{nullptr, 0}, InRow{dH_post, 4}, InRow{nullptr, 0}, part, (int)nblk, rowbuf, B,
       K, iters, eps);
   if ((rc = hip_status(hipGetLastError(), "layer weights backward rows launch"))) return rc;
+  // The pooled rows: x, or without it (S = 1) H's own rows, read in H's dtype; grad_x stays f32.
+  const void* xr = x ? (const void*)x : H;
+  const int xdt = x ? MHC_DTYPE_F32 : dtype;
   if (B >= kLayerBulkRows)
-    rc = dynw_grad_pass(x, MHC_DTYPE_F32, phi, rowbuf, dH ? gx : nullptr, grad_phi, grad_bias, grad_alpha, B, K,
+    rc = dynw_grad_pass(xr, xdt, phi, rowbuf, dH ? gx : nullptr, true, grad_phi, grad_bias, grad_alpha, B, K,
                         wsb + L.grad_split, st);
   else
-    rc = hip_status(launch_dynw_bwd_wide<float, float>(x, phi, rowbuf, dH ? gx : nullptr, grad_phi, nullptr,
-                                                       grad_bias, grad_alpha, B, K, B, 1u, aligned16(phi), st),
-                    "layer weights backward wide launch");
+    rc = MHC_DISPATCH_DTYPE(xdt, [&] {
+      return hip_status(launch_dynw_bwd_wide<T, float>((const T*)xr, phi, rowbuf, dH ? gx : nullptr, grad_phi,
+                                                       nullptr, grad_bias, grad_alpha, B, K, B, 1u, aligned16(phi),
+                                                       st),
+                        "layer weights backward wide launch");
+    });
   if (rc) return rc;
   if (!dH || S * D == 0) return MHC_OK;
   // Pass C: dH.

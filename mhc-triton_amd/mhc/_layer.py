@@ -86,7 +86,8 @@ def dynamic_forward(H, phi, H_pre_base, H_post_base, H_res_base, alpha_pre, alph
 def dynamic_backward(H, d_bi, dH_new, dH_post, phi, H_pre_base, H_post_base, H_res_base, alpha_pre,
                      alpha_post, alpha_res, x, w, aux, iters: int, eps: float, need_dH: bool = True):
     """mhc_layer_dynamic_backward -> (dH or None, grad_phi [4D,24], grad_bias [24], grad_alpha [3]), f32
-    parameter gradients.  dH_new / dH_post are the closure's gradients (None if it was not called)."""
+    parameter gradients.  dH_new / dH_post are the closure's gradients (None if it was not called).
+    x may be None at S = 1, where the pooled rows are H's rows and the kernels read them from H."""
     B, S, _, D = H.shape
     dev = _lib.require_gpu(H, phi)
     H = H.contiguous()
@@ -95,7 +96,10 @@ def dynamic_backward(H, d_bi, dH_new, dH_post, phi, H_pre_base, H_post_base, H_r
     dH_post = None if dH_post is None else _f32(dH_post)
     params = [_f32(t) for t in (phi, H_pre_base, H_post_base, H_res_base,
                                 alpha_pre.reshape(1), alpha_post.reshape(1), alpha_res.reshape(1))]
-    x, w, aux = _f32(x), _f32(w), _f32(aux)
+    if x is None and S != 1:
+        raise ValueError("mhc: layer_dynamic_backward needs the pooled rows x unless S == 1")
+    x = None if x is None else _f32(x)
+    w, aux = _f32(w), _f32(aux)
     dH = torch.empty_like(H) if need_dH else None
     gphi = torch.empty(4 * D, 24, device=dev, dtype=torch.float32)
     gbias = torch.empty(24, device=dev, dtype=torch.float32)
@@ -106,7 +110,7 @@ def dynamic_backward(H, d_bi, dH_new, dH_post, phi, H_pre_base, H_post_base, H_r
     with _lib.on_device(dev):
         _lib.check(lib.mhc_layer_dynamic_backward(
             H.data_ptr(), code, d_bi.data_ptr(), _lib.ptr(dH_new), _lib.ptr(dH_post),
-            *[p.data_ptr() for p in params], x.data_ptr(), w.data_ptr(), aux.data_ptr(),
+            *[p.data_ptr() for p in params], _lib.ptr(x), w.data_ptr(), aux.data_ptr(),
             _lib.ptr(dH), gphi.data_ptr(), gbias.data_ptr(), galpha.data_ptr(), B, S, D, int(iters), float(eps),
             *_wsargs(ws), _lib.stream(dev)), "layer_dynamic_backward")
     return dH, gphi, gbias, galpha
@@ -256,8 +260,9 @@ class _DynamicLayer(torch.autograd.Function):
                 iters: int, eps: float, keep_x: bool):
         params = (phi, H_pre_base, H_post_base, H_res_base, alpha_pre, alpha_post, alpha_res)
         # the pooled rows x serve only the backward: the caller drops them when no gradient can
-        # reach this node (ctx.needs_input_grad reflects requires_grad even under torch.no_grad)
-        bi, x, w, aux = dynamic_forward(H, *params, iters, eps, keep_x=keep_x)
+        # reach this node (ctx.needs_input_grad reflects requires_grad even under torch.no_grad),
+        # and at S = 1 they are H's rows, which the backward reads from H
+        bi, x, w, aux = dynamic_forward(H, *params, iters, eps, keep_x=keep_x and H.shape[1] != 1)
         ctx.save_for_backward(H, x, w, aux, *params)
         ctx.iters = iters
         ctx.eps = eps
@@ -267,7 +272,7 @@ class _DynamicLayer(torch.autograd.Function):
     @staticmethod
     def backward(ctx, d_bi, d_w, d_link, d_post):
         H, x, w, aux, *params = ctx.saved_tensors
-        if x is None:
+        if x is None and H.shape[1] != 1:
             raise RuntimeError("mhc: backward through a dynamic layer forward that kept no pooled rows "
                                "(it ran where no gradient could reach it)")
         dH, gphi, gbias, galpha = dynamic_backward(H, d_bi, d_link, d_post, *params, x, w, aux,

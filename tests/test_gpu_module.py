@@ -113,7 +113,8 @@ def test_unfused_dynamic_fp32():
                                          (4, 7, 96, torch.float32), (2, 9, 64, torch.bfloat16),
                                          (200, 3, 128, torch.bfloat16), (512, 1, 128, torch.float32),
                                          (600, 2, 64, torch.bfloat16), (515, 12, 32, torch.float16),
-                                         (520, 1, 99, torch.bfloat16), (70, 2, 99, torch.float32)])
+                                         (520, 1, 99, torch.bfloat16), (70, 2, 99, torch.float32),
+                                         (96, 1, 256, torch.float16), (600, 1, 128, torch.bfloat16)])
 def test_short_sequences(B, S, D, dtype):
     """Decode-like sequence lengths and batches of many sequences: S up to 8 takes the
     single-launch mean-pool (colsum_direct_kernel), S = 9 and 12 the two-kernel one; from 64
@@ -144,6 +145,41 @@ def test_no_grad_forward_matches_grad_forward(B, S, D, dtype):
     obi, oHn, _ = O.layer_forward(params_np(hc), to_np(H), to_np(bo), True, True, hc.sinkhorn_iters, hc.eps)
     tol = 1e-5 if dtype == torch.float32 else 2e-2
     assert rel_err(to_np(bi0), obi) < tol and rel_err(to_np(Hn0), oHn) < tol
+
+
+@pytest.mark.parametrize("B,D,dtype", [(5, 256, torch.bfloat16), (96, 256, torch.float16),
+                                       (600, 128, torch.bfloat16), (70, 99, torch.bfloat16),
+                                       (80, 64, torch.float32)])
+def test_s1_backward_reads_h_rows(B, D, dtype):
+    """At S = 1 the training forward keeps no pooled rows: the backward reads H's rows in H's dtype
+    (x = H exactly, as the mean of one row).  Its gradients against the same backward given x in
+    f32: the same bits where both run the same pass (below 64 batches the one-chunk VALU pass,
+    above it the MFMA pass, whose 16-bit x is one bf16 term where f32 x is hi + a zero mid); D = 99
+    in bf16 (4D % 8 = 4) leaves the 16-bit rows to the VALU pass, to fp32 tolerance."""
+    from mhc import _layer
+
+    hc, H, _, dHn, dbi = make_case(B, 1, D, dtype, phi_std=0.02)
+    params = [hc.phi, hc.H_pre_base, hc.H_post_base, hc.H_res_base, hc.alpha_pre, hc.alpha_post, hc.alpha_res]
+    params = [p.detach() for p in params]
+    bi, x, w, aux = _layer.dynamic_forward(H, *params, hc.sinkhorn_iters, hc.eps)
+    bi0, x0, w0, aux0 = _layer.dynamic_forward(H, *params, hc.sinkhorn_iters, hc.eps, keep_x=False)
+    assert x0 is None and torch.equal(x, H.float().reshape(B, 4 * D))
+    assert torch.equal(bi, bi0) and torch.equal(w, w0) and torch.equal(aux, aux0)
+    dpost = torch.randn((B, 4), device=DEV)
+    got = _layer.dynamic_backward(H, dbi, dHn, dpost, *params, None, w, aux, hc.sinkhorn_iters, hc.eps)
+    want = _layer.dynamic_backward(H, dbi, dHn, dpost, *params, x, w, aux, hc.sinkhorn_iters, hc.eps)
+    exact = dtype == torch.float32 or D % 2 == 0
+    for name, g, t in zip(("dH", "grad_phi", "grad_bias", "grad_alpha"), got, want):
+        if exact:
+            assert torch.equal(g, t), name
+        else:
+            # fp32 sums in another order; dH (bf16) then rounds a few elements the other way
+            e = rel_err(to_np(g), to_np(t))
+            print(f"{name}: {e:.2e}", flush=True)
+            assert e < (1e-2 if name == "dH" else 1e-5), (name, e)
+    with pytest.raises(ValueError):
+        _layer.dynamic_backward(H.expand(B, 2, 4, D), dbi.expand(B, 2, D), None, None, *params, None, w, aux,
+                                hc.sinkhorn_iters, hc.eps)
 
 
 def test_ragged_dim_bf16():
