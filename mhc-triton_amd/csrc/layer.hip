@@ -221,36 +221,52 @@ static int mix_bwd_dispatch(const void* dbi, const void* dhn, const void* H, con
                                                        D, nblk, st);
 }
 
-// Pass C of the dynamic backward: two tokens per lane (grad_x loaded once for
-// both), 2 workgroups per CU; both measured best at config-3 size.
-constexpr int kDhTokens = 2;
+// Pass C of the dynamic backward: TT tokens per lane, grad_x loaded once for all of them, 2
+// workgroups per CU.  Two tokens measured best at config-3 size (eight: 5 us slower per step).
+// A short sequence fits in one group instead, or two at S <= 16, so that grad_x is read once or
+// twice per batch rather than S / 2 times (training steps, D = 4096 bf16, two tokens -> dh_tokens:
+// S = 3 292.8 -> 283.6 us, S = 4 331.7 -> 323.9, S = 5 327.6 -> 317.5, S = 8 307.5 -> 295.1,
+// S = 16 313.9 -> 307.8; at S = 32 and 64 eight tokens gained 1-2 us).  The same arithmetic per
+// element: the same bits for every choice.
+static int dh_tokens(int64_t S) { return S <= 2 ? 2 : (S <= 4 ? 4 : (S <= 16 ? 8 : 2)); }
 
-template <typename T, int W, bool HAS_DHN>
+template <typename T, int W, bool HAS_DHN, int TT>
 static int launch_dh(const T* dbi, const T* dhn, const float* gx, const float* w, T* dH, int64_t B, int64_t S,
                      int64_t D, hipStream_t st) {
-  const int64_t groups = (S + kDhTokens - 1) / kDhTokens;
+  const int64_t groups = (S + TT - 1) / TT;
   const int64_t items = groups * (D / W);  // (token group, column vector) pairs, < 2^32 by check_bsd
   if (items == 0) return MHC_OK;
   const unsigned nwg = (unsigned)((items + kThreads - 1) / kThreads);
   const float inv_S = 1.f / (float)S;
   return for_batch_chunks(B, [&](int64_t b0, int64_t nb) {
-    dh_kernel<T, W, kDhTokens, HAS_DHN, kNt><<<dim3(nwg, (unsigned)nb), kThreads, occupancy_lds(2), st>>>(
+    dh_kernel<T, W, TT, HAS_DHN, kNt><<<dim3(nwg, (unsigned)nb), kThreads, occupancy_lds(2), st>>>(
         dbi, dhn, gx, inv_S, WRow{w, kOut}, WRow{w + 8, kOut}, dH, S, D, (uint32_t)groups, b0);
     return hip_status(hipGetLastError(), "layer dH launch");
   });
+}
+
+template <typename T, int W, bool HAS_DHN>
+static int launch_dh_tt(int tt, const T* dbi, const T* dhn, const float* gx, const float* w, T* dH, int64_t B,
+                        int64_t S, int64_t D, hipStream_t st) {
+  if (tt == 8) return launch_dh<T, W, HAS_DHN, 8>(dbi, dhn, gx, w, dH, B, S, D, st);
+  if (tt == 4) return launch_dh<T, W, HAS_DHN, 4>(dbi, dhn, gx, w, dH, B, S, D, st);
+  return launch_dh<T, W, HAS_DHN, 2>(dbi, dhn, gx, w, dH, B, S, D, st);
 }
 
 template <typename T>
 static int dh_dispatch(const void* dbi, const void* dhn, const float* gx, const float* w, void* dH, int64_t B,
                        int64_t S, int64_t D, hipStream_t st) {
   constexpr int WV = Vec<T>::N;
+  int tt = dh_tokens(S);
   const bool vec = vec_ok(D, WV, {dbi, dhn, dH}) && aligned16(gx);
+  // a tile's buffer spans grow with the tokens per lane (vec_ok bounds them for two)
+  if (vec && !span_ok(tt / 2 * (16384 + 8 * D), 4)) tt = 2;
   if (dhn) {
-    if (vec) return launch_dh<T, WV, true>((const T*)dbi, (const T*)dhn, gx, w, (T*)dH, B, S, D, st);
-    return launch_dh<T, 1, true>((const T*)dbi, (const T*)dhn, gx, w, (T*)dH, B, S, D, st);
+    if (vec) return launch_dh_tt<T, WV, true>(tt, (const T*)dbi, (const T*)dhn, gx, w, (T*)dH, B, S, D, st);
+    return launch_dh_tt<T, 1, true>(tt, (const T*)dbi, (const T*)dhn, gx, w, (T*)dH, B, S, D, st);
   }
-  if (vec) return launch_dh<T, WV, false>((const T*)dbi, nullptr, gx, w, (T*)dH, B, S, D, st);
-  return launch_dh<T, 1, false>((const T*)dbi, nullptr, gx, w, (T*)dH, B, S, D, st);
+  if (vec) return launch_dh_tt<T, WV, false>(tt, (const T*)dbi, nullptr, gx, w, (T*)dH, B, S, D, st);
+  return launch_dh_tt<T, 1, false>(tt, (const T*)dbi, nullptr, gx, w, (T*)dH, B, S, D, st);
 }
 
 }  // namespace mhc

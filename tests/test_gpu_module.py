@@ -114,14 +114,16 @@ def test_unfused_dynamic_fp32():
                                          (200, 3, 128, torch.bfloat16), (512, 1, 128, torch.float32),
                                          (600, 2, 64, torch.bfloat16), (515, 12, 32, torch.float16),
                                          (520, 1, 99, torch.bfloat16), (70, 2, 99, torch.float32),
-                                         (96, 1, 256, torch.float16), (600, 1, 128, torch.bfloat16)])
+                                         (96, 1, 256, torch.float16), (600, 1, 128, torch.bfloat16),
+                                         (6, 5, 99, torch.bfloat16), (40, 16, 64, torch.float16)])
 def test_short_sequences(B, S, D, dtype):
     """Decode-like sequence lengths and batches of many sequences: S up to 8 takes the
     single-launch mean-pool (colsum_direct_kernel), S = 9 and 12 the two-kernel one; from 64
     batches the weights backward runs on the MFMA kernel in row chunks, from 512 the pooled
     rows' projection too; D = 99 (4D % 16 = 12) keeps the folded projection and the scalar
-    mean-pool, with the backward's MFMA pass on ragged column blocks.  Dynamic fused weights,
-    phi ~ N(0, 0.02)."""
+    mean-pool, with the backward's MFMA pass on ragged column blocks.  Pass C takes 2 tokens per
+    lane, 4 at S = 3-4 and 8 at S = 5-16 (S = 5 at D = 99 on the scalar path).  Dynamic fused
+    weights, phi ~ N(0, 0.02)."""
     hc, H, bo, dHn, dbi = make_case(B, S, D, dtype, phi_std=0.02)
     tol = 1e-5 if dtype == torch.float32 else 2e-2
     check_layer(hc, H, bo, dHn, dbi, tol, 1e-4 if dtype == torch.float32 else 2e-2, 1e-4)
