@@ -227,8 +227,15 @@ static int mix_bwd_dispatch(const void* dbi, const void* dhn, const void* H, con
 // twice per batch rather than S / 2 times (training steps, D = 4096 bf16, two tokens -> dh_tokens:
 // S = 3 292.8 -> 283.6 us, S = 4 331.7 -> 323.9, S = 5 327.6 -> 317.5, S = 8 307.5 -> 295.1,
 // S = 16 313.9 -> 307.8; at S = 32 and 64 eight tokens gained 1-2 us).  The same arithmetic per
-// element: the same bits for every choice.
-static int dh_tokens(int64_t S) { return S <= 2 ? 2 : (S <= 4 ? 4 : (S <= 16 ? 8 : 2)); }
+// element: the same bits for every choice.  Only while the grid keeps at least 1024 workgroups
+// (four per CU): at B = 64, S = 8 eight tokens left 128 and the step took 80.8 us against 79.5;
+// at 256 workgroups the larger groups went either way (B = 128, S = 8: 2.7 us less; B = 64,
+// S = 16: 1.7 us more).
+static int dh_tokens(int64_t B, int64_t S, int64_t D, int W) {
+  for (int tt = S <= 2 ? 2 : (S <= 4 ? 4 : (S <= 16 ? 8 : 2)); tt > 2; tt /= 2)
+    if (B * ((S + tt - 1) / tt) * (D / W) >= 1024 * (int64_t)kThreads) return tt;
+  return 2;
+}
 
 template <typename T, int W, bool HAS_DHN, int TT>
 static int launch_dh(const T* dbi, const T* dhn, const float* gx, const float* w, T* dH, int64_t B, int64_t S,
@@ -257,8 +264,8 @@ template <typename T>
 static int dh_dispatch(const void* dbi, const void* dhn, const float* gx, const float* w, void* dH, int64_t B,
                        int64_t S, int64_t D, hipStream_t st) {
   constexpr int WV = Vec<T>::N;
-  int tt = dh_tokens(S);
   const bool vec = vec_ok(D, WV, {dbi, dhn, dH}) && aligned16(gx);
+  int tt = dh_tokens(B, S, D, vec ? WV : 1);
   // a tile's buffer spans grow with the tokens per lane (vec_ok bounds them for two)
   if (vec && !span_ok(tt / 2 * (16384 + 8 * D), 4)) tt = 2;
   if (dhn) {

@@ -121,9 +121,9 @@ def test_short_sequences(B, S, D, dtype):
     single-launch mean-pool (colsum_direct_kernel), S = 9 and 12 the two-kernel one; from 64
     batches the weights backward runs on the MFMA kernel in row chunks, from 512 the pooled
     rows' projection too; D = 99 (4D % 16 = 12) keeps the folded projection and the scalar
-    mean-pool, with the backward's MFMA pass on ragged column blocks.  Pass C takes 2 tokens per
-    lane, 4 at S = 3-4 and 8 at S = 5-16 (S = 5 at D = 99 on the scalar path).  Dynamic fused
-    weights, phi ~ N(0, 0.02)."""
+    mean-pool, with the backward's MFMA pass on ragged column blocks.  (Pass C's 4 and 8 tokens
+    per lane at S = 3-16 need grids of 1024 workgroups: test_gpu_rounding covers them.)  Dynamic
+    fused weights, phi ~ N(0, 0.02)."""
     hc, H, bo, dHn, dbi = make_case(B, S, D, dtype, phi_std=0.02)
     tol = 1e-5 if dtype == torch.float32 else 2e-2
     check_layer(hc, H, bo, dHn, dbi, tol, 1e-4 if dtype == torch.float32 else 2e-2, 1e-4)

@@ -234,6 +234,26 @@ def test_layer_rounds_once(kind, dtype):
     check_layer_rounding(kind, hc, H, bo, dHn, dbi)
 
 
+@pytest.mark.parametrize("B,S,D,dtype", [(2048, 4, 1024, torch.bfloat16), (2048, 7, 1024, torch.float16),
+                                         (2700, 5, 99, torch.bfloat16)])
+def test_dh_many_short_sequences_rounds_once(B, S, D, dtype):
+    """Pass C (mhc_layer_mix_dh) where a lane takes 4 tokens (S = 4) or 8 (S = 5 and 7; D = 99 on
+    the scalar path), with grids of 1024 workgroups and more, against the float64 expression
+    rounded once: dH[m] = pre[m] d_bi + sum_n res[n, m] dH_new[n] + grad_x[m] / S."""
+    from mhc import _layer
+
+    g = torch.Generator(device=DEV).manual_seed(11)
+    dbi = _randn(g, (B, S, D), dtype)
+    dHn = _randn(g, (B, S, 4, D), dtype)
+    w = torch.rand((B, 24), generator=g, device=DEV)
+    gx = _randn(g, (B, 4 * D))
+    dH = _layer.mix_dh(dbi, dHn, w, gx, (B, S, 4, D), dtype)
+    w64 = w.double()
+    dH64, dHa = _dh_ref(dbi.double(), dHn.double(), w64[:, 0:4], w64[:, 8:24].reshape(B, 4, 4))
+    gxs = gx.double().reshape(B, 1, 4, D) / S
+    assert_rounded_once(dH, dH64 + gxs, dHa + gxs.abs(), f"dH B={B} S={S} D={D}")
+
+
 def test_layer_rounds_once_ragged_dim():
     """D = 100: the scalar (one element per lane) path of every streaming kernel."""
     hc, H, bo, dHn, dbi = _layer_case("dynamic", torch.bfloat16, 3, 40, 100, seed=4)
