@@ -227,7 +227,8 @@ int dynw_grad_pass(const void* x, int dtype_x, const float* phi, const float* ro
   const WidePlan w = wide_plan(R, K);
   const int esize = dtype_x == MHC_DTYPE_F32 ? 4 : 2;
   const int span_esize = gx_f32 && grad_x ? 4 : esize;  // the wider of x and grad_x
-  const bool mfma_ok = R >= kMfmaMinRows && K % (16 / esize) == 0 && aligned16(x) && (!grad_x || aligned16(grad_x));
+  const bool mfma_ok = R >= kMfmaMinRows && K > 0 && K % (16 / esize) == 0 && aligned16(x) &&
+                       (!grad_x || aligned16(grad_x));
   // the row chunks of the pass that runs (the MFMA plan has at most w.nR)
   const WidePlan pl = mfma_ok ? mfma_bwd_plan(R, K, w, span_esize) : w;
   float* gphi_part = (pl.nR > 1 && grad_phi) ? (float*)split_ws : nullptr;
