@@ -37,10 +37,10 @@ def _check_oracle(hc, H, bo, dHn, dbi, got, dtype):
         assert err < 1e-4, n
 
 
-def _setup(dynamic, fused=True, seed=0, dtype=torch.bfloat16):
+def _setup(dynamic, fused=True, seed=0, dtype=torch.bfloat16, shape=(2, 64, 256)):
     import mhc
 
-    B, S, D = 2, 64, 256
+    B, S, D = shape
     g = torch.Generator(device="cuda")
     g.manual_seed(seed)
     hc = mhc.HyperConnection(D, dynamic=dynamic, use_fused_weights=fused).cuda()
@@ -75,7 +75,17 @@ def _snapshot(hc, H, bo, bi, H_new):
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
 @pytest.mark.parametrize("dynamic,fused", [(True, True), (False, True), (True, False)])
 def test_layer_step_graph_replays_match_eager(dynamic, fused, dtype):
-    hc, H, bo, dHn, dbi, mk = _setup(dynamic, fused, dtype=dtype)
+    _graph_replays_match_eager(*_setup(dynamic, fused, dtype=dtype), dtype)
+
+
+@pytest.mark.parametrize("shape", [(600, 1, 128), (530, 3, 64)])
+def test_many_sequences_graph_replays_match_eager(shape):
+    """Many short sequences, dynamic fused weights: the bulk-batch paths (the projection and the
+    weights backward on the MFMA kernels; at S = 1 both read H's rows, with no pooled rows kept)."""
+    _graph_replays_match_eager(*_setup(True, True, dtype=torch.bfloat16, shape=shape), torch.bfloat16)
+
+
+def _graph_replays_match_eager(hc, H, bo, dHn, dbi, mk, dtype):
     ref = _snapshot(hc, H, bo, *_step(hc, H, bo, dHn, dbi))
 
     side = torch.cuda.Stream()

@@ -160,3 +160,32 @@ def test_layer_overwrites_what_it_reads(kind, closure, dtype, D):
         return res
 
     _twice(run)
+
+
+@pytest.mark.parametrize("B,S,D", [(600, 1, 128), (530, 3, 64), (512, 5, 4096)])
+def test_many_sequences_layer_overwrites_what_it_reads(B, S, D):
+    """The dynamic layer's bulk-batch paths: the mean-pool without the projection, the pooled
+    rows (at S = 1 H's own rows, with no x kept) projected and differentiated on the MFMA
+    kernels in row chunks, and at B = 512, S = 5, D = 4096 pass C at 8 tokens per lane."""
+    import mhc
+
+    g = torch.Generator(device=DEV).manual_seed(3)
+    hc = mhc.HyperConnection(D).to(DEV)
+    with torch.no_grad():
+        for p in hc.parameters():
+            p.add_(_rand(g, *p.shape, scale=0.05))
+    H = _rand(g, B, S, 4, D, dtype=torch.bfloat16)
+    bo = _rand(g, B, S, D, dtype=torch.bfloat16)
+    dHn, dbi = _rand(g, B, S, 4, D, dtype=torch.bfloat16), _rand(g, B, S, D, dtype=torch.bfloat16)
+
+    def run():
+        hc.zero_grad(set_to_none=True)
+        Hl, bol = H.clone().requires_grad_(True), bo.clone().requires_grad_(True)
+        bi, add = hc(Hl)
+        Hn = add(bol)
+        torch.autograd.backward([Hn, bi], [dHn, dbi])
+        res = {"bi": bi, "Hn": Hn, "dH": Hl.grad, "dbo": bol.grad}
+        res.update({n: p.grad for n, p in hc.named_parameters()})
+        return res
+
+    _twice(run)
