@@ -39,11 +39,15 @@ int dynw_grad_pass(const void* x, int dtype_x, const float* phi, const float* ro
 // latency is what counts there.  At B = 4096, S = 1, D = 4096 the folded projection took 397 us
 // and the one-chunk backward 1842 us.  Measured crossovers (graph-replayed steps at D = 4096):
 // the backward on the MFMA kernel in row chunks wins from 64 batches on (fwd+bwd 69 -> 59 us at
-// B = 64, 2504 -> 622 us at B = 4096); the projection of the pooled rows on the MFMA kernel, after
-// a mean-pool without it, only from 512 on (forward 72 -> 63 us at B = 512, 457 -> 329 us at
-// B = 4096; 28 against 23 us at B = 64).
+// B = 64, 2504 -> 622 us at B = 4096).  The projection on the MFMA kernel: at S = 1, where it
+// reads H's rows and no mean-pool runs, from 64 batches (no-grad forward with the closure / training
+// step: B = 96 27.1 -> 24.2 / 61.1 -> 58.5 us, B = 256 42.2 -> 27.3 / 91.0 -> 73.7; equal at 64);
+// for S > 1, after a mean-pool without it, from 256 (B = 256, S = 8: 88.1 -> 79.9 / 190.4 ->
+// 183.5; S = 32: 235.7 -> 222.2 / 532.5 -> 515.8; at 128 it went either way: S = 4, D = 2048
+// 26.8 -> 29.6 / 67.6 -> 69.8, S = 16 82.1 -> 76.4 / 181.3 -> 175.2).
 constexpr int64_t kLayerBulkRows = 64;
-constexpr int64_t kLayerBulkProjRows = 512;
+constexpr int64_t kLayerBulkProjRowsS1 = 64;
+constexpr int64_t kLayerBulkProjRows = 256;
 
 constexpr int kLU = 1;   // items per lane per tile, streaming passes
 constexpr int kLRU = 2;  // items per lane per tile, the reduction-only pass B
@@ -330,7 +334,8 @@ static int layer_dynamic_forward_run(const void* H, int dtype, const float* phi,
   // allocation-free entry) then takes the folded projection below.
   const bool s1 = S == 1 && dynw_project_rows_ok(B, K, H, dtype);
   float* xp = x ? x : (full_ws ? (float*)(wsb + L.gx) : nullptr);
-  if (B >= kLayerBulkProjRows && (s1 || (xp && dynw_project_rows_ok(B, K, xp, MHC_DTYPE_F32)))) {
+  if (s1 ? B >= kLayerBulkProjRowsS1
+         : (B >= kLayerBulkProjRows && xp && dynw_project_rows_ok(B, K, xp, MHC_DTYPE_F32))) {
     if (x || !s1)
       if (int rc = mean_pool_any(H, dtype, xp, nullptr, nullptr, (float*)(wsb + L.colpart), B, S, D, nullptr, st))
         return rc;
