@@ -223,9 +223,10 @@ int mhc_layer_dynamic_forward(const void* H, int dtype, const float* phi,
  * is looked up on the first call on each GPU and kept for the process: once
  * this entry point has run on a GPU, do not call it there again after
  * hipDeviceReset (which unloads the code object the address points into).
- * With x NULL at 256 batches or more and S > 1 its weights can differ in their
- * last bits from the workspace entry's: it has no room to keep the pooled rows
- * for their projection, and folds the projection into the mean-pool instead. */
+ * With x NULL, S > 1 and B * D of 2^19 or more (B >= 64) its weights can
+ * differ in their last bits from the workspace entry's: it has no room to keep
+ * the pooled rows for their projection, and folds the projection into the
+ * mean-pool instead. */
 int mhc_layer_dynamic_forward_noalloc(const void* H, int dtype, const float* phi,
                                       const float* H_pre_base, const float* H_post_base,
                                       const float* H_res_base, const float* alpha_pre,

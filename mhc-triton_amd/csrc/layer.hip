@@ -42,12 +42,15 @@ int dynw_grad_pass(const void* x, int dtype_x, const float* phi, const float* ro
 // B = 64, 2504 -> 622 us at B = 4096).  The projection on the MFMA kernel: at S = 1, where it
 // reads H's rows and no mean-pool runs, from 64 batches (no-grad forward with the closure / training
 // step: B = 96 27.1 -> 24.2 / 61.1 -> 58.5 us, B = 256 42.2 -> 27.3 / 91.0 -> 73.7; equal at 64);
-// for S > 1, after a mean-pool without it, from 256 (B = 256, S = 8: 88.1 -> 79.9 / 190.4 ->
-// 183.5; S = 32: 235.7 -> 222.2 / 532.5 -> 515.8; at 128 it went either way: S = 4, D = 2048
-// 26.8 -> 29.6 / 67.6 -> 69.8, S = 16 82.1 -> 76.4 / 181.3 -> 175.2).
+// for S > 1, after a mean-pool without it, from 64 batches once B * D reaches 2^19: the folded
+// projection re-reads phi (4 D x 24 floats) for every batch, so the crossover scales with B * D
+// (B = 256, S = 8: 88.1 -> 79.9 / 190.4 -> 183.5; B = 128, S = 16: 82.1 -> 76.5 / 181.1 ->
+// 175.8; B = 80, S = 32, D = 7168: 141.0 -> 135.9 / 317.6 -> 310.8; at B = 128, S = 4 the
+// forward lost 1.7 us and the step gained 1.6; below 2^19, at B = 128, D = 2048, S = 4 it lost:
+// 26.8 -> 29.6 / 67.6 -> 69.8).
 constexpr int64_t kLayerBulkRows = 64;
 constexpr int64_t kLayerBulkProjRowsS1 = 64;
-constexpr int64_t kLayerBulkProjRows = 256;
+constexpr int64_t kLayerBulkProjElems = (int64_t)1 << 19;  // B * D
 
 constexpr int kLU = 1;   // items per lane per tile, streaming passes
 constexpr int kLRU = 2;  // items per lane per tile, the reduction-only pass B
@@ -335,7 +338,8 @@ static int layer_dynamic_forward_run(const void* H, int dtype, const float* phi,
   const bool s1 = S == 1 && dynw_project_rows_ok(B, K, H, dtype);
   float* xp = x ? x : (full_ws ? (float*)(wsb + L.gx) : nullptr);
   if (s1 ? B >= kLayerBulkProjRowsS1
-         : (B >= kLayerBulkProjRows && xp && dynw_project_rows_ok(B, K, xp, MHC_DTYPE_F32))) {
+         : (B >= kLayerBulkRows && B * D >= kLayerBulkProjElems && xp &&
+            dynw_project_rows_ok(B, K, xp, MHC_DTYPE_F32))) {
     if (x || !s1)
       if (int rc = mean_pool_any(H, dtype, xp, nullptr, nullptr, (float*)(wsb + L.colpart), B, S, D, nullptr, st))
         return rc;

@@ -116,12 +116,13 @@ def test_unfused_dynamic_fp32():
                                          (520, 1, 99, torch.bfloat16), (70, 2, 99, torch.float32),
                                          (96, 1, 256, torch.float16), (600, 1, 128, torch.bfloat16),
                                          (6, 5, 99, torch.bfloat16), (40, 16, 64, torch.float16),
-                                         (80, 1, 128, torch.bfloat16), (300, 3, 64, torch.bfloat16)])
+                                         (80, 1, 128, torch.bfloat16), (300, 3, 64, torch.bfloat16),
+                                         (512, 2, 1024, torch.bfloat16), (66, 3, 8192, torch.float16)])
 def test_short_sequences(B, S, D, dtype):
     """Decode-like sequence lengths and batches of many sequences: S up to 8 takes the
     single-launch mean-pool (colsum_direct_kernel), S = 9 and 12 the two-kernel one; from 64
     batches the weights backward runs on the MFMA kernel in row chunks, and the projection too
-    at S = 1 (on H's rows), for S > 1 from 256 (on the pooled rows); D = 99 (4D % 16 = 12) keeps the folded projection and the scalar
+    at S = 1 (on H's rows), for S > 1 once B * D reaches 2^19 (on the pooled rows); D = 99 (4D % 16 = 12) keeps the folded projection and the scalar
     mean-pool, with the backward's MFMA pass on ragged column blocks.  (Pass C's 4 and 8 tokens
     per lane at S = 3-16 need grids of 1024 workgroups: test_gpu_rounding covers them.)  Dynamic
     fused weights, phi ~ N(0, 0.02)."""
@@ -133,7 +134,8 @@ def test_short_sequences(B, S, D, dtype):
 @pytest.mark.parametrize("B,S,D,dtype", [(600, 1, 128, torch.bfloat16), (520, 3, 64, torch.bfloat16),
                                          (8, 4, 256, torch.float32), (3, 20, 96, torch.bfloat16),
                                          (512, 1, 64, torch.float16), (530, 1, 99, torch.bfloat16),
-                                         (100, 1, 128, torch.bfloat16), (300, 4, 64, torch.bfloat16)])
+                                         (100, 1, 128, torch.bfloat16), (300, 4, 64, torch.bfloat16),
+                                         (260, 4, 2048, torch.bfloat16)])
 def test_no_grad_forward_matches_grad_forward(B, S, D, dtype):
     """A forward no gradient reaches keeps no pooled rows x (at S = 1 with many batches it never
     forms them: the projection reads H's rows); branch_input and the closure's H_new come out

@@ -162,7 +162,7 @@ def test_layer_overwrites_what_it_reads(kind, closure, dtype, D):
     _twice(run)
 
 
-@pytest.mark.parametrize("B,S,D", [(600, 1, 128), (530, 3, 64), (512, 5, 4096)])
+@pytest.mark.parametrize("B,S,D", [(600, 1, 128), (530, 3, 1024), (512, 5, 4096)])
 def test_many_sequences_layer_overwrites_what_it_reads(B, S, D):
     """The dynamic layer's bulk-batch paths: the mean-pool without the projection, the pooled
     rows (at S = 1 H's own rows, with no x kept) projected and differentiated on the MFMA
