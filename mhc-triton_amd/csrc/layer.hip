@@ -541,9 +541,18 @@ extern "C" int mhc_layer_dynamic_backward(const void* H, int dtype, const void* 
   // kernel also sums grad_bias / grad_alpha.
   DynParams P{H_pre_base, H_post_base, H_res_base, alpha_pre, alpha_post, alpha_res};
   const int64_t K = 4 * D;
-  dynw_bwd_rows_kernel<1><<<dim3((unsigned)B), kThreads, 0, st>>>(
-      aux, P, InRow{w, kOut}, InRow{nullptr, 0}, InRow{dH_post, 4}, InRow{nullptr, 0}, part, (int)nblk, rowbuf, B,
-      K, iters, eps);
+  // A workgroup per batch sums up to thousands of partials (B = 1: 2048); with at most 64 per
+  // batch (from 32 batches on) one wave's lanes hold them all, so a workgroup takes four batches,
+  // a wave each, and adds the same four 16-lane row sums in the same order (B = 4096, S = 1:
+  // 16.0 us for one batch per workgroup, whose Sinkhorn backward then keeps 16 of 64 lanes busy).
+  if (nblk <= 64)
+    dynw_bwd_rows_kernel<4><<<dim3((unsigned)((B + 3) / 4)), kThreads, 0, st>>>(
+        aux, P, InRow{w, kOut}, InRow{nullptr, 0}, InRow{dH_post, 4}, InRow{nullptr, 0}, part, (int)nblk, rowbuf,
+        B, K, iters, eps);
+  else
+    dynw_bwd_rows_kernel<1><<<dim3((unsigned)B), kThreads, 0, st>>>(
+        aux, P, InRow{w, kOut}, InRow{nullptr, 0}, InRow{dH_post, 4}, InRow{nullptr, 0}, part, (int)nblk, rowbuf,
+        B, K, iters, eps);
   if ((rc = hip_status(hipGetLastError(), "layer weights backward rows launch"))) return rc;
   // The pooled rows: x, or without it (S = 1) H's own rows, read in H's dtype; grad_x stays f32.
   const void* xr = x ? (const void*)x : H;
@@ -592,8 +601,8 @@ extern "C" int mhc_layer_static_backward(const void* H, int dtype, const void* d
                                                    &nblk, st);
   });
   if (rc) return rc;
-  reduce_split_kernel<20, 4><<<dim3((unsigned)B, 5), kRedThreads, 0, st>>>(part, dpre, dres, (int)nblk);
-  if ((rc = hip_status(hipGetLastError(), "layer static reduce launch"))) return rc;
+  rc = hip_status(launch_reduce_split<20, 4>(part, dpre, dres, (int)nblk, B, st), "layer static reduce launch");
+  if (rc) return rc;
   static_weights_bwd_kernel<<<1, kThreads, 0, st>>>(H_pre_base, H_post_base, H_res_base, w, dpre, dH_post, dres,
                                                     grad_bias, B, iters);
   return hip_status(hipGetLastError(), "static weights backward launch");
@@ -633,8 +642,8 @@ extern "C" int mhc_layer_mix_backward(const void* H, int dtype, const void* d_br
                                                    &nblk, st);
   });
   if (rc) return rc;
-  reduce_split_kernel<20, 4><<<dim3((unsigned)B, 5), kRedThreads, 0, st>>>(part, dH_pre, dH_res, (int)nblk);
-  return hip_status(hipGetLastError(), "layer mix backward reduce launch");
+  return hip_status(launch_reduce_split<20, 4>(part, dH_pre, dH_res, (int)nblk, B, st),
+                    "layer mix backward reduce launch");
 }
 
 extern "C" int mhc_layer_mix_dh(const void* d_branch_input, const void* dH_new, int dtype, const float* w,

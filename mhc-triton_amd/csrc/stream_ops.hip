@@ -40,8 +40,8 @@ static int stream_mix_bwd(const T* dbi, const T* dhr, const T* H, const float* p
     return hip_status(hipGetLastError(), "stream_mix_backward launch");
   });
   if (rc) return rc;
-  reduce_split_kernel<20, 4><<<dim3((unsigned)B, 5), kRedThreads, 0, st>>>(part, dpre, dres, (int)nblk);
-  return hip_status(hipGetLastError(), "stream_mix_backward reduce launch");
+  return hip_status(launch_reduce_split<20, 4>(part, dpre, dres, (int)nblk, B, st),
+                    "stream_mix_backward reduce launch");
 }
 
 template <typename TH, typename TB, int W>
@@ -77,8 +77,8 @@ static int add_res_bwd(const TH* dhn, const TB* bo, WRow post, TB* dbo, float* d
     return hip_status(hipGetLastError(), "add_residual_backward launch");
   });
   if (rc) return rc;
-  reduce_split_kernel<4, 4><<<dim3((unsigned)B, 1), kRedThreads, 0, st>>>(part, dpost, nullptr, (int)nblk);
-  return hip_status(hipGetLastError(), "add_residual_backward reduce launch");
+  return hip_status(launch_reduce_split<4, 4>(part, dpost, nullptr, (int)nblk, B, st),
+                    "add_residual_backward reduce launch");
 }
 
 template <typename TH, typename TB>
