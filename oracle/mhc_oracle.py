@@ -27,6 +27,11 @@ def _a(x, dt):
     return np.asarray(x, dtype=dt)
 
 
+def _s(x, dt):
+    """A scalar parameter (a Python number or a one-element array) as dt."""
+    return dt(np.asarray(x).reshape(-1)[0])
+
+
 def sigmoid(z):
     return 1.0 / (1.0 + np.exp(-z))
 
@@ -242,9 +247,9 @@ def unfused_weights(x, W_pre, W_post, W_res, s_pre, s_post, s_res, H_pre_base, H
     B, K = x.shape
     rms = np.sqrt((x * x).mean(axis=-1, keepdims=True) + dt(eps))
     xn = x / rms
-    zp = _a(H_post_base, dt) + (xn @ _a(W_post, dt).T) * dt(s_post)
-    zq = _a(H_pre_base, dt) + (xn @ _a(W_pre, dt).T) * dt(s_pre)
-    zr = _a(H_res_base, dt) + (xn @ _a(W_res, dt).T).reshape(B, 4, 4) * dt(s_res)
+    zp = _a(H_post_base, dt) + (xn @ _a(W_post, dt).T) * _s(s_post, dt)
+    zq = _a(H_pre_base, dt) + (xn @ _a(W_pre, dt).T) * _s(s_pre, dt)
+    zr = _a(H_res_base, dt) + (xn @ _a(W_res, dt).T).reshape(B, 4, 4) * _s(s_res, dt)
     H_post = sigmoid(zp)
     sq = sigmoid(zq)
     H_pre = sq / (sq.sum(axis=-1, keepdims=True) + 1e-8)
@@ -261,9 +266,9 @@ def unfused_weights_backward(x, W_pre, W_post, W_res, s_pre, s_post, s_res, H_pr
     rms = np.sqrt((x * x).mean(axis=-1, keepdims=True) + dt(eps))
     xn = x / rms
     lp, lq, lr = xn @ Wp.T, xn @ Wq.T, xn @ Wr.T
-    zp = _a(H_post_base, dt) + lp * dt(s_post)
-    zq = _a(H_pre_base, dt) + lq * dt(s_pre)
-    zr = _a(H_res_base, dt) + (lr * dt(s_res)).reshape(B, 4, 4)
+    zp = _a(H_post_base, dt) + lp * _s(s_post, dt)
+    zq = _a(H_pre_base, dt) + lq * _s(s_pre, dt)
+    zr = _a(H_res_base, dt) + (lr * _s(s_res, dt)).reshape(B, 4, 4)
     sp = sigmoid(zp)
     g_zp = _a(gH_post, dt) * sp * (1 - sp)
     sq = sigmoid(zq)
@@ -279,11 +284,11 @@ def unfused_weights_backward(x, W_pre, W_post, W_res, s_pre, s_post, s_res, H_pr
         "scale_post": np.array([(g_zp * lp).sum()]),
         "scale_pre": np.array([(g_zq * lq).sum()]),
         "scale_res": np.array([(g_zr * lr).sum()]),
-        "W_post": (g_zp * dt(s_post)).T @ xn,
-        "W_pre": (g_zq * dt(s_pre)).T @ xn,
-        "W_res": (g_zr * dt(s_res)).T @ xn,
+        "W_post": (g_zp * _s(s_post, dt)).T @ xn,
+        "W_pre": (g_zq * _s(s_pre, dt)).T @ xn,
+        "W_res": (g_zr * _s(s_res, dt)).T @ xn,
     }
-    g_xn = (g_zp * dt(s_post)) @ Wp + (g_zq * dt(s_pre)) @ Wq + (g_zr * dt(s_res)) @ Wr
+    g_xn = (g_zp * _s(s_post, dt)) @ Wp + (g_zq * _s(s_pre, dt)) @ Wq + (g_zr * _s(s_res, dt)) @ Wr
     # xn = x / rms, rms = sqrt(mean(x^2) + eps)
     out["x"] = g_xn / rms - x * (g_xn * x).sum(axis=-1, keepdims=True) / (K * rms ** 3)
     return out
