@@ -22,7 +22,8 @@ Printed: one JSON line (metric, value = tokens/s of the whole job, roofline of
 the dominant kernel measured with HIP events on the stream it runs on, the CPU
 baseline of the reference's PyTorch path timed on this host).  The default
 config3 run also times configs 4 and 5 (GPU legs only) and reports them under
-"workloads"; --no-workloads skips them.
+"workloads", with config 2 (Sinkhorn) and the dynamic-weights op at R = tokens
+under "workloads.ops"; --no-workloads skips them.
 
 Workloads (reference benchmark shapes, src/mhc/module.py layer):
   config3  dim 4096 bf16, B=4 S=4096, dynamic fused weights (the headline)
@@ -93,8 +94,8 @@ def _parse():
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--workload", default="config3", choices=sorted(WORKLOADS))
     ap.add_argument("--no-workloads", action="store_true",
-                    help="skip the GPU legs of configs 4 and 5 that the default (config3) run adds under "
-                         "'workloads'")
+                    help="skip the GPU legs that the default (config3) run adds under 'workloads': configs "
+                         "4 and 5, and 'ops' (config-2 Sinkhorn, dynamic weights at R = K = 16384 bf16)")
     ap.add_argument("--cpu-reps", type=int, default=3,
                     help="timed runs of the cpu_baseline leg at the workload's shape, after one warm-up "
                          "(0 disables it)")
@@ -390,13 +391,18 @@ def _decode_leg(D: int = 4096, reps: int = 5, calls: int = 30) -> dict:
     return out
 
 
-def _ops_leg(n: int = 20, warm: int = 3) -> dict:
+OPS_GROUPS = ("sinkhorn", "stream", "dynw_rows", "dynw_bf16", "dynw_other")
+
+
+def _ops_leg(n: int = 20, warm: int = 3, groups=OPS_GROUPS) -> dict:
     """Each low-level op alone, timed with HIP events on torch's current stream
     (the stream the kernels run on): time per call (the median of three blocks of
     ``n`` calls, each block's mean, so that a stretch of lowered clocks on the box
     moves one block, not the figure) and the fraction of 8 TB/s its algorithmic
     bytes reach.  Inputs are resident before timing; gradient calls use
-    torch.autograd.grad, so nothing accumulates between calls."""
+    torch.autograd.grad, so nothing accumulates between calls.  ``groups`` picks
+    from OPS_GROUPS: config-2 Sinkhorn, the stream ops at config-3 size, dynamic
+    weights at R = 4, at R = K = 16384 bf16, and at R = K = 16384 fp16 / fp32."""
     import torch
 
     import mhc
@@ -431,14 +437,58 @@ def _ops_leg(n: int = 20, warm: int = 3) -> dict:
     def rec(name, us, nbytes):
         out[name] = {"us": round(us, 1), "hbm_frac": round(nbytes / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4)}
 
-    # config 2: Sinkhorn over 2^20 fp32 matrices (fwd reads M, writes P; bwd reads M, dP, writes dM)
-    M = torch.exp(torch.randn((1 << 20, 4, 4), generator=g, device=dev))
-    dP = torch.randn((1 << 20, 4, 4), generator=g, device=dev)
-    rec("sinkhorn_fwd config2", timed(lambda: K.sinkhorn_forward(M, 20, 1e-8)), 2 * M.numel() * 4)
-    rec("sinkhorn_bwd config2", timed(lambda: KB.sinkhorn_backward(M, dP, 20, 1e-8)), 3 * M.numel() * 4)
-    del M, dP
-    # the stream ops at config-3 size, bf16
+    if "sinkhorn" in groups:
+        # config 2: Sinkhorn over 2^20 fp32 matrices (fwd reads M, writes P; bwd reads M, dP, writes dM)
+        M = torch.exp(torch.randn((1 << 20, 4, 4), generator=g, device=dev))
+        dP = torch.randn((1 << 20, 4, 4), generator=g, device=dev)
+        rec("sinkhorn_fwd config2", timed(lambda: K.sinkhorn_forward(M, 20, 1e-8)), 2 * M.numel() * 4)
+        rec("sinkhorn_bwd config2", timed(lambda: KB.sinkhorn_backward(M, dP, 20, 1e-8)), 3 * M.numel() * 4)
+        del M, dP
     B, S, D = 4, 4096, 4096
+    e, T = 2, B * S
+    if "stream" in groups:
+        _stream_ops(g, B, S, D, timed, rec)
+    # fused dynamic weights: R = B rows (the module's use) and R = tokens rows (bf16, MFMA path)
+    phi = torch.randn((4 * D, 24), generator=g, device=dev) * 0.02
+    bias = torch.randn(24, generator=g, device=dev)
+    al = [torch.tensor([0.1], device=dev) for _ in range(3)]
+    if "dynw_rows" in groups:
+        x4 = torch.randn((4, 4 * D), generator=g, device=dev)
+        rec("dynamic_weights_fwd R=4 K=16384 f32",
+            timed(lambda: K.fused_dynamic_weights_forward(x4, phi, bias, *al)), 4 * 4 * D * 4)
+    phl = phi.clone().requires_grad_(True)
+    gs = [torch.randn((T, 4), generator=g, device=dev), torch.randn((T, 4), generator=g, device=dev),
+          torch.randn((T, 4, 4), generator=g, device=dev)]
+    # bf16 rows, then the same op on fp16 and fp32 rows (MFMA kernels: fp16 forward on the f16
+    # MFMA, the rest with x split into bf16 parts in registers); x read by the forward, x read
+    # and grad_x written by the backward
+    dts = ((torch.bfloat16, "bf16"),) if "dynw_bf16" in groups else ()
+    if "dynw_other" in groups:
+        dts += ((torch.float16, "f16"), (torch.float32, "f32"))
+    for dt, tag in dts:
+        xd = torch.randn((T, 4 * D), generator=g, device=dev).to(dt)
+        nb = T * 4 * D * xd.element_size()
+        rec(f"dynamic_weights_fwd R=16384 K=16384 {tag}",
+            timed(lambda: K.fused_dynamic_weights_forward(xd, phi, bias, *al)), nb)
+        xdl = xd.clone().requires_grad_(True)
+
+        def fwd_bwd_d():
+            o = mhc.fused_dynamic_weights(xdl, phl, bias, *al)
+            torch.autograd.grad(o, [xdl, phl], gs)
+
+        rec(f"dynamic_weights_fwd+bwd R=16384 K=16384 {tag}", timed(fwd_bwd_d), 3 * nb)
+        del xd, xdl
+    return out
+
+
+def _stream_ops(g, B, S, D, timed, rec) -> None:
+    """The stream ops at one layout (bf16), for _ops_leg."""
+    import torch
+
+    from mhc import _backward as KB
+    from mhc import _kernels as K
+
+    dev = "cuda"
     e, T = 2, B * S
     H = torch.randn((B, S, 4, D), generator=g, device=dev).bfloat16()
     pre = torch.softmax(torch.randn((B, 4), generator=g, device=dev), -1)
@@ -454,45 +504,6 @@ def _ops_leg(n: int = 20, warm: int = 3) -> dict:
     rec("mean_pool config3", timed(lambda: K.mean_pool(H)), 4 * D * e * T)
     rec("stream_expand config3", timed(lambda: K.stream_expand(bo)), 5 * D * e * T)
     rec("stream_collapse config3", timed(lambda: K.stream_collapse(H, 0.25)), 5 * D * e * T)
-    del hr, dhn, bi
-    # fused dynamic weights: R = B rows (the module's use) and R = tokens rows (bf16, MFMA path)
-    phi = torch.randn((4 * D, 24), generator=g, device=dev) * 0.02
-    bias = torch.randn(24, generator=g, device=dev)
-    al = [torch.tensor([0.1], device=dev) for _ in range(3)]
-    x4 = torch.randn((4, 4 * D), generator=g, device=dev)
-    rec("dynamic_weights_fwd R=4 K=16384 f32", timed(lambda: K.fused_dynamic_weights_forward(x4, phi, bias, *al)),
-        4 * 4 * D * 4)
-    xt = torch.randn((T, 4 * D), generator=g, device=dev).bfloat16()
-    rec("dynamic_weights_fwd R=16384 K=16384 bf16",
-        timed(lambda: K.fused_dynamic_weights_forward(xt, phi, bias, *al)), T * 4 * D * e)
-    xl = xt.clone().requires_grad_(True)
-    phl = phi.clone().requires_grad_(True)
-    gs = [torch.randn((T, 4), generator=g, device=dev), torch.randn((T, 4), generator=g, device=dev),
-          torch.randn((T, 4, 4), generator=g, device=dev)]
-
-    def fwd_bwd():
-        o = mhc.fused_dynamic_weights(xl, phl, bias, *al)
-        torch.autograd.grad(o, [xl, phl], gs)
-
-    # x read by the forward, x read and grad_x written by the backward
-    rec("dynamic_weights_fwd+bwd R=16384 K=16384 bf16", timed(fwd_bwd), 3 * T * 4 * D * e)
-    del xt, xl
-    # the same op on fp16 and fp32 rows (MFMA kernels: fp16 forward on the f16 MFMA, the rest
-    # with x split into bf16 parts in registers)
-    for dt, tag in ((torch.float16, "f16"), (torch.float32, "f32")):
-        xd = torch.randn((T, 4 * D), generator=g, device=dev).to(dt)
-        nb = T * 4 * D * xd.element_size()
-        rec(f"dynamic_weights_fwd R=16384 K=16384 {tag}",
-            timed(lambda: K.fused_dynamic_weights_forward(xd, phi, bias, *al)), nb)
-        xdl = xd.clone().requires_grad_(True)
-
-        def fwd_bwd_d():
-            o = mhc.fused_dynamic_weights(xdl, phl, bias, *al)
-            torch.autograd.grad(o, [xdl, phl], gs)
-
-        rec(f"dynamic_weights_fwd+bwd R=16384 K=16384 {tag}", timed(fwd_bwd_d), 3 * nb)
-        del xd, xdl
-    return out
 
 
 # The reference's published table (README.md:183-202): NVIDIA H100 80GB HBM3, batch=16, seq=2048,
@@ -893,6 +904,12 @@ def main() -> int:
             workloads[name] = _workload_summary(name, WORKLOADS[name], wr)
             _log(f"bench: {name} {wr['ms']:.4f} ms/step, layer {workloads[name]['layer_roofline']['frac']:.4f} of "
                  f"8 TB/s, H_new kernel {wr['add_ms'] * 1e3:.1f} us")
+        # config 2 (Sinkhorn over 2^20 matrices) and the dynamic-weights op at R = tokens (the
+        # MFMA kernels), as `--ops` times them: well under a second of GPU time
+        ops = _ops_leg(groups=("sinkhorn", "dynw_bf16"))
+        workloads["ops"] = {"unit": "us per call (median of three blocks of 20), hbm_frac of 8 TB/s", **ops}
+        for k, v in ops.items():
+            _log(f"bench: {k} {v['us']} us, {v['hbm_frac']:.4f} of 8 TB/s")
 
     cpu = None
     if args.cpu_reps > 0:
