@@ -154,7 +154,7 @@ def _stream_ceiling(tokens: int, row_bytes: int, caps=(0, 2, 3, 4, 6, 8), reps: 
 
     import torch
 
-    path = os.path.join(ROOT, "mhc-triton_amd", "mhc", "libmhc_probe.so")
+    path = os.path.join(ROOT, "mhc-triton_amd", "probe", "libmhc_probe.so")
     if not os.path.exists(path):
         raise RuntimeError(f"{path} is not built (make -C mhc-triton_amd)")
     lib = ctypes.CDLL(path)
@@ -226,7 +226,7 @@ def _dynw_ceiling(R: int = 16384, K: int = 16384, reps: int = 10, warm: int = 2,
     from mhc import _backward as KB
     from mhc import _kernels as KF
 
-    path = os.path.join(ROOT, "mhc-triton_amd", "mhc", "libmhc_probe.so")
+    path = os.path.join(ROOT, "mhc-triton_amd", "probe", "libmhc_probe.so")
     if not os.path.exists(path):
         raise RuntimeError(f"{path} is not built (make -C mhc-triton_amd)")
     lib = ctypes.CDLL(path)

@@ -134,7 +134,7 @@ def test_stream_ceiling_probe_rejects_bad_shapes_without_gpu(lib):
     its probe, and refuses unsupported mixes and shapes before any device work."""
     import ctypes
 
-    path = os.path.join(ROOT, "mhc-triton_amd", "mhc", "libmhc_probe.so")
+    path = os.path.join(ROOT, "mhc-triton_amd", "probe", "libmhc_probe.so")
     if not os.path.exists(path):
         import __graft_entry__
 

@@ -15,7 +15,7 @@ import torch
 pytestmark = pytest.mark.gpu
 
 ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
-PROBE = os.path.join(ROOT, "mhc-triton_amd", "mhc", "libmhc_probe.so")
+PROBE = os.path.join(ROOT, "mhc-triton_amd", "probe", "libmhc_probe.so")
 MIXES = [(1, 0, 0, 0), (0, 0, 0, 1), (1, 0, 0, 1), (4, 0, 0, 0), (4, 0, 0, 1), (4, 1, 0, 4), (4, 1, 0, 1),
          (4, 4, 1, 0), (4, 0, 0, 5), (1, 0, 0, 4), (4, 4, 1, 4)]
 
