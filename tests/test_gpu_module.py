@@ -431,3 +431,19 @@ def test_in_place_check_covers_views_of_one_buffer():
         buf[1].zero_()
     _, oHn, _ = O.layer_forward(params_np(hc), to_np(H), to_np(bo))
     assert rel_err(to_np(add(bo)), oHn) < 1e-5
+
+
+@pytest.mark.parametrize("dynamic,dtype", [(True, torch.bfloat16), (False, torch.float16), (True, torch.float32)])
+def test_autocast_leaves_the_fused_layers_unchanged(dynamic, dtype):
+    """Mixed-precision training runs the layer under torch.autocast.  The fused dynamic and static
+    layers call no autocast-eligible torch op: every weight stays fp32 and the kernels see the same
+    inputs, so the outputs and every gradient are the same bits as without autocast (as in the
+    reference, whose fused path is Triton launches on the same tensors)."""
+    hc, H, bo, dHn, dbi = make_case(3, 40, 96, dtype, dynamic=dynamic, phi_std=0.02, res_std=0.5)
+    bi0, Hn0, g0 = run_gpu(hc, H, bo, dHn, dbi)
+    with torch.autocast("cuda", dtype=torch.bfloat16):
+        bi1, Hn1, g1 = run_gpu(hc, H, bo, dHn, dbi)
+    assert bi1.dtype == dtype and Hn1.dtype == dtype
+    assert torch.equal(bi0, bi1) and torch.equal(Hn0, Hn1)
+    for n in g0:
+        assert torch.equal(g0[n], g1[n]), n
