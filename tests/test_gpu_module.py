@@ -447,3 +447,38 @@ def test_autocast_leaves_the_fused_layers_unchanged(dynamic, dtype):
     assert torch.equal(bi0, bi1) and torch.equal(Hn0, Hn1)
     for n in g0:
         assert torch.equal(g0[n], g1[n]), n
+
+
+@pytest.mark.parametrize("dynamic,fused", [(True, True), (False, True), (True, False)])
+@pytest.mark.parametrize("use_reentrant", [False, True])
+def test_activation_checkpointing(dynamic, fused, use_reentrant):
+    """A transformer block under torch.utils.checkpoint: the layer's forward runs again inside the
+    backward.  The kernels are deterministic, so every gradient is the same bits as the same block
+    without checkpointing."""
+    from torch.utils.checkpoint import checkpoint
+
+    hc, H, _, dHn, _ = make_case(2, 24, 64, torch.bfloat16, dynamic=dynamic, fused=fused, phi_std=0.02,
+                                 res_std=0.5)
+    torch.manual_seed(3)
+    branch = torch.nn.Linear(64, 64, device=DEV).to(torch.bfloat16)
+
+    def block(h):
+        bi, add = hc(h)
+        return add(branch(bi))
+
+    def grads(ckpt):
+        hc.zero_grad(set_to_none=True)
+        branch.zero_grad(set_to_none=True)
+        Hl = H.clone().requires_grad_(True)
+        out = checkpoint(block, Hl, use_reentrant=use_reentrant) if ckpt else block(Hl)
+        out.backward(dHn)
+        g = {n: p.grad.clone() for n, p in list(hc.named_parameters()) + list(branch.named_parameters())}
+        g["H"] = Hl.grad
+        return out.detach(), g
+
+    out0, g0 = grads(False)
+    out1, g1 = grads(True)
+    assert torch.equal(out0, out1)
+    assert set(g0) == set(g1)
+    for n in g0:
+        assert torch.equal(g0[n], g1[n]), n
