@@ -482,3 +482,26 @@ def test_activation_checkpointing(dynamic, fused, use_reentrant):
     assert set(g0) == set(g1)
     for n in g0:
         assert torch.equal(g0[n], g1[n]), n
+
+
+@pytest.mark.parametrize("dynamic", [True, False])
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+def test_module_cast_to_half_precision(dynamic, dtype):
+    """The reference's benchmark casts the whole module with .half() (benchmarks/benchmark.py:147,150).
+    The kernels read the half-precision parameters as fp32 values, so the layer is the oracle's
+    at those parameter values; every parameter gradient comes back in the parameter's dtype,
+    rounded once from fp32 (to within one unit in the last place of its largest entry)."""
+    hc, H, bo, dHn, dbi = make_case(2, 48, 96, dtype, dynamic=dynamic, phi_std=0.02, res_std=0.5)
+    hc = hc.to(dtype)
+    bi, Hn, grads = run_gpu(hc, H, bo, dHn, dbi)
+    p = params_np(hc)
+    obi, oHn, cache = O.layer_forward(p, to_np(H), to_np(bo), dynamic, True, hc.sinkhorn_iters, hc.eps)
+    og = {k.replace(".weight", ""): v for k, v in O.layer_backward(p, cache, to_np(dHn), to_np(dbi)).items()}
+    assert rel_err(to_np(bi), obi) < 2e-2 and rel_err(to_np(Hn), oHn) < 2e-2
+    assert rel_err(to_np(grads["H"]), og["H"]) < 2e-2 and rel_err(to_np(grads["bo"]), og["bo"]) < 2e-2
+    ulp = 2.0 ** -10 if dtype == torch.float16 else 2.0 ** -7
+    for n, param in hc.named_parameters():
+        k = n.replace(".weight", "")
+        assert grads[k].dtype == param.dtype == dtype, n
+        err = rel_err(to_np(grads[k]).reshape(np.shape(og[k])), og[k])
+        assert err < ulp, (n, err)
