@@ -145,6 +145,48 @@ def _step_of(hc):
     return step
 
 
+@pytest.mark.parametrize("dynamic,fused", [(True, True), (False, True), (True, False)])
+def test_compiled_reduce_overhead_matches_eager(dynamic, fused):
+    """torch.compile(mode="reduce-overhead"): inductor replays the step, forward and backward, as
+    CUDA graphs from its own memory pool, workspaces included.  Four steps with new input values:
+    each one the same bits as the eager step (bo an independent leaf, so that no torch op of the
+    caller's, which inductor would compile differently, sits between the two halves of the layer;
+    the unfused weights are such torch ops: within 1e-5 in fp32, two bf16 units in the last place
+    in the bf16 outputs and dH)."""
+    hc, H, _, gHn, gbi = _layer_case(dynamic, fused, torch.bfloat16)
+    g = torch.Generator().manual_seed(7)
+    bo = torch.randn(gbi.shape, generator=g).to(torch.bfloat16).to(DEV)
+
+    def step(Hl, bol):
+        bi, add = hc(Hl)
+        return bi, add(bol)
+
+    def run(f, Hs):
+        hc.zero_grad(set_to_none=True)
+        Hl, bol = Hs.clone().requires_grad_(True), bo.clone().requires_grad_(True)
+        bi, Hn = f(Hl, bol)
+        torch.autograd.backward([bi, Hn], [gbi, gHn])
+        out = {"bi": bi.detach().clone(), "H_new": Hn.detach().clone(), "H": Hl.grad, "bo": bol.grad}
+        out.update({n: p.grad.clone() for n, p in hc.named_parameters()})
+        return out
+
+    torch._dynamo.reset()
+    step_c = torch.compile(step, mode="reduce-overhead", fullgraph=True)
+    for it in range(4):
+        Hs = (H.float() * (1 + 0.25 * it)).to(H.dtype)
+        want = run(step, Hs)
+        torch.compiler.cudagraph_mark_step_begin()
+        got = run(step_c, Hs)
+        if dynamic and not fused:
+            # fp32 results to 1e-5; the bf16 ones (bi, H_new, dH, d_bo) to two units in the last
+            # place, where the weights' last fp32 bits move a rounding
+            for k in want:
+                tol = 1e-5 if want[k].dtype == torch.float32 else 2.0 ** -6
+                assert rel_err(to_np(got[k]), to_np(want[k])) < tol, (it, k)
+        else:
+            _assert_identical(want, got)
+
+
 def test_compiled_layer_with_dynamic_shapes():
     """One compiled graph serves three sequence lengths (symbolic shapes through the fake kernels)."""
     from torch._dynamo.utils import counters
