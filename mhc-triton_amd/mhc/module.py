@@ -164,7 +164,9 @@ class HyperConnection(nn.Module):
         torch.compile the closure reads a snapshot of ``H`` instead (the reference's
         semantics; inductor drops the copy when the closure runs in the same graph).  A strided
         ``H`` is made contiguous once, here, and that copy serves the forward, the closure and
-        the backward.
+        the backward.  An inference tensor (made under ``torch.inference_mode``) has no version
+        counter, so for it the check does not run: modify such an ``H`` in place only after the
+        closure has been called.
 
         A subclass that overrides ``_compute_weights`` gets the reference's composition on the
         HIP ops: its weights, ``fused_stream_mix`` and a closure over ``H_residual`` that calls
@@ -176,7 +178,8 @@ class HyperConnection(nn.Module):
         H = H.contiguous()
         if torch.compiler.is_compiling():
             return self._forward_traced(H)
-        version = H._version
+        # inference tensors (made under torch.inference_mode) keep no version counter
+        version = None if H.is_inference() else H._version
         if not self.dynamic:
             bi, w, link, post_link = _layer._StaticLayer.apply(H, self.H_pre_base, self.H_post_base,
                                                                self.H_res_base, self.sinkhorn_iters)
@@ -195,7 +198,7 @@ class HyperConnection(nn.Module):
                                                                 w_link)
 
         def add_residual(branch_output: torch.Tensor) -> torch.Tensor:
-            if H._version != version:
+            if version is not None and H._version != version:
                 raise RuntimeError(
                     "HyperConnection: H was modified in place after forward(H); add_residual recomputes "
                     "H_res @ H from H and would mix the modified values. Clone H before modifying it "

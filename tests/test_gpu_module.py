@@ -505,3 +505,49 @@ def test_module_cast_to_half_precision(dynamic, dtype):
         assert grads[k].dtype == param.dtype == dtype, n
         err = rel_err(to_np(grads[k]).reshape(np.shape(og[k])), og[k])
         assert err < ulp, (n, err)
+
+
+@pytest.mark.parametrize("dynamic,fused", [(True, True), (False, True), (True, False)])
+def test_inference_mode(dynamic, fused):
+    """Serving stacks run under torch.inference_mode, where new tensors are inference tensors with
+    no version counter.  The layer runs there (the closure's in-place check is skipped for such an
+    H) and gives the same bits as under torch.no_grad; so do the four public ops."""
+    import mhc
+
+    hc, H, bo, _, _ = make_case(3, 20, 64, torch.bfloat16, dynamic=dynamic, fused=fused, phi_std=0.02,
+                                res_std=0.5)
+    with torch.no_grad():
+        bi0, add0 = hc(H)
+        Hn0 = add0(bo)
+    with torch.inference_mode():
+        Hi, boi = H.clone(), bo.clone()
+        assert Hi.is_inference()
+        bi1, add1 = hc(Hi)
+        Hn1 = add1(boi)
+        # a normal tensor made before inference mode keeps its check
+        bi2, add2 = hc(H)
+        Hn2 = add2(bo)
+    assert torch.equal(bi0, bi1) and torch.equal(Hn0, Hn1)
+    assert torch.equal(bi0, bi2) and torch.equal(Hn0, Hn2)
+    Hc = H.clone()
+    with torch.inference_mode():
+        _, add3 = hc(Hc)
+        Hc.add_(1.0)
+        with pytest.raises(RuntimeError, match="modified in place"):
+            add3(bo)
+    if dynamic and fused:
+        x = H.float().mean(1).reshape(3, -1)
+        bias = torch.cat([hc.H_pre_base, hc.H_post_base, hc.H_res_base.flatten()]).detach()
+        alphas = (hc.alpha_pre, hc.alpha_post, hc.alpha_res)
+
+        def ops(x, H, bo):
+            pre, post, res = mhc.fused_dynamic_weights(x, hc.phi, bias, *alphas, 20, 1e-6)
+            bi, h_res = mhc.fused_stream_mix(H, pre, res)
+            return pre, post, res, bi, h_res, mhc.fused_add_residual(h_res, bo, post), mhc.sinkhorn_knopp(res, 20)
+
+        with torch.no_grad():
+            want = ops(x, H, bo)
+        with torch.inference_mode():
+            got = ops(x.clone(), H.clone(), bo.clone())
+        for a, b in zip(want, got):
+            assert torch.equal(a, b)
