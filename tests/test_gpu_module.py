@@ -551,3 +551,27 @@ def test_inference_mode(dynamic, fused):
             got = ops(x.clone(), H.clone(), bo.clone())
         for a, b in zip(want, got):
             assert torch.equal(a, b)
+
+
+@pytest.mark.parametrize("dynamic,fused", [(True, True), (False, True), (True, False)])
+def test_frozen_parameters(dynamic, fused):
+    """Fine-tuning with the layer's parameters frozen (all of them, or only the first): dH and
+    d branch_output, and the gradients of the parameters left trainable, are the same bits as with
+    every parameter trainable; frozen parameters get no gradient."""
+    hc, H, bo, dHn, dbi = make_case(2, 24, 64, torch.bfloat16, dynamic=dynamic, fused=fused, phi_std=0.02,
+                                    res_std=0.5)
+    _, _, g_all = run_gpu(hc, H, bo, dHn, dbi)
+    names = [n for n, _ in hc.named_parameters()]
+    for frozen in (names, names[:1]):
+        for n, p in hc.named_parameters():
+            p.requires_grad_(n not in frozen)
+        _, _, g = run_gpu(hc, H, bo, dHn, dbi)
+        assert torch.equal(g["H"], g_all["H"]) and torch.equal(g["bo"], g_all["bo"])
+        for n in names:
+            k = n.replace(".weight", "")
+            if n in frozen:
+                assert g[k] is None, n
+            else:
+                assert torch.equal(g[k], g_all[k]), n
+    for p in hc.parameters():
+        p.requires_grad_(True)
