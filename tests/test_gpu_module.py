@@ -45,9 +45,9 @@ def params_np(hc):
     return {n.replace(".weight", ""): to_np(p) for n, p in hc.named_parameters()}
 
 
-def run_gpu(hc, H, bo, dHn, dbi):
-    Hl = H.clone().requires_grad_(True)
-    bol = bo.clone().requires_grad_(True)
+def run_gpu(hc, H, bo, dHn, dbi, copy=torch.clone):
+    Hl = copy(H).requires_grad_(True)
+    bol = copy(bo).requires_grad_(True)
     hc.zero_grad(set_to_none=True)
     bi, add = hc(Hl)
     Hn = add(bol)
@@ -58,8 +58,8 @@ def run_gpu(hc, H, bo, dHn, dbi):
     return bi, Hn, grads
 
 
-def check_layer(hc, H, bo, dHn, dbi, fwd_tol, h_tol, p_tol):
-    bi, Hn, grads = run_gpu(hc, H, bo, dHn, dbi)
+def check_layer(hc, H, bo, dHn, dbi, fwd_tol, h_tol, p_tol, copy=torch.clone):
+    bi, Hn, grads = run_gpu(hc, H, bo, dHn, dbi, copy)
     p = params_np(hc)
     obi, oHn, cache = O.layer_forward(p, to_np(H), to_np(bo), hc.dynamic, hc.use_fused_weights or not hc.dynamic,
                                       hc.sinkhorn_iters, hc.eps)
@@ -575,3 +575,26 @@ def test_frozen_parameters(dynamic, fused):
                 assert torch.equal(g[k], g_all[k]), n
     for p in hc.parameters():
         p.requires_grad_(True)
+
+
+def _offset_by_one(t):
+    """A contiguous copy of t that starts one element past a 16-byte boundary."""
+    buf = torch.empty(t.numel() + 8, dtype=t.dtype, device=t.device)
+    out = buf[1:1 + t.numel()].view(t.shape)
+    out.copy_(t)
+    return out
+
+
+@pytest.mark.parametrize("B,S,D,dynamic,fused", [(2, 24, 64, True, True), (2, 24, 64, False, True),
+                                                 (2, 24, 64, True, False), (64, 1, 64, True, True),
+                                                 (64, 2, 8192, True, True)])
+def test_contiguous_inputs_off_a_16_byte_boundary(B, S, D, dynamic, fused):
+    """H and branch_output contiguous but one element off a 16-byte boundary (slices of a packed
+    buffer): every kernel that loads 16 bytes at a time checks the pointers it is given and the
+    layer takes the element-wise forms, on the small-batch and the bulk-batch paths.  Against the
+    oracle."""
+    hc, H, bo, dHn, dbi = make_case(B, S, D, torch.bfloat16, dynamic=dynamic, fused=fused, phi_std=0.02,
+                                    res_std=0.5)
+    dHnm, dbim = _offset_by_one(dHn), _offset_by_one(dbi)
+    assert _offset_by_one(H).data_ptr() % 16 != 0 and _offset_by_one(H).is_contiguous()
+    check_layer(hc, H, bo, dHnm, dbim, 2e-2, 2e-2, 1e-4, copy=_offset_by_one)
