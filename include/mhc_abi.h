@@ -288,7 +288,8 @@ int mhc_layer_add_backward(const void* dH_new, int dtype_h, const void* branch_o
  * writes dH [B,S,4,D] (NULL to skip) and the f32 parameter gradients
  * grad_phi [4D,24], grad_bias [24] (pre, post, res), grad_alpha [3].  x is the
  * forward's pooled rows; at S = 1 it may be NULL (the forward then need not
- * write it): the pooled rows are H's own rows, read from H. */
+ * write it): the pooled rows are H's own rows, read from H.  With B = 0 the
+ * parameter gradients are zero (empty sums). */
 int mhc_layer_dynamic_backward(const void* H, int dtype, const void* d_branch_input,
                                const void* dH_new, const float* dH_post,
                                const float* phi, const float* H_pre_base,
@@ -301,7 +302,7 @@ int mhc_layer_dynamic_backward(const void* H, int dtype, const void* d_branch_in
                                mhc_stream_t stream);
 
 /* Static layer backward: dH (NULL to skip) and grad_bias [24] f32 for
- * (H_pre_base, H_post_base, H_res_base). */
+ * (H_pre_base, H_post_base, H_res_base); zero with B = 0. */
 int mhc_layer_static_backward(const void* H, int dtype, const void* d_branch_input,
                               const void* dH_new, const float* dH_post,
                               const float* H_pre_base, const float* H_post_base,

@@ -518,7 +518,15 @@ extern "C" int mhc_layer_dynamic_backward(const void* H, int dtype, const void* 
                                           void* workspace, size_t workspace_bytes, mhc_stream_t stream) {
   if (int rc = check_bsd("layer_dynamic_backward", B, S, D)) return rc;
   if (iters < 0) { set_error("layer_dynamic_backward: negative iters"); return MHC_ERR_ARG; }
-  if (B == 0) return MHC_OK;
+  if (B == 0) {
+    // No rows: every parameter gradient is an empty sum.
+    hipStream_t st = (hipStream_t)stream;
+    if (grad_phi)
+      if (int rc = fill_zero(grad_phi, 4 * D * kOut, st)) return rc;
+    if (grad_bias)
+      if (int rc = fill_zero(grad_bias, kOut, st)) return rc;
+    return grad_alpha ? fill_zero(grad_alpha, 3, st) : MHC_OK;
+  }
   const bool nz = S * D != 0;  // bulk tensors may be empty (null) when S * D == 0
   if ((nz && (!H || !d_branch_input)) || !phi || !H_pre_base || !H_post_base || !H_res_base || !alpha_pre ||
       !alpha_post || !alpha_res || (!x && S != 1) || !w || !aux) {
@@ -580,7 +588,7 @@ extern "C" int mhc_layer_static_backward(const void* H, int dtype, const void* d
                                          size_t workspace_bytes, mhc_stream_t stream) {
   if (int rc = check_bsd("layer_static_backward", B, S, D)) return rc;
   if (iters < 0) { set_error("layer_static_backward: negative iters"); return MHC_ERR_ARG; }
-  if (B == 0) return MHC_OK;
+  if (B == 0) return grad_bias ? fill_zero(grad_bias, kOut, (hipStream_t)stream) : MHC_OK;  // empty sums
   const bool nz = S * D != 0;  // bulk tensors may be empty (null) when S * D == 0
   if ((nz && (!H || !d_branch_input)) || !H_pre_base || !H_post_base || !H_res_base || !w || !grad_bias) {
     set_error("layer_static_backward: null pointer");

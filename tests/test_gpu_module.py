@@ -258,6 +258,28 @@ def test_empty_sequence(dynamic):
         assert float(hc.H_post_base.grad.abs().sum()) == 0.0
 
 
+@pytest.mark.parametrize("dynamic,fused", [(True, True), (False, True), (True, False)])
+def test_empty_batch(dynamic, fused):
+    """B = 0: empty outputs, and every parameter gradient an empty sum, exactly zero (as torch's
+    sums over no rows are), not what the gradient buffers held before."""
+    import mhc
+
+    hc = mhc.HyperConnection(64, dynamic=dynamic, use_fused_weights=fused).to(DEV)
+    H = torch.zeros((0, 5, 4, 64), device=DEV, dtype=torch.bfloat16, requires_grad=True)
+    bo = torch.zeros((0, 5, 64), device=DEV, dtype=torch.bfloat16, requires_grad=True)
+    # a dirty allocator pool: gradient buffers allocated next would hold these values
+    junk = torch.full((1 << 20,), float("nan"), device=DEV)
+    del junk
+    bi, add = hc(H)
+    Hn = add(bo)
+    assert bi.shape == (0, 5, 64) and Hn.shape == (0, 5, 4, 64)
+    (Hn.float().sum() + bi.float().sum()).backward()
+    torch.cuda.synchronize()
+    assert H.grad.shape == H.shape and bo.grad.shape == bo.shape
+    for n, p in hc.named_parameters():
+        assert p.grad is not None and float(p.grad.abs().sum()) == 0.0, n
+
+
 # --------------------------------------------------------------------------- closure edge cases
 
 def _oracle_grads(hc, H, bo, dHn, dbi):
